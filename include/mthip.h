@@ -1,0 +1,250 @@
+/*
+ * libmthip -- MI355X (gfx950) device backend for mtorch's SD-UNet dense-inference hot path.
+ *
+ * Plain C ABI: raw device pointers, int64 sizes/strides, dtype codes, scalars.  No C++ or
+ * framework types cross it, so mtorch's C++ core (a dispatch hook at the top of each public
+ * op), its CPython binding, ctypes or any other FFI can bind it directly.
+ *
+ * Every function returns 0 (MTHIP_OK) on success or a non-zero status; the message of the
+ * last failure on the calling thread is returned by mthip_last_error().  Kernels are
+ * enqueued asynchronously on one in-order HIP stream per device (mthip_stream); device-to-host
+ * copies and mthip_synchronize wait for it.
+ *
+ * Citations are file:line into kazhiramatsu/mtorch; each names the reference interface the
+ * entry point serves when a tensor lives on the GPU device.
+ */
+#ifndef MTHIP_H
+#define MTHIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* dtype codes: the order of mtorch::ScalarType (tensor.h:13-20). */
+enum {
+  MTHIP_F16 = 0,
+  MTHIP_F32 = 1,
+  MTHIP_F64 = 2,
+  MTHIP_I32 = 3,
+  MTHIP_I64 = 4,
+  MTHIP_BOOL = 5
+};
+
+/* status codes */
+enum {
+  MTHIP_OK = 0,
+  MTHIP_ERR_INVALID = 1,     /* bad argument, shape or dtype (caller bug) */
+  MTHIP_ERR_HIP = 2,         /* a HIP runtime call failed */
+  MTHIP_ERR_OOM = 3,         /* device allocation failed */
+  MTHIP_ERR_UNSUPPORTED = 4  /* valid request this backend does not implement */
+};
+
+/* ===================================================================== runtime */
+
+/* Thread-local message of the last failure ("" if none). */
+const char* mthip_last_error(void);
+/* Library build identifier (offload arch and version). */
+const char* mthip_version(void);
+
+/* Number of visible GPUs.  Backs mtorch.cuda.is_available/device_count, which the reference
+ * stubs to False/0 (mtorch/__init__.py:2320-2321). */
+int mthip_device_count(int* count);
+/* Name and compute-unit count of a device (for reports). */
+int mthip_device_info(int device, char* name, size_t name_len, int* cu_count, size_t* total_mem);
+
+/* ---- memory: the device Allocator seam planned at docs/design/08-phase5-device-layer.md:660-695
+ * (allocate / deallocate / copy_from_host / copy_to_host / copy_on_device).  Storage for a GPU
+ * tensor (tensor.h:60-85 gains a device buffer) is obtained here.  Blocks are cached per device
+ * and reused by size; MTHIP_DISABLE_CACHING=1 in the environment frees eagerly. */
+int mthip_malloc(int device, size_t nbytes, void** ptr);
+int mthip_free(int device, void* ptr);
+int mthip_empty_cache(int device);
+int mthip_memory_stats(int device, size_t* allocated_bytes, size_t* reserved_bytes);
+
+/* Host<->device copies behind mtorch::to(input, dtype, device) (tensor.cpp:8479-8508) and
+ * Tensor.cpu() (module.cpp:9257).  h2d returns once the host buffer may be reused; d2h
+ * returns once the data is on the host. */
+int mthip_memcpy_h2d(int device, void* dst, const void* src, size_t nbytes);
+int mthip_memcpy_d2h(int device, void* dst, const void* src, size_t nbytes);
+int mthip_memcpy_d2d(int device, void* dst, const void* src, size_t nbytes);
+int mthip_synchronize(int device);
+/* The device's stream as an opaque hipStream_t. */
+void* mthip_stream(int device);
+
+/* ---- stream capture into a replayable HIP graph (launch-bound inner loops).  While a
+ * capture is open, freed blocks stay reserved for the graph until mthip_graph_destroy. */
+int mthip_graph_begin(int device);
+int mthip_graph_end(int device, void** graph);
+int mthip_graph_launch(int device, void* graph);
+int mthip_graph_destroy(int device, void* graph);
+
+/* ---- events on the device stream, for timing. */
+int mthip_event_create(void** event);
+int mthip_event_record(int device, void* event);
+int mthip_event_elapsed_ms(void* start, void* end, float* ms);
+int mthip_event_destroy(void* event);
+
+/* ===================================================================== data movement */
+
+/* dtype conversion of n contiguous elements (F16/F32/F64/I32/I64/BOOL).  fp32->fp16 follows
+ * float_to_half_bits (tensor.cpp:276-315, half-away-from-zero); fp64->fp16 narrows to fp32
+ * first as storage_set_unchecked does (tensor.cpp:593-597).  Serves mtorch::to with a dtype
+ * change (tensor.cpp:8479-8508, try_dense_cast :2764-2796, cast_dense_numeric_to_half :2642). */
+int mthip_cast(int device, int src_dtype, const void* src, int dst_dtype, void* dst, int64_t n);
+
+/* dst (contiguous, dtype) <- src viewed through sizes/strides (element units), rank <= 8.
+ * Serves Tensor::contiguous() (tensor.cpp:8210-8226) for permuted/transposed/sliced views. */
+int mthip_copy_strided(int device, int dtype, const void* src, int rank, const int64_t* sizes,
+                       const int64_t* src_strides, void* dst);
+
+/* dst[i] = value for n contiguous elements.  Serves full/zeros/ones/fill_ (tensor.h:143-149). */
+int mthip_fill(int device, int dtype, void* dst, int64_t n, double value);
+
+/* Concatenation of `count` contiguous inputs along `dim` of an output of rank `rank` and
+ * shape out_sizes (each input shares every other extent).  Serves mtorch::cat (tensor.cpp:32141). */
+int mthip_cat(int device, int dtype, int count, const void* const* inputs, const int64_t* dim_sizes,
+              int rank, const int64_t* out_sizes, int dim, void* out);
+
+/* Nearest-neighbour 2-D upsampling of x[B*C, H, W] by integer factors.  Serves
+ * interpolate(mode="nearest") (tensor.cpp:10897) on the UNet decoder path. */
+int mthip_upsample_nearest2d(int device, int dtype, const void* x, void* y, int64_t planes,
+                             int64_t H, int64_t W, int64_t scale_h, int64_t scale_w);
+
+/* ===================================================================== elementwise */
+
+enum { MTHIP_BIN_ADD = 0, MTHIP_BIN_MUL = 1, MTHIP_BIN_SUB = 2, MTHIP_BIN_DIV = 3 };
+
+/* out = a (op) b with broadcasting expressed through strides (0 on broadcast axes), rank <= 8,
+ * out contiguous with shape out_sizes.  a, b and out share `dtype` (F16 or F32); the op is
+ * evaluated in fp32 and narrowed once (fp16: float_to_half_bits).  Serves
+ * binary_tensor_tensor (tensor.cpp:18965-19104) for add/sub/mul/div. */
+int mthip_binary(int device, int op, int dtype, const void* a, const int64_t* a_strides,
+                 const void* b, const int64_t* b_strides, void* out, int rank,
+                 const int64_t* out_sizes);
+
+/* out = x (op) scalar for n contiguous elements; scalar_first swaps the operands.
+ * Serves binary_tensor_scalar (tensor.cpp:19106-19176). */
+int mthip_binary_scalar(int device, int op, int dtype, const void* x, double scalar, int scalar_first,
+                        void* out, int64_t n);
+
+enum {
+  MTHIP_UNARY_SILU = 0,      /* silu       tensor.cpp:16480-16613 */
+  MTHIP_UNARY_GELU = 1,      /* gelu none  tensor.cpp:17207-17288 */
+  MTHIP_UNARY_GELU_TANH = 2, /* gelu tanh  tensor.cpp:17275-17279 */
+  MTHIP_UNARY_EXP = 3,
+  MTHIP_UNARY_SIN = 4,
+  MTHIP_UNARY_COS = 5,
+  MTHIP_UNARY_NEG = 6,
+  MTHIP_UNARY_SIGMOID = 7,
+  MTHIP_UNARY_RELU = 8
+};
+/* y = f(x) for n contiguous elements (F16/F32). */
+int mthip_unary(int device, int op, int dtype, const void* x, void* y, int64_t n);
+
+/* GEGLU gating on a [rows, 2*D] tensor: y[r, d] = x[r, d] * gelu(x[r, D + d]) -- the
+ * `chunk(2, -1)` + gelu + mul of the SD feed-forward, evaluated with the same per-op roundings
+ * (gelu result narrowed, then the product narrowed). */
+int mthip_geglu(int device, int dtype, const void* x, void* y, int64_t rows, int64_t D);
+
+/* ===================================================================== contractions */
+
+enum {
+  MTHIP_ACT_NONE = 0,
+  MTHIP_ACT_GELU = 1,
+  MTHIP_ACT_GELU_TANH = 2,
+  MTHIP_ACT_SILU = 3
+};
+
+/* y[M,N] = act(x[M,K] . w[N,K]^T + b[N]) (+ residual[M,N]) -- mtorch::linear
+ * (tensor.cpp:31401-31694; binding py_linear module.cpp:6778-6804) with optional fused
+ * activation and residual.  Fusions apply each op's own narrowing in order (linear result
+ * narrowed to dtype, then the activation's, then the residual sum's), so a fused call equals
+ * the unfused op sequence.  lda/ldw/ldy are row strides in elements; b, residual may be NULL.
+ * x, w, b, y, residual share dtype (F16: fp16 MFMA, fp32 accumulate; F32: fp32 MFMA). */
+int mthip_linear(int device, int dtype, const void* x, int64_t lda, const void* w, int64_t ldw,
+                 const void* b, void* y, int64_t ldy, int64_t M, int64_t N, int64_t K, int act,
+                 const void* residual, int64_t ld_res);
+
+/* Batched GEMM: c[bt] = alpha * a[bt] . op(b[bt]) (+ beta * c_in), op(b) = b (b_trans=0,
+ * b is [K,N]) or b^T (b_trans=1, b is [N,K]).  Strides in elements; batch strides may be 0
+ * to broadcast.  c_in (may be NULL) is read with its own strides (broadcast allowed) and is
+ * narrowed as narrow(beta*c_in) before alpha*product is added, as addmm does
+ * (tensor.cpp:25253-25258, 25320-25334).  Serves matmul (tensor.cpp:24896-25064),
+ * batched_matmul (:24822-24894), bmm (:25066) and addmm (:25184-25366). */
+int mthip_gemm(int device, int dtype, int64_t batch, int64_t M, int64_t N, int64_t K,
+               const void* a, int64_t lda, int64_t stride_a,
+               const void* b, int64_t ldb, int64_t stride_b, int b_trans,
+               void* c, int64_t ldc, int64_t stride_c,
+               double alpha, double beta, const void* c_in, int64_t c_in_rs, int64_t c_in_cs,
+               int64_t stride_c_in);
+
+/* y[B,O,OH,OW] = conv2d(x[B,C,H,W], w[O,C/groups,KH,KW]) + b[O] (+ residual[B,O,OH,OW]),
+ * NCHW contiguous in and out -- mtorch::conv2d (tensor.cpp:26490-27528; py_conv2d
+ * module.cpp:6912-6961).  groups == 1 runs as an implicit GEMM on MFMA (fp16: fp32
+ * accumulate); the residual, when given, is added after the conv result is narrowed.
+ * `workspace` may be NULL (the library allocates). */
+int mthip_conv2d(int device, int dtype, const void* x, const void* w, const void* b, void* y,
+                 int64_t B, int64_t C, int64_t H, int64_t W, int64_t O, int64_t KH, int64_t KW,
+                 int64_t stride_h, int64_t stride_w, int64_t pad_h, int64_t pad_w,
+                 int64_t dil_h, int64_t dil_w, int64_t groups, const void* residual);
+
+/* ===================================================================== attention */
+
+enum { MTHIP_MASK_NONE = 0, MTHIP_MASK_BOOL = 1, MTHIP_MASK_ADD = 2 };
+
+/* o = softmax(q k^T * scale + mask) v over heads -- mtorch::scaled_dot_product_attention
+ * (tensor.cpp:30930-31324; py_scaled_dot_product_attention module.cpp:7407-7459).
+ * Layout: q[B,H,Lq,E], k[B,Hk,Lk,E], v[B,Hk,Lk,Ev] addressed by element strides
+ * (qs/ks/vs = {batch, head, seq}; the last dim is contiguous); o is contiguous [B,H,Lq,Ev].
+ * Hk divides H (H/Hk query heads share a key head: enable_gqa).  mask: MTHIP_MASK_BOOL
+ * (uint8, false -> -inf) or MTHIP_MASK_ADD (mask_dtype F32 or the query dtype, added to the
+ * scaled score), read through 4 strides {b, h, q, k} with 0 on broadcast axes.  is_causal
+ * masks keys after the query.  scale <= 0 selects 1/sqrt(E).  q/k/v/o share dtype F16
+ * (fp16 MFMA, fp32 softmax) or F32.  Fully-masked rows give NaN, as the reference does. */
+int mthip_sdpa(int device, int dtype, const void* q, const int64_t* qs, const void* k,
+               const int64_t* ks, const void* v, const int64_t* vs, void* o, int64_t B, int64_t H,
+               int64_t Hk, int64_t Lq, int64_t Lk, int64_t E, int64_t Ev, int mask_kind,
+               int mask_dtype, const void* mask, const int64_t* mask_strides, int is_causal,
+               double scale);
+
+/* ===================================================================== normalisation */
+
+/* group_norm on contiguous x[B, C, inner] (tensor.cpp:18643-18963; py_group_norm
+ * module.cpp:7646-7693); weight/bias [C] or NULL.  fuse_silu != 0 applies silu to the
+ * narrowed result (the GroupNorm->SiLU pair of every SD ResBlock) with silu's own rounding. */
+int mthip_group_norm(int device, int dtype, const void* x, const void* weight, const void* bias,
+                     void* y, int64_t B, int64_t C, int64_t inner, int64_t groups, double eps,
+                     int fuse_silu);
+
+/* layer_norm over the trailing N elements of contiguous x[rows, N] (tensor.cpp:17386-17708;
+ * py_layer_norm module.cpp:7461-7516); weight/bias [N] or NULL.  fp16 uses the two-pass
+ * centred variance, fp32 the one-pass form, as the reference does. */
+int mthip_layer_norm(int device, int dtype, const void* x, const void* weight, const void* bias,
+                     void* y, int64_t rows, int64_t N, double eps);
+
+/* softmax over the last dim of contiguous x[rows, cols] (tensor.cpp:15145-15221,
+ * try_softmax_float32_kernel :7508-7741, try_softmax_float16_kernel :7743-7802).
+ * divide != 0 divides by the row total (fp32 rank<=2), else multiplies by its reciprocal. */
+int mthip_softmax_lastdim(int device, int dtype, const void* x, void* y, int64_t rows,
+                          int64_t cols, int divide);
+
+/* ===================================================================== RNG (host) */
+
+/* mtorch's generator: splitmix64 + Marsaglia polar normals with a spare-normal cache
+ * (module.cpp:47-183, 245-274, 335-365).  A generator is an opaque host object; fills write
+ * host buffers of `dtype` (F16/F32) exactly as the reference's randn/normal_/uniform_ do. */
+void* mthip_generator_create(uint64_t seed);
+void mthip_generator_destroy(void* gen);
+int mthip_generator_seed(void* gen, uint64_t seed);           /* manual_seed module.cpp:2626 */
+int mthip_generator_get_state(void* gen, uint64_t* state, int* has_spare, double* spare);
+int mthip_generator_set_state(void* gen, uint64_t state, int has_spare, double spare);
+int mthip_rng_normal(void* gen, int dtype, void* host_dst, int64_t n, double mean, double std);
+int mthip_rng_uniform(void* gen, int dtype, void* host_dst, int64_t n, double from, double to);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* MTHIP_H */

@@ -1,0 +1,87 @@
+// Activation functions shared by the elementwise kernels and the GEMM/conv/norm epilogues,
+// each evaluated the way mtorch's Linux CPU path evaluates it for the given storage dtype.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+
+#include "common.h"
+
+namespace mthip {
+// fp32 GELU exactly as the reference's Linux fp32 path: truncated series for |x| <= 1,
+// else Abramowitz-Stegun 7.1.26 erf (tensor.cpp:17132-17154, 17265-17273).
+__device__ __forceinline__ float gelu_ref_f32(float x) {
+  if (fabsf(x) <= 1.0f) {
+    const float inv_sqrt_two_pi = 0.39894228040143267794f;
+    const float x2 = x * x;
+    const float series =
+        1.0f + x2 * (-1.0f / 6.0f + x2 * (1.0f / 40.0f + x2 * (-1.0f / 336.0f + x2 * (1.0f / 3456.0f + x2 * (-1.0f / 42240.0f)))));
+    return 0.5f * x + inv_sqrt_two_pi * x2 * series;
+  }
+  const float v = x * 0.70710678118654752440f;
+  const float sign = v < 0.0f ? -1.0f : 1.0f;
+  const float ax = fabsf(v);
+  const float t = 1.0f / (1.0f + 0.3275911f * ax);
+  const float poly = (((((1.061405429f * t + -1.453152027f) * t + 1.421413741f) * t + -0.284496736f) * t + 0.254829592f) * t);
+  const float erfv = sign * (1.0f - poly * expf(-ax * ax));
+  return 0.5f * x * (1.0f + erfv);
+}
+
+// fp16 GELU: the reference evaluates 0.5*x*(1+erf(x/sqrt 2)) in double (tensor.cpp:17103-17113,
+// 17225-17235); doubles are cheap next to the HBM traffic of this op.
+__device__ __forceinline__ float gelu_ref_f16(float xf) {
+  const double x = (double)xf;
+  return (float)(0.5 * x * (1.0 + erf(x * 0.70710678118654752440)));
+}
+
+__device__ __forceinline__ float gelu_tanh_f32(float x) {
+  return 0.5f * x * (1.0f + tanhf(0.79788456080286535588f * (x + 0.044715f * x * x * x)));
+}
+
+__device__ __forceinline__ float gelu_tanh_f16(float xf) {
+  const double x = (double)xf;
+  return (float)(0.5 * x * (1.0 + tanh(0.79788456080286535588 * (x + 0.044715 * x * x * x))));
+}
+
+template <typename T>
+__device__ __forceinline__ float apply_unary(int op, float x);
+
+template <>
+__device__ __forceinline__ float apply_unary<float>(int op, float x) {
+  switch (op) {
+    case MTHIP_UNARY_SILU: return x / (1.0f + expf(-x));
+    case MTHIP_UNARY_GELU: return gelu_ref_f32(x);
+    case MTHIP_UNARY_GELU_TANH: return gelu_tanh_f32(x);
+    case MTHIP_UNARY_EXP: return (float)exp((double)x);
+    case MTHIP_UNARY_SIN: return (float)sin((double)x);
+    case MTHIP_UNARY_COS: return (float)cos((double)x);
+    case MTHIP_UNARY_NEG: return -x;
+    case MTHIP_UNARY_SIGMOID: return (float)(1.0 / (1.0 + exp(-(double)x)));
+    default: return x > 0.0f ? x : 0.0f;
+  }
+}
+
+template <>
+__device__ __forceinline__ float apply_unary<uint16_t>(int op, float x) {
+  switch (op) {
+    case MTHIP_UNARY_SILU: return x / (1.0f + expf(-x));
+    case MTHIP_UNARY_GELU: return gelu_ref_f16(x);
+    case MTHIP_UNARY_GELU_TANH: return gelu_tanh_f16(x);
+    default: return apply_unary<float>(op, x);
+  }
+}
+
+
+// Activation codes of the fused epilogues (MTHIP_ACT_*) mapped onto the unary ops.
+template <typename T>
+__device__ __forceinline__ float apply_act(int act, float x) {
+  switch (act) {
+    case MTHIP_ACT_GELU: return apply_unary<T>(MTHIP_UNARY_GELU, x);
+    case MTHIP_ACT_GELU_TANH: return apply_unary<T>(MTHIP_UNARY_GELU_TANH, x);
+    case MTHIP_ACT_SILU: return apply_unary<T>(MTHIP_UNARY_SILU, x);
+    default: return x;
+  }
+}
+
+}  // namespace mthip

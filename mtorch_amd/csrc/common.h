@@ -1,0 +1,102 @@
+// Shared definitions for libmthip: dtype codes, error plumbing, stream access and the
+// device-side fp16 conversion that follows mtorch's rounding rule.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <cstring>
+#include <string>
+
+#include "../../include/mthip.h"
+
+namespace mthip {
+
+// ---- errors -----------------------------------------------------------------------------
+// Every C entry point returns 0 on success; on failure it stores a message retrievable
+// through mthip_last_error() (thread-local) and returns a non-zero status.
+void set_error(const std::string& msg);
+int fail(int code, const std::string& msg);
+
+#define MTHIP_CHECK_HIP(expr)                                                                  \
+  do {                                                                                         \
+    hipError_t _e = (expr);                                                                    \
+    if (_e != hipSuccess)                                                                      \
+      return ::mthip::fail(MTHIP_ERR_HIP, std::string(#expr) + ": " + hipGetErrorString(_e)); \
+  } while (0)
+
+#define MTHIP_REQUIRE(cond, msg)                                        \
+  do {                                                                  \
+    if (!(cond)) return ::mthip::fail(MTHIP_ERR_INVALID, (msg));        \
+  } while (0)
+
+// Per-device in-order stream (created on first use, default priority, non-blocking with
+// respect to the legacy null stream).  Returns nullptr and sets the error on failure.
+hipStream_t stream_for(int device);
+// Makes `device` current for the calling host thread; returns 0 or an error status.
+int use_device(int device);
+// After a kernel launch: turns a launch error into a status.
+int check_launch(const char* what);
+
+__host__ __device__ inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// ---- device fp16 conversion ------------------------------------------------------------
+// mtorch's float_to_half_bits (tensor.cpp:276-315) rounds the magnitude half-away-from-zero
+// (add 0x1000 then drop 13 bits), shifts subnormals before rounding and flushes anything
+// below 2^-25 to a signed zero.  The hardware v_cvt_f16_f32 rounds to nearest-even, so every
+// kernel that narrows to fp16 uses this integer restatement instead.
+__device__ __forceinline__ uint16_t f2h_bits(float value) {
+  const uint32_t bits = __float_as_uint(value);
+  const uint32_t sign = (bits >> 16) & 0x8000u;
+  const uint32_t raw_exponent = (bits >> 23) & 0xffu;
+  uint32_t mantissa = bits & 0x7fffffu;
+  if (raw_exponent == 0xffu) {
+    if (mantissa == 0) return (uint16_t)(sign | 0x7c00u);
+    const uint32_t payload = mantissa >> 13;
+    return (uint16_t)(sign | 0x7c00u | (payload == 0 ? 0x0200u : payload));
+  }
+  int32_t exponent = (int32_t)raw_exponent - 112;  // -127 + 15
+  if (exponent <= 0) {
+    if (exponent < -10) return (uint16_t)sign;
+    mantissa = (mantissa | 0x800000u) >> (1 - exponent);
+    return (uint16_t)(sign | ((mantissa + 0x1000u) >> 13));
+  }
+  // Normal range: rounding may carry into the exponent; a carry out of exponent 30 gives
+  // 0x7c00 (inf), which is exactly what adding the rounded mantissa bits produces.
+  const uint32_t rounded = ((uint32_t)exponent << 10) + ((mantissa + 0x1000u) >> 13);
+  return (uint16_t)(sign | (rounded >= 0x7c00u ? 0x7c00u : rounded));
+}
+
+// Exact widening; finite values and infinities match tensor.cpp:317-344 bit for bit.
+__device__ __forceinline__ float h2f_bits(uint16_t h) {
+  return (float)__builtin_bit_cast(_Float16, h);
+}
+
+// Exact widening including NaN payloads (integer restatement of tensor.cpp:317-344),
+// used by the dtype-cast kernel where bit-exactness covers every pattern.
+__device__ __forceinline__ float h2f_exact(uint16_t value) {
+  const uint32_t sign = (uint32_t)(value & 0x8000u) << 16;
+  const uint32_t exponent = (value >> 10) & 0x1fu;
+  const uint32_t mantissa = value & 0x03ffu;
+  if (exponent == 31) return __uint_as_float(sign | 0x7f800000u | (mantissa << 13));
+  return (float)__builtin_bit_cast(_Float16, value);
+}
+
+// Element load/store in the op's dtype, computing in fp32.
+template <typename T>
+struct Elem;
+template <>
+struct Elem<float> {
+  static __device__ __forceinline__ float load(const float* p, int64_t i) { return p[i]; }
+  static __device__ __forceinline__ void store(float* p, int64_t i, float v) { p[i] = v; }
+  // Value as the reference would read it back after storing (identity for fp32).
+  static __device__ __forceinline__ float round_trip(float v) { return v; }
+};
+template <>
+struct Elem<uint16_t> {
+  static __device__ __forceinline__ float load(const uint16_t* p, int64_t i) { return h2f_bits(p[i]); }
+  static __device__ __forceinline__ void store(uint16_t* p, int64_t i, float v) { p[i] = f2h_bits(v); }
+  static __device__ __forceinline__ float round_trip(float v) { return h2f_bits(f2h_bits(v)); }
+};
+
+}  // namespace mthip

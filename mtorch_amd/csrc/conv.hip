@@ -1,0 +1,184 @@
+// conv2d (NCHW in, NCHW out) as an implicit GEMM on MFMA.
+//
+//   Y[o, pixel] = sum_{ky,kx,c} Wp[o, (ky,kx,c)] * X_nhwc[img, oy*s-p+ky*d, ox*s-p+kx*d, c]
+//
+// The activation is staged once as NHWC with the channel count padded to a whole 16-byte
+// chunk (Cp), and the weight as [O][KH][KW][Cp], so every im2col chunk the GEMM gathers is a
+// single aligned 16-byte load of Cp-contiguous channels.  Rows of the GEMM are output channels
+// and columns are output pixels, so the MFMA output lanes walk consecutive pixels and the
+// NCHW store stays coalesced.  Bias and an optional residual are applied in the epilogue.
+#include <hip/hip_runtime.h>
+
+#include "gemm_core.h"
+
+namespace mthip {
+
+int launch_conv_gemm(int dtype, const GemmArgs& a, hipStream_t s);
+
+namespace {
+
+// xp[b][hw][cp] = x[b][c][hw] (0 for c >= C), through a 32x32 LDS tile.
+template <typename T>
+__global__ void nchw_to_nhwc_pad_kernel(const T* __restrict__ x, T* __restrict__ xp, int64_t C, int64_t Cp,
+                                        int64_t HW) {
+  __shared__ T tile[32][33];
+  const int64_t b = blockIdx.z;
+  const int64_t hw0 = (int64_t)blockIdx.x * 32, c0 = (int64_t)blockIdx.y * 32;
+  const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;
+  for (int j = ty; j < 32; j += 8) {
+    const int64_t c = c0 + j, hw = hw0 + tx;
+    T v = T(0);
+    if (c < C && hw < HW) v = x[(b * C + c) * HW + hw];
+    tile[j][tx] = v;
+  }
+  __syncthreads();
+  for (int j = ty; j < 32; j += 8) {
+    const int64_t hw = hw0 + j, c = c0 + tx;
+    if (hw < HW && c < Cp) xp[(b * HW + hw) * Cp + c] = tile[tx][j];
+  }
+}
+
+// wp[o][ky][kx][cp] = w[o][c][ky][kx] (0 for c >= C).
+template <typename T>
+__global__ void pack_weight_kernel(const T* __restrict__ w, T* __restrict__ wp, int64_t O, int64_t C, int64_t Cp,
+                                   int64_t KH, int64_t KW) {
+  const int64_t n = O * KH * KW * Cp;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+    const int64_t c = i % Cp;
+    int64_t t = i / Cp;
+    const int64_t kx = t % KW;
+    t /= KW;
+    const int64_t ky = t % KH;
+    const int64_t o = t / KH;
+    wp[i] = c < C ? w[((o * C + c) * KH + ky) * KW + kx] : T(0);
+  }
+}
+
+// Direct convolution for grouped convs (not on the SD path): one lane per output element,
+// fp32 accumulation in (c, ky, kx) order.
+template <typename T>
+__global__ void conv_direct_kernel(const T* __restrict__ x, const T* __restrict__ w, const T* __restrict__ bias,
+                                   const T* __restrict__ residual, T* __restrict__ y, int64_t B, int64_t C, int64_t H,
+                                   int64_t W, int64_t O, int64_t KH, int64_t KW, int64_t OH, int64_t OW, int64_t sh,
+                                   int64_t sw, int64_t ph, int64_t pw, int64_t dh, int64_t dw, int64_t groups) {
+  const int64_t n = B * O * OH * OW;
+  const int64_t Cg = C / groups, Og = O / groups;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+    const int64_t ox = i % OW;
+    int64_t t = i / OW;
+    const int64_t oy = t % OH;
+    t /= OH;
+    const int64_t o = t % O;
+    const int64_t b = t / O;
+    const int64_t c0 = (o / Og) * Cg;
+    float acc = 0.0f;
+    for (int64_t c = 0; c < Cg; ++c)
+      for (int64_t ky = 0; ky < KH; ++ky) {
+        const int64_t iy = oy * sh - ph + ky * dh;
+        if (iy < 0 || iy >= H) continue;
+        for (int64_t kx = 0; kx < KW; ++kx) {
+          const int64_t ix = ox * sw - pw + kx * dw;
+          if (ix < 0 || ix >= W) continue;
+          acc += Elem<T>::load(x, ((b * C + c0 + c) * H + iy) * W + ix) * Elem<T>::load(w, ((o * Cg + c) * KH + ky) * KW + kx);
+        }
+      }
+    if (bias) acc += Elem<T>::load(bias, o);
+    if (residual) acc = Elem<T>::round_trip(acc) + Elem<T>::load(residual, i);
+    Elem<T>::store(y, i, acc);
+  }
+}
+
+template <typename T>
+int run_conv(int device, int dtype, const void* x, const void* w, const void* b, void* y, int64_t B, int64_t C,
+             int64_t H, int64_t W, int64_t O, int64_t KH, int64_t KW, int64_t sh, int64_t sw, int64_t ph, int64_t pw,
+             int64_t dh, int64_t dw, int64_t groups, const void* residual, hipStream_t s) {
+  const int64_t OH = (H + 2 * ph - dh * (KH - 1) - 1) / sh + 1;
+  const int64_t OW = (W + 2 * pw - dw * (KW - 1) - 1) / sw + 1;
+  if (B == 0 || O == 0 || OH <= 0 || OW <= 0) return MTHIP_OK;
+  if (groups != 1) {
+    const int64_t n = B * O * OH * OW;
+    const unsigned g = (unsigned)std::min<int64_t>(ceil_div(n, 256), 8192);
+    hipLaunchKernelGGL(conv_direct_kernel<T>, dim3(g), dim3(256), 0, s, (const T*)x, (const T*)w, (const T*)b,
+                       (const T*)residual, (T*)y, B, C, H, W, O, KH, KW, OH, OW, sh, sw, ph, pw, dh, dw, groups);
+    return check_launch("conv_direct_kernel");
+  }
+  constexpr int VEC = Mfma<T>::VEC;
+  const int64_t Cp = ceil_div(C, VEC) * VEC;
+  const int64_t HW = H * W;
+  const int64_t K = KH * KW * Cp;
+  void* xp = nullptr;
+  void* wp = nullptr;
+  if (int rc = mthip_malloc(device, (size_t)(B * HW * Cp) * sizeof(T), &xp)) return rc;
+  if (int rc = mthip_malloc(device, (size_t)(O * K) * sizeof(T), &wp)) {
+    mthip_free(device, xp);
+    return rc;
+  }
+  int rc = MTHIP_OK;
+  {
+    dim3 grid((unsigned)ceil_div(HW, 32), (unsigned)ceil_div(Cp, 32), (unsigned)B);
+    hipLaunchKernelGGL(nchw_to_nhwc_pad_kernel<T>, grid, dim3(256), 0, s, (const T*)x, (T*)xp, C, Cp, HW);
+    rc = check_launch("nchw_to_nhwc_pad_kernel");
+  }
+  if (rc == MTHIP_OK) {
+    const int64_t n = O * K;
+    hipLaunchKernelGGL(pack_weight_kernel<T>, dim3((unsigned)std::min<int64_t>(ceil_div(n, 256), 4096)), dim3(256), 0, s,
+                       (const T*)w, (T*)wp, O, C, Cp, KH, KW);
+    rc = check_launch("pack_weight_kernel");
+  }
+  if (rc == MTHIP_OK) {
+    GemmArgs a{};
+    a.M = O;
+    a.N = B * OH * OW;
+    a.K = K;
+    a.a = wp;
+    a.lda = K;
+    a.b = xp;
+    a.c = y;
+    a.bias = b;
+    a.residual = residual;
+    a.H = H;
+    a.W = W;
+    a.Cp = Cp;
+    a.OH = OH;
+    a.OW = OW;
+    a.KW = KW;
+    a.sh = sh;
+    a.sw = sw;
+    a.ph = ph;
+    a.pw = pw;
+    a.dh = dh;
+    a.dw = dw;
+    a.vec_ok = 1;  // packed buffers: rows are whole chunks, bases come from the allocator
+    rc = launch_conv_gemm(dtype, a, s);
+  }
+  // Stream-ordered frees: the blocks are only reused by work enqueued after this conv.
+  mthip_free(device, xp);
+  mthip_free(device, wp);
+  return rc;
+}
+
+}  // namespace
+}  // namespace mthip
+
+using namespace mthip;
+
+extern "C" int mthip_conv2d(int device, int dtype, const void* x, const void* w, const void* b, void* y, int64_t B,
+                            int64_t C, int64_t H, int64_t W, int64_t O, int64_t KH, int64_t KW, int64_t stride_h,
+                            int64_t stride_w, int64_t pad_h, int64_t pad_w, int64_t dil_h, int64_t dil_w,
+                            int64_t groups, const void* residual) {
+  MTHIP_REQUIRE(dtype == MTHIP_F16 || dtype == MTHIP_F32, "mthip_conv2d: dtype must be F16 or F32");
+  MTHIP_REQUIRE(B >= 0 && C > 0 && H > 0 && W > 0 && O > 0 && KH > 0 && KW > 0, "mthip_conv2d: bad extents");
+  MTHIP_REQUIRE(stride_h > 0 && stride_w > 0 && dil_h > 0 && dil_w > 0 && pad_h >= 0 && pad_w >= 0,
+                "mthip_conv2d: bad stride/padding/dilation");
+  MTHIP_REQUIRE(groups > 0 && C % groups == 0 && O % groups == 0, "mthip_conv2d: bad groups");
+  hipStream_t s = stream_for(device);
+  if (!s) return MTHIP_ERR_HIP;
+  if (int rc = use_device(device)) return rc;
+  if (dtype == MTHIP_F16)
+    return run_conv<uint16_t>(device, dtype, x, w, b, y, B, C, H, W, O, KH, KW, stride_h, stride_w, pad_h, pad_w,
+                              dil_h, dil_w, groups, residual, s);
+  return run_conv<float>(device, dtype, x, w, b, y, B, C, H, W, O, KH, KW, stride_h, stride_w, pad_h, pad_w, dil_h,
+                         dil_w, groups, residual, s);
+}

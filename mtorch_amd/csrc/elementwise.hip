@@ -1,0 +1,572 @@
+// HBM-streaming elementwise kernels: casts, fills, strided copies, broadcast binary ops,
+// activations, GEGLU gating, concatenation and nearest upsampling.
+//
+// Contiguous inputs run through grid-stride loops that move 16 bytes per lane per step;
+// strided and broadcast inputs go through a rank-collapsed index walk.  Every narrowing to
+// fp16 uses f2h_bits (mtorch's half-away-from-zero rule).
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <vector>
+
+#include "activations.h"
+#include "common.h"
+
+namespace mthip {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kMaxRank = 8;
+
+// Enough workgroups to cover every CU several times over; grid-stride loops do the rest.
+inline unsigned grid_for(int64_t work_items, int per_thread = 1) {
+  int64_t blocks = ceil_div(std::max<int64_t>(work_items, 1), (int64_t)kThreads * per_thread);
+  return (unsigned)std::min<int64_t>(blocks, 256 * 32);
+}
+
+struct Shape {
+  int rank;
+  int64_t sizes[kMaxRank];
+  int64_t a_strides[kMaxRank];
+  int64_t b_strides[kMaxRank];
+};
+
+// Merge adjacent dims whose strides are contiguous with respect to each other in every
+// operand, and drop size-1 dims.  Returns the collapsed rank (0 means a single element).
+int collapse(int rank, const int64_t* sizes, const int64_t* const* strides, int n_ops,
+             int64_t* out_sizes, int64_t* const* out_strides) {
+  int r = 0;
+  for (int d = 0; d < rank; ++d) {
+    if (sizes[d] == 1) continue;
+    if (r > 0) {
+      bool merge = true;
+      for (int o = 0; o < n_ops; ++o) {
+        if (out_strides[o][r - 1] != strides[o][d] * sizes[d]) merge = false;
+      }
+      if (merge) {
+        out_sizes[r - 1] *= sizes[d];
+        for (int o = 0; o < n_ops; ++o) out_strides[o][r - 1] = strides[o][d];
+        continue;
+      }
+    }
+    out_sizes[r] = sizes[d];
+    for (int o = 0; o < n_ops; ++o) out_strides[o][r] = strides[o][d];
+    ++r;
+  }
+  return r;
+}
+
+// ------------------------------------------------------------------------------ casts
+// Element readers/writers by dtype code for the cast kernel (values widened to double, the
+// way storage_get_unchecked does; narrowed the way storage_set_unchecked does).
+__device__ __forceinline__ double read_as_double(int dtype, const void* p, int64_t i) {
+  switch (dtype) {
+    case MTHIP_F16: return (double)h2f_exact(((const uint16_t*)p)[i]);
+    case MTHIP_F32: return (double)((const float*)p)[i];
+    case MTHIP_F64: return ((const double*)p)[i];
+    case MTHIP_I32: return (double)((const int32_t*)p)[i];
+    case MTHIP_I64: return (double)((const int64_t*)p)[i];
+    default: return ((const uint8_t*)p)[i] ? 1.0 : 0.0;
+  }
+}
+
+__device__ __forceinline__ void write_from_double(int dtype, void* p, int64_t i, double v) {
+  switch (dtype) {
+    case MTHIP_F16: ((uint16_t*)p)[i] = f2h_bits((float)v); break;
+    case MTHIP_F32: ((float*)p)[i] = (float)v; break;
+    case MTHIP_F64: ((double*)p)[i] = v; break;
+    case MTHIP_I32: ((int32_t*)p)[i] = (int32_t)v; break;
+    case MTHIP_I64: ((int64_t*)p)[i] = (int64_t)v; break;
+    default: ((uint8_t*)p)[i] = v == 0.0 ? 0 : 1; break;
+  }
+}
+
+// fp32 -> fp16, 8 elements per lane per step (two 16-byte loads, one 16-byte store).
+__global__ void cast_f32_f16_kernel(const float* __restrict__ src, uint16_t* __restrict__ dst, int64_t n) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  const int64_t nvec = n / 8;
+  for (int64_t v = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; v < nvec; v += stride) {
+    const float4 a = reinterpret_cast<const float4*>(src)[2 * v];
+    const float4 b = reinterpret_cast<const float4*>(src)[2 * v + 1];
+    uint4 out;
+    out.x = (uint32_t)f2h_bits(a.x) | ((uint32_t)f2h_bits(a.y) << 16);
+    out.y = (uint32_t)f2h_bits(a.z) | ((uint32_t)f2h_bits(a.w) << 16);
+    out.z = (uint32_t)f2h_bits(b.x) | ((uint32_t)f2h_bits(b.y) << 16);
+    out.w = (uint32_t)f2h_bits(b.z) | ((uint32_t)f2h_bits(b.w) << 16);
+    reinterpret_cast<uint4*>(dst)[v] = out;
+  }
+  for (int64_t i = nvec * 8 + (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
+    dst[i] = f2h_bits(src[i]);
+}
+
+__global__ void cast_f16_f32_kernel(const uint16_t* __restrict__ src, float* __restrict__ dst, int64_t n) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  const int64_t nvec = n / 8;
+  for (int64_t v = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; v < nvec; v += stride) {
+    const uint4 in = reinterpret_cast<const uint4*>(src)[v];
+    float4 a, b;
+    a.x = h2f_exact((uint16_t)(in.x & 0xffff));
+    a.y = h2f_exact((uint16_t)(in.x >> 16));
+    a.z = h2f_exact((uint16_t)(in.y & 0xffff));
+    a.w = h2f_exact((uint16_t)(in.y >> 16));
+    b.x = h2f_exact((uint16_t)(in.z & 0xffff));
+    b.y = h2f_exact((uint16_t)(in.z >> 16));
+    b.z = h2f_exact((uint16_t)(in.w & 0xffff));
+    b.w = h2f_exact((uint16_t)(in.w >> 16));
+    reinterpret_cast<float4*>(dst)[2 * v] = a;
+    reinterpret_cast<float4*>(dst)[2 * v + 1] = b;
+  }
+  for (int64_t i = nvec * 8 + (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
+    dst[i] = h2f_exact(src[i]);
+}
+
+// Dense casts convert element by element with static_cast (cast_dense_numeric_to_half /
+// cast_dense_half_to_numeric, tensor.cpp:2633-2657): fp32<->fp16 never widens to double, so
+// NaN payloads pass through untouched; the other pairs go through double exactly.
+__global__ void cast_generic_kernel(int src_dtype, const void* src, int dst_dtype, void* dst, int64_t n) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+    if (src_dtype == MTHIP_F32 && dst_dtype == MTHIP_F16)
+      ((uint16_t*)dst)[i] = f2h_bits(((const float*)src)[i]);
+    else if (src_dtype == MTHIP_F16 && dst_dtype == MTHIP_F32)
+      ((float*)dst)[i] = h2f_exact(((const uint16_t*)src)[i]);
+    else
+      write_from_double(dst_dtype, dst, i, read_as_double(src_dtype, src, i));
+  }
+}
+
+// ------------------------------------------------------------------------------ copies
+template <typename T>
+__global__ void copy_strided_kernel(const T* __restrict__ src, T* __restrict__ dst, Shape s, int64_t n) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+    int64_t rem = i, off = 0;
+    for (int d = s.rank - 1; d >= 0; --d) {
+      const int64_t idx = rem % s.sizes[d];
+      rem /= s.sizes[d];
+      off += idx * s.a_strides[d];
+    }
+    dst[i] = src[off];
+  }
+}
+
+// 2-D tiled transpose through LDS for views whose source is unit-stride along the second-last
+// collapsed dim (head split/merge [B,L,H,D] <-> [B,H,L,D], NCHW <-> NHWC):
+//   dst[b][r][c] (contiguous, c fastest) = src[b*sb + r + c*sc].
+// Reads walk r across lanes and writes walk c across lanes, so both are coalesced.
+template <typename T>
+__global__ void transpose_kernel(const T* __restrict__ src, T* __restrict__ dst, int64_t R, int64_t C, int64_t sb,
+                                 int64_t sc) {
+  __shared__ T tile[32][33];
+  const int64_t b = blockIdx.z;
+  const int64_t r0 = (int64_t)blockIdx.x * 32, c0 = (int64_t)blockIdx.y * 32;
+  const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;  // 32 x 8 threads
+  for (int j = ty; j < 32; j += 8) {
+    const int64_t r = r0 + tx, c = c0 + j;
+    if (r < R && c < C) tile[j][tx] = src[b * sb + r + c * sc];
+  }
+  __syncthreads();
+  for (int j = ty; j < 32; j += 8) {
+    const int64_t c = c0 + tx, r = r0 + j;
+    if (r < R && c < C) dst[(b * R + r) * C + c] = tile[tx][j];
+  }
+}
+
+template <typename T>
+__global__ void fill_kernel(T* __restrict__ dst, int64_t n, T value) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) dst[i] = value;
+}
+
+// ------------------------------------------------------------------------------ binary
+__device__ __forceinline__ float apply_bin(int op, float a, float b) {
+  switch (op) {
+    case MTHIP_BIN_ADD: return a + b;
+    case MTHIP_BIN_MUL: return a * b;
+    case MTHIP_BIN_SUB: return a - b;
+    default: return a / b;
+  }
+}
+
+template <typename T>
+__global__ void binary_contig_kernel(int op, const T* __restrict__ a, const T* __restrict__ b, T* __restrict__ out,
+                                     int64_t n) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
+    Elem<T>::store(out, i, apply_bin(op, Elem<T>::load(a, i), Elem<T>::load(b, i)));
+}
+
+// fp16 same-shape add/mul with 8 lanes-elements per 16-byte access.
+__global__ void binary_contig_h8_kernel(int op, const uint4* __restrict__ a, const uint4* __restrict__ b,
+                                        uint4* __restrict__ out, int64_t nvec) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t v = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; v < nvec; v += stride) {
+    const uint4 x = a[v], y = b[v];
+    const uint32_t xs[4] = {x.x, x.y, x.z, x.w}, ys[4] = {y.x, y.y, y.z, y.w};
+    uint32_t r[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float lo = apply_bin(op, h2f_bits((uint16_t)(xs[j] & 0xffff)), h2f_bits((uint16_t)(ys[j] & 0xffff)));
+      const float hi = apply_bin(op, h2f_bits((uint16_t)(xs[j] >> 16)), h2f_bits((uint16_t)(ys[j] >> 16)));
+      r[j] = (uint32_t)f2h_bits(lo) | ((uint32_t)f2h_bits(hi) << 16);
+    }
+    out[v] = make_uint4(r[0], r[1], r[2], r[3]);
+  }
+}
+
+template <typename T>
+__global__ void binary_strided_kernel(int op, const T* __restrict__ a, const T* __restrict__ b, T* __restrict__ out,
+                                      Shape s, int64_t n) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+    int64_t rem = i, oa = 0, ob = 0;
+    for (int d = s.rank - 1; d >= 0; --d) {
+      const int64_t idx = rem % s.sizes[d];
+      rem /= s.sizes[d];
+      oa += idx * s.a_strides[d];
+      ob += idx * s.b_strides[d];
+    }
+    Elem<T>::store(out, i, apply_bin(op, Elem<T>::load(a, oa), Elem<T>::load(b, ob)));
+  }
+}
+
+// Tensor-scalar ops run in double and are narrowed once, as the reference's double path does.
+template <typename T>
+__global__ void binary_scalar_kernel(int op, const T* __restrict__ x, double scalar, int scalar_first,
+                                     T* __restrict__ out, int64_t n) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+    const double v = (double)Elem<T>::load(x, i);
+    const double l = scalar_first ? scalar : v, r = scalar_first ? v : scalar;
+    double res;
+    switch (op) {
+      case MTHIP_BIN_ADD: res = l + r; break;
+      case MTHIP_BIN_MUL: res = l * r; break;
+      case MTHIP_BIN_SUB: res = l - r; break;
+      default: res = l / r; break;
+    }
+    Elem<T>::store(out, i, (float)res);
+  }
+}
+
+// ------------------------------------------------------------------------------ unary
+template <typename T>
+__global__ void unary_kernel(int op, const T* __restrict__ x, T* __restrict__ y, int64_t n) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
+    Elem<T>::store(y, i, apply_unary<T>(op, Elem<T>::load(x, i)));
+}
+
+template <typename T>
+__global__ void geglu_kernel(const T* __restrict__ x, T* __restrict__ y, int64_t rows, int64_t D) {
+  const int64_t n = rows * D;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+    const int64_t r = i / D, d = i - r * D;
+    const float val = Elem<T>::load(x, r * 2 * D + d);
+    const float gate = Elem<T>::load(x, r * 2 * D + D + d);
+    const float g = Elem<T>::round_trip(apply_unary<T>(MTHIP_UNARY_GELU, gate));
+    Elem<T>::store(y, i, val * g);
+  }
+}
+
+// ------------------------------------------------------------------------------ cat / upsample
+template <typename T>
+__global__ void copy_2d_kernel(const T* __restrict__ src, T* __restrict__ dst, int64_t outer, int64_t inner,
+                               int64_t dst_row_stride) {
+  const int64_t n = outer * inner;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+    const int64_t o = i / inner, j = i - o * inner;
+    dst[o * dst_row_stride + j] = src[i];
+  }
+}
+
+template <typename T>
+__global__ void upsample_nearest_kernel(const T* __restrict__ x, T* __restrict__ y, int64_t planes, int64_t H,
+                                        int64_t W, int64_t sh, int64_t sw) {
+  const int64_t OH = H * sh, OW = W * sw;
+  const int64_t n = planes * OH * OW;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+    const int64_t ox = i % OW;
+    const int64_t t = i / OW;
+    const int64_t oy = t % OH;
+    const int64_t p = t / OH;
+    y[i] = x[(p * H + oy / sh) * W + ox / sw];
+  }
+}
+
+int elem_size(int dtype) {
+  switch (dtype) {
+    case MTHIP_F16: return 2;
+    case MTHIP_F32: return 4;
+    case MTHIP_F64: return 8;
+    case MTHIP_I32: return 4;
+    case MTHIP_I64: return 8;
+    case MTHIP_BOOL: return 1;
+    default: return 0;
+  }
+}
+
+}  // namespace
+}  // namespace mthip
+
+using namespace mthip;
+
+extern "C" {
+
+int mthip_cast(int device, int src_dtype, const void* src, int dst_dtype, void* dst, int64_t n) {
+  MTHIP_REQUIRE(elem_size(src_dtype) && elem_size(dst_dtype), "mthip_cast: unknown dtype");
+  MTHIP_REQUIRE(n >= 0, "mthip_cast: negative element count");
+  if (n == 0) return MTHIP_OK;
+  hipStream_t s = stream_for(device);
+  if (!s) return MTHIP_ERR_HIP;
+  if (int rc = use_device(device)) return rc;
+  const bool aligned = ((uintptr_t)src % 16 == 0) && ((uintptr_t)dst % 16 == 0);
+  if (src_dtype == dst_dtype) {
+    MTHIP_CHECK_HIP(hipMemcpyAsync(dst, src, (size_t)n * elem_size(src_dtype), hipMemcpyDeviceToDevice, s));
+    return MTHIP_OK;
+  }
+  if (src_dtype == MTHIP_F32 && dst_dtype == MTHIP_F16 && aligned) {
+    hipLaunchKernelGGL(cast_f32_f16_kernel, dim3(grid_for(n, 8)), dim3(kThreads), 0, s, (const float*)src, (uint16_t*)dst, n);
+  } else if (src_dtype == MTHIP_F16 && dst_dtype == MTHIP_F32 && aligned) {
+    hipLaunchKernelGGL(cast_f16_f32_kernel, dim3(grid_for(n, 8)), dim3(kThreads), 0, s, (const uint16_t*)src, (float*)dst, n);
+  } else {
+    hipLaunchKernelGGL(cast_generic_kernel, dim3(grid_for(n)), dim3(kThreads), 0, s, src_dtype, src, dst_dtype, dst, n);
+  }
+  return check_launch("mthip_cast");
+}
+
+int mthip_copy_strided(int device, int dtype, const void* src, int rank, const int64_t* sizes,
+                       const int64_t* src_strides, void* dst) {
+  const int es = elem_size(dtype);
+  MTHIP_REQUIRE(es != 0, "mthip_copy_strided: unknown dtype");
+  MTHIP_REQUIRE(rank >= 0 && rank <= kMaxRank, "mthip_copy_strided: rank must be <= 8");
+  int64_t n = 1;
+  for (int d = 0; d < rank; ++d) {
+    MTHIP_REQUIRE(sizes[d] >= 0, "mthip_copy_strided: negative size");
+    n *= sizes[d];
+  }
+  if (n == 0) return MTHIP_OK;
+  hipStream_t s = stream_for(device);
+  if (!s) return MTHIP_ERR_HIP;
+  if (int rc = use_device(device)) return rc;
+  // Destination strides are contiguous; collapse dims jointly with the source strides.
+  int64_t dst_strides[kMaxRank];
+  {
+    int64_t acc = 1;
+    for (int d = rank - 1; d >= 0; --d) {
+      dst_strides[d] = acc;
+      acc *= sizes[d];
+    }
+  }
+  Shape sh{};
+  int64_t* outs[2] = {sh.a_strides, sh.b_strides};
+  const int64_t* ins[2] = {src_strides, dst_strides};
+  sh.rank = collapse(rank, sizes, ins, 2, sh.sizes, outs);
+  if (sh.rank == 0 || (sh.rank == 1 && sh.a_strides[0] == 1)) {
+    MTHIP_CHECK_HIP(hipMemcpyAsync(dst, src, (size_t)n * es, hipMemcpyDeviceToDevice, s));
+    return MTHIP_OK;
+  }
+  // Source unit-stride along the second-last collapsed dim: tiled transpose through LDS.
+  if (sh.rank >= 2 && sh.rank <= 3 && sh.a_strides[sh.rank - 2] == 1 && (es == 2 || es == 4)) {
+    const int64_t R = sh.sizes[sh.rank - 2], C = sh.sizes[sh.rank - 1];
+    const int64_t batch = sh.rank == 3 ? sh.sizes[0] : 1;
+    const int64_t sb = sh.rank == 3 ? sh.a_strides[0] : 0;
+    const int64_t sc = sh.a_strides[sh.rank - 1];
+    dim3 grid((unsigned)ceil_div(R, 32), (unsigned)ceil_div(C, 32), (unsigned)batch);
+    if (batch <= 65535 && ceil_div(C, 32) <= 65535) {
+      if (es == 2)
+        hipLaunchKernelGGL(transpose_kernel<uint16_t>, grid, dim3(256), 0, s, (const uint16_t*)src, (uint16_t*)dst, R, C, sb, sc);
+      else
+        hipLaunchKernelGGL(transpose_kernel<uint32_t>, grid, dim3(256), 0, s, (const uint32_t*)src, (uint32_t*)dst, R, C, sb, sc);
+      return check_launch("mthip_copy_strided(transpose)");
+    }
+  }
+  switch (es) {
+    case 1: hipLaunchKernelGGL(copy_strided_kernel<uint8_t>, dim3(grid_for(n)), dim3(kThreads), 0, s, (const uint8_t*)src, (uint8_t*)dst, sh, n); break;
+    case 2: hipLaunchKernelGGL(copy_strided_kernel<uint16_t>, dim3(grid_for(n)), dim3(kThreads), 0, s, (const uint16_t*)src, (uint16_t*)dst, sh, n); break;
+    case 4: hipLaunchKernelGGL(copy_strided_kernel<uint32_t>, dim3(grid_for(n)), dim3(kThreads), 0, s, (const uint32_t*)src, (uint32_t*)dst, sh, n); break;
+    default: hipLaunchKernelGGL(copy_strided_kernel<uint64_t>, dim3(grid_for(n)), dim3(kThreads), 0, s, (const uint64_t*)src, (uint64_t*)dst, sh, n); break;
+  }
+  return check_launch("mthip_copy_strided");
+}
+
+int mthip_fill(int device, int dtype, void* dst, int64_t n, double value) {
+  MTHIP_REQUIRE(elem_size(dtype) != 0, "mthip_fill: unknown dtype");
+  if (n <= 0) return MTHIP_OK;
+  hipStream_t s = stream_for(device);
+  if (!s) return MTHIP_ERR_HIP;
+  if (int rc = use_device(device)) return rc;
+  const unsigned g = grid_for(n);
+  switch (dtype) {
+    case MTHIP_F16: {
+      // f2h_bits is a device function; the host restatement below mirrors it for one value.
+      float f = (float)value;
+      uint32_t bits;
+      std::memcpy(&bits, &f, 4);
+      const uint32_t sign = (bits >> 16) & 0x8000u, raw = (bits >> 23) & 0xffu;
+      uint32_t man = bits & 0x7fffffu;
+      uint16_t h;
+      if (raw == 0xffu) {
+        h = (uint16_t)(sign | 0x7c00u | (man ? ((man >> 13) ? (man >> 13) : 0x200u) : 0u));
+      } else {
+        int32_t e = (int32_t)raw - 112;
+        if (e <= 0) {
+          h = e < -10 ? (uint16_t)sign : (uint16_t)(sign | ((((man | 0x800000u) >> (1 - e)) + 0x1000u) >> 13));
+        } else {
+          const uint32_t r = ((uint32_t)e << 10) + ((man + 0x1000u) >> 13);
+          h = (uint16_t)(sign | (r >= 0x7c00u ? 0x7c00u : r));
+        }
+      }
+      hipLaunchKernelGGL(fill_kernel<uint16_t>, dim3(g), dim3(kThreads), 0, s, (uint16_t*)dst, n, h);
+      break;
+    }
+    case MTHIP_F32: hipLaunchKernelGGL(fill_kernel<float>, dim3(g), dim3(kThreads), 0, s, (float*)dst, n, (float)value); break;
+    case MTHIP_F64: hipLaunchKernelGGL(fill_kernel<double>, dim3(g), dim3(kThreads), 0, s, (double*)dst, n, value); break;
+    case MTHIP_I32: hipLaunchKernelGGL(fill_kernel<int32_t>, dim3(g), dim3(kThreads), 0, s, (int32_t*)dst, n, (int32_t)value); break;
+    case MTHIP_I64: hipLaunchKernelGGL(fill_kernel<int64_t>, dim3(g), dim3(kThreads), 0, s, (int64_t*)dst, n, (int64_t)value); break;
+    default: hipLaunchKernelGGL(fill_kernel<uint8_t>, dim3(g), dim3(kThreads), 0, s, (uint8_t*)dst, n, (uint8_t)(value != 0.0)); break;
+  }
+  return check_launch("mthip_fill");
+}
+
+int mthip_cat(int device, int dtype, int count, const void* const* inputs, const int64_t* dim_sizes, int rank,
+              const int64_t* out_sizes, int dim, void* out) {
+  const int es = elem_size(dtype);
+  MTHIP_REQUIRE(es != 0, "mthip_cat: unknown dtype");
+  MTHIP_REQUIRE(rank >= 1 && dim >= 0 && dim < rank, "mthip_cat: bad dim");
+  int64_t outer = 1, inner = 1, total = 0;
+  for (int d = 0; d < dim; ++d) outer *= out_sizes[d];
+  for (int d = dim + 1; d < rank; ++d) inner *= out_sizes[d];
+  for (int i = 0; i < count; ++i) total += dim_sizes[i];
+  MTHIP_REQUIRE(total == out_sizes[dim], "mthip_cat: input extents do not sum to the output extent");
+  hipStream_t s = stream_for(device);
+  if (!s) return MTHIP_ERR_HIP;
+  if (int rc = use_device(device)) return rc;
+  int64_t offset = 0;
+  for (int i = 0; i < count; ++i) {
+    const int64_t in_inner = dim_sizes[i] * inner;
+    const int64_t n = outer * in_inner;
+    if (n > 0) {
+      char* dst = (char*)out + offset * inner * es;
+      const unsigned g = grid_for(n);
+      switch (es) {
+        case 1: hipLaunchKernelGGL(copy_2d_kernel<uint8_t>, dim3(g), dim3(kThreads), 0, s, (const uint8_t*)inputs[i], (uint8_t*)dst, outer, in_inner, total * inner); break;
+        case 2: hipLaunchKernelGGL(copy_2d_kernel<uint16_t>, dim3(g), dim3(kThreads), 0, s, (const uint16_t*)inputs[i], (uint16_t*)dst, outer, in_inner, total * inner); break;
+        case 4: hipLaunchKernelGGL(copy_2d_kernel<uint32_t>, dim3(g), dim3(kThreads), 0, s, (const uint32_t*)inputs[i], (uint32_t*)dst, outer, in_inner, total * inner); break;
+        default: hipLaunchKernelGGL(copy_2d_kernel<uint64_t>, dim3(g), dim3(kThreads), 0, s, (const uint64_t*)inputs[i], (uint64_t*)dst, outer, in_inner, total * inner); break;
+      }
+      if (int rc = check_launch("mthip_cat")) return rc;
+    }
+    offset += dim_sizes[i];
+  }
+  return MTHIP_OK;
+}
+
+int mthip_upsample_nearest2d(int device, int dtype, const void* x, void* y, int64_t planes, int64_t H, int64_t W,
+                             int64_t scale_h, int64_t scale_w) {
+  const int es = elem_size(dtype);
+  MTHIP_REQUIRE(es == 2 || es == 4, "mthip_upsample_nearest2d: dtype must be F16 or F32");
+  MTHIP_REQUIRE(scale_h >= 1 && scale_w >= 1, "mthip_upsample_nearest2d: scale must be >= 1");
+  const int64_t n = planes * H * scale_h * W * scale_w;
+  if (n == 0) return MTHIP_OK;
+  hipStream_t s = stream_for(device);
+  if (!s) return MTHIP_ERR_HIP;
+  if (int rc = use_device(device)) return rc;
+  if (es == 2)
+    hipLaunchKernelGGL(upsample_nearest_kernel<uint16_t>, dim3(grid_for(n)), dim3(kThreads), 0, s, (const uint16_t*)x, (uint16_t*)y, planes, H, W, scale_h, scale_w);
+  else
+    hipLaunchKernelGGL(upsample_nearest_kernel<uint32_t>, dim3(grid_for(n)), dim3(kThreads), 0, s, (const uint32_t*)x, (uint32_t*)y, planes, H, W, scale_h, scale_w);
+  return check_launch("mthip_upsample_nearest2d");
+}
+
+int mthip_binary(int device, int op, int dtype, const void* a, const int64_t* a_strides, const void* b,
+                 const int64_t* b_strides, void* out, int rank, const int64_t* out_sizes) {
+  MTHIP_REQUIRE(dtype == MTHIP_F16 || dtype == MTHIP_F32, "mthip_binary: dtype must be F16 or F32");
+  MTHIP_REQUIRE(op >= MTHIP_BIN_ADD && op <= MTHIP_BIN_DIV, "mthip_binary: unknown op");
+  MTHIP_REQUIRE(rank >= 0 && rank <= kMaxRank, "mthip_binary: rank must be <= 8");
+  int64_t n = 1;
+  for (int d = 0; d < rank; ++d) n *= out_sizes[d];
+  if (n == 0) return MTHIP_OK;
+  hipStream_t s = stream_for(device);
+  if (!s) return MTHIP_ERR_HIP;
+  if (int rc = use_device(device)) return rc;
+  int64_t out_strides[kMaxRank];
+  {
+    int64_t acc = 1;
+    for (int d = rank - 1; d >= 0; --d) {
+      out_strides[d] = acc;
+      acc *= out_sizes[d];
+    }
+  }
+  Shape sh{};
+  int64_t o_str[kMaxRank];
+  int64_t* outs[3] = {sh.a_strides, sh.b_strides, o_str};
+  const int64_t* ins[3] = {a_strides, b_strides, out_strides};
+  sh.rank = collapse(rank, out_sizes, ins, 3, sh.sizes, outs);
+  const bool contig = sh.rank <= 1 && (sh.rank == 0 || (sh.a_strides[0] == 1 && sh.b_strides[0] == 1));
+  const unsigned g = grid_for(n);
+  if (contig) {
+    if (dtype == MTHIP_F16 && n % 8 == 0 && (uintptr_t)a % 16 == 0 && (uintptr_t)b % 16 == 0 && (uintptr_t)out % 16 == 0)
+      hipLaunchKernelGGL(binary_contig_h8_kernel, dim3(grid_for(n / 8)), dim3(kThreads), 0, s, op, (const uint4*)a, (const uint4*)b, (uint4*)out, n / 8);
+    else if (dtype == MTHIP_F16)
+      hipLaunchKernelGGL(binary_contig_kernel<uint16_t>, dim3(g), dim3(kThreads), 0, s, op, (const uint16_t*)a, (const uint16_t*)b, (uint16_t*)out, n);
+    else
+      hipLaunchKernelGGL(binary_contig_kernel<float>, dim3(g), dim3(kThreads), 0, s, op, (const float*)a, (const float*)b, (float*)out, n);
+  } else {
+    if (sh.rank == 0) sh.rank = 1, sh.sizes[0] = 1, sh.a_strides[0] = 0, sh.b_strides[0] = 0;
+    if (dtype == MTHIP_F16)
+      hipLaunchKernelGGL(binary_strided_kernel<uint16_t>, dim3(g), dim3(kThreads), 0, s, op, (const uint16_t*)a, (const uint16_t*)b, (uint16_t*)out, sh, n);
+    else
+      hipLaunchKernelGGL(binary_strided_kernel<float>, dim3(g), dim3(kThreads), 0, s, op, (const float*)a, (const float*)b, (float*)out, sh, n);
+  }
+  return check_launch("mthip_binary");
+}
+
+int mthip_binary_scalar(int device, int op, int dtype, const void* x, double scalar, int scalar_first, void* out,
+                        int64_t n) {
+  MTHIP_REQUIRE(dtype == MTHIP_F16 || dtype == MTHIP_F32, "mthip_binary_scalar: dtype must be F16 or F32");
+  MTHIP_REQUIRE(op >= MTHIP_BIN_ADD && op <= MTHIP_BIN_DIV, "mthip_binary_scalar: unknown op");
+  if (n <= 0) return MTHIP_OK;
+  hipStream_t s = stream_for(device);
+  if (!s) return MTHIP_ERR_HIP;
+  if (int rc = use_device(device)) return rc;
+  if (dtype == MTHIP_F16)
+    hipLaunchKernelGGL(binary_scalar_kernel<uint16_t>, dim3(grid_for(n)), dim3(kThreads), 0, s, op, (const uint16_t*)x, scalar, scalar_first, (uint16_t*)out, n);
+  else
+    hipLaunchKernelGGL(binary_scalar_kernel<float>, dim3(grid_for(n)), dim3(kThreads), 0, s, op, (const float*)x, scalar, scalar_first, (float*)out, n);
+  return check_launch("mthip_binary_scalar");
+}
+
+int mthip_unary(int device, int op, int dtype, const void* x, void* y, int64_t n) {
+  MTHIP_REQUIRE(dtype == MTHIP_F16 || dtype == MTHIP_F32, "mthip_unary: dtype must be F16 or F32");
+  MTHIP_REQUIRE(op >= MTHIP_UNARY_SILU && op <= MTHIP_UNARY_RELU, "mthip_unary: unknown op");
+  if (n <= 0) return MTHIP_OK;
+  hipStream_t s = stream_for(device);
+  if (!s) return MTHIP_ERR_HIP;
+  if (int rc = use_device(device)) return rc;
+  if (dtype == MTHIP_F16)
+    hipLaunchKernelGGL(unary_kernel<uint16_t>, dim3(grid_for(n)), dim3(kThreads), 0, s, op, (const uint16_t*)x, (uint16_t*)y, n);
+  else
+    hipLaunchKernelGGL(unary_kernel<float>, dim3(grid_for(n)), dim3(kThreads), 0, s, op, (const float*)x, (float*)y, n);
+  return check_launch("mthip_unary");
+}
+
+int mthip_geglu(int device, int dtype, const void* x, void* y, int64_t rows, int64_t D) {
+  MTHIP_REQUIRE(dtype == MTHIP_F16 || dtype == MTHIP_F32, "mthip_geglu: dtype must be F16 or F32");
+  const int64_t n = rows * D;
+  if (n <= 0) return MTHIP_OK;
+  hipStream_t s = stream_for(device);
+  if (!s) return MTHIP_ERR_HIP;
+  if (int rc = use_device(device)) return rc;
+  if (dtype == MTHIP_F16)
+    hipLaunchKernelGGL(geglu_kernel<uint16_t>, dim3(grid_for(n)), dim3(kThreads), 0, s, (const uint16_t*)x, (uint16_t*)y, rows, D);
+  else
+    hipLaunchKernelGGL(geglu_kernel<float>, dim3(grid_for(n)), dim3(kThreads), 0, s, (const float*)x, (float*)y, rows, D);
+  return check_launch("mthip_geglu");
+}
+
+}  // extern "C"

@@ -1,0 +1,424 @@
+"""GPU parity: every hot-path operator through libmthip's C ABI against the CPU oracle on the
+same seeded inputs.
+
+Tolerances: max |gpu - ref| / max |ref| <= 1e-4 for fp32 kernels and
+<= 1e-2 for fp16 kernels (fp32 accumulate); bit-exact for dtype casts, copies and metadata."""
+
+import os
+import sys
+
+import numpy as np
+import pytest
+
+import mtorch_amd as mt
+import oracle as orc
+
+pytestmark = pytest.mark.gpu
+HERE = os.path.dirname(__file__)
+sys.path.insert(0, os.path.join(HERE, "golden"))
+import closed_form  # noqa: E402
+
+F = mt.nn.functional
+TOL = {"float32": 1e-4, "float16": 1e-2}
+
+
+def rel(got, ref):
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    assert got.shape == ref.shape, (got.shape, ref.shape)
+    if got.size == 0:
+        return 0.0
+    assert np.array_equal(np.isnan(got), np.isnan(ref)), "NaN pattern differs"
+    m = ~np.isnan(ref)
+    return float(np.max(np.abs(got[m] - ref[m])) / max(np.max(np.abs(ref[m])), 1e-30)) if m.any() else 0.0
+
+
+class Gen:
+    """Seeded inputs from mtorch's generator (via the oracle) in a given dtype."""
+
+    def __init__(self, seed):
+        self.r = orc.Rng(seed)
+
+    def randn(self, shape, dt, std=1.0):
+        return self.r.randn(shape, dt, 0.0, std)
+
+
+def dev(a):
+    return mt.from_numpy(a, dtype=mt.float16 if a.dtype == np.uint16 else None).to("cuda")
+
+
+def host(t):
+    return t.cpu().half_bits() if t.dtype is mt.float16 else t.cpu().numpy()
+
+
+def val(a):
+    return orc.h2f(a) if a.dtype == np.uint16 else a
+
+
+@pytest.fixture(autouse=True)
+def _no_grad():
+    with mt.no_grad():
+        yield
+
+
+def test_device_visible():
+    assert mt.cuda.is_available()
+    name = mt.cuda.get_device_name(0)
+    assert "gfx950" in name, name
+
+
+# ------------------------------------------------------------------ data movement
+
+
+def test_cast_bit_exact():
+    rng = np.random.default_rng(3)
+    bits = rng.integers(0, 2**32, size=1 << 20, dtype=np.uint64).astype(np.uint32)
+    x = bits.view(np.float32)
+    t = mt.from_numpy(x).to("cuda")
+    got = t.to(mt.float16).cpu().half_bits()
+    assert np.array_equal(got, orc.f2h(x))
+    allh = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    back = mt.from_numpy(allh, dtype=mt.float16).to("cuda").to(mt.float32).cpu().numpy()
+    assert np.array_equal(back.view(np.uint32), orc.h2f(allh).view(np.uint32))
+    # odd sizes / offsets take the scalar path
+    sub = t[3:1000]
+    assert np.array_equal(sub.half().cpu().half_bits(), orc.f2h(x[3:1000]))
+
+
+def test_strided_copies_bit_exact():
+    rng = np.random.default_rng(4)
+    a = rng.standard_normal((3, 37, 5, 41)).astype(np.float32)
+    t = mt.from_numpy(a).to("cuda")
+    for perm in [(0, 2, 1, 3), (0, 1, 3, 2), (3, 2, 1, 0), (1, 0, 2, 3)]:
+        got = t.permute(*perm).contiguous().cpu().numpy()
+        assert np.array_equal(got, np.ascontiguousarray(a.transpose(perm)))
+    h = orc.f2h(a)
+    th = dev(h)
+    got = th.transpose(1, 2).contiguous().cpu().half_bits()
+    assert np.array_equal(got, np.ascontiguousarray(h.transpose(0, 2, 1, 3)))
+    assert np.array_equal(th[:, 5:20:3, :, ::2].contiguous().cpu().half_bits(), h[:, 5:20:3, :, ::2])
+
+
+def test_view_metadata_matches_reference_rules():
+    t = mt.zeros(2, 3, 4, device="cuda")
+    assert t.transpose(0, 2).stride() == (1, 4, 12)
+    r = t.transpose(1, 2).reshape(2, 12)  # not viewable -> copy, contiguous strides
+    assert r.stride() == (12, 1) and r.is_contiguous()
+    v = t.permute(0, 2, 1).unsqueeze(1)
+    assert v.shape == (2, 1, 4, 3) and v.stride() == (12, 4, 1, 4)
+    a, b = t.chunk(2, dim=-1)
+    assert a.shape == (2, 3, 2) and b.storage_offset() == 2 and b.stride() == (12, 4, 1)
+
+
+# ------------------------------------------------------------------ elementwise
+
+
+@pytest.mark.parametrize("dt", ["float32", "float16"])
+def test_binary_ops(dt):
+    g = Gen(11)
+    a = g.randn((4, 6, 9, 10), dt)
+    b = g.randn((4, 6, 9, 10), dt)
+    for op in ("add", "mul", "sub"):
+        got = host({"add": dev(a) + dev(b), "mul": dev(a) * dev(b), "sub": dev(a) - dev(b)}[op])
+        assert np.array_equal(got, orc.binary(a, b, op)), op  # same-shape ops are exact
+    # broadcasts: channel bias [1,6,1,1], time embedding [4,6,1,1], row [10]
+    for shape in [(1, 6, 1, 1), (4, 6, 1, 1), (10,), (9, 1)]:
+        c = g.randn(shape, dt)
+        got = host(dev(a) + dev(c))
+        ref = orc.binary(a, np.broadcast_to(c, a.shape), "add")
+        assert np.array_equal(got, ref), shape
+
+
+@pytest.mark.parametrize("dt", ["float32", "float16"])
+def test_activations(dt):
+    g = Gen(12)
+    x = g.randn((3, 1001), dt, 3.0)
+    for name, fn, ref in [("silu", F.silu, orc.silu(x)), ("gelu", F.gelu, orc.gelu(x)),
+                          ("gelu_tanh", lambda t: F.gelu(t, approximate="tanh"), orc.gelu(x, "tanh"))]:
+        got = host(fn(dev(x)))
+        assert rel(val(got), val(ref)) <= (2e-6 if dt == "float32" else 1e-3), name
+
+
+def test_geglu_matches_chunk_gelu_mul():
+    g = Gen(13)
+    x = g.randn((2, 17, 64), "float16", 2.0)
+    got = host(F.geglu(dev(x)))
+    a, gate = x[..., :32], x[..., 32:]
+    ref = orc.binary(np.ascontiguousarray(a), orc.gelu(np.ascontiguousarray(gate)), "mul")
+    assert rel(val(got), val(ref)) <= 1e-3
+
+
+def test_scalar_ops_and_unary_math():
+    g = Gen(14)
+    x = g.randn((1000,), "float32")
+    t = dev(x)
+    assert rel(host(t * 0.125), x.astype(np.float64) * 0.125) <= 1e-7
+    assert rel(host(2.0 - t), 2.0 - x.astype(np.float64)) <= 1e-7
+    assert rel(host(t.exp()), np.exp(x.astype(np.float64))) <= 1e-6
+    assert rel(host(t.sin()), np.sin(x.astype(np.float64))) <= 1e-6
+
+
+# ------------------------------------------------------------------ contractions
+
+
+@pytest.mark.parametrize("dt", ["float32", "float16"])
+@pytest.mark.parametrize("M,N,K", [(37, 23, 19), (128, 320, 320), (200, 130, 72), (2, 1280, 320), (64, 77, 768)])
+def test_linear(dt, M, N, K):
+    g = Gen(M * 7 + N)
+    x = g.randn((M, K), dt)
+    w = g.randn((N, K), dt, 1.0 / np.sqrt(K))
+    b = g.randn((N,), dt)
+    got = host(F.linear(dev(x), dev(w), dev(b)))
+    assert rel(val(got), val(orc.linear(x, w, b))) <= TOL[dt]
+
+
+@pytest.mark.parametrize("dt", ["float32", "float16"])
+def test_linear_fused_epilogues(dt):
+    g = Gen(21)
+    x = g.randn((3, 50, 96), dt)
+    w = g.randn((128, 96), dt, 0.1)
+    b = g.randn((128,), dt)
+    r = g.randn((3, 50, 128), dt)
+    lin = orc.linear(x, w, b)
+    got = host(F.linear_gelu(dev(x), dev(w), dev(b)))
+    assert rel(val(got), val(orc.gelu(lin))) <= TOL[dt]
+    got = host(F.linear_silu(dev(x), dev(w), dev(b)))
+    assert rel(val(got), val(orc.silu(lin))) <= TOL[dt]
+    got = host(F.linear_residual(dev(x), dev(w), dev(b), dev(r)))
+    assert rel(val(got), val(orc.binary(lin, r, "add"))) <= TOL[dt]
+
+
+def test_linear_strided_input_and_transposed_weight():
+    g = Gen(22)
+    x = g.randn((40, 2, 64), "float32")
+    w = g.randn((64, 48), "float32", 0.1)  # used as w.t()
+    xt = dev(x).transpose(0, 1)  # [2, 40, 64] non-contiguous
+    got = host(F.linear(xt, dev(w).t()))
+    ref = orc.linear(np.ascontiguousarray(x.transpose(1, 0, 2)), np.ascontiguousarray(w.T))
+    assert rel(got, ref) <= 1e-4
+
+
+@pytest.mark.parametrize("dt", ["float32", "float16"])
+def test_matmul_batched_broadcast_and_transposes(dt):
+    g = Gen(31)
+    a = g.randn((2, 3, 33, 20), dt)
+    b = g.randn((3, 20, 45), dt)
+    got = host(mt.matmul(dev(a), dev(b)))
+    ref = orc.matmul(a.reshape(6, 33, 20), np.broadcast_to(b[None], (2, 3, 20, 45)).reshape(6, 20, 45))
+    assert rel(val(got), val(ref.reshape(2, 3, 33, 45))) <= TOL[dt]
+    # attention-style: q @ k^T with k^T a transposed view
+    k = g.randn((3, 45, 20), dt)
+    got = host(mt.matmul(dev(a[0]), dev(k).transpose(-2, -1)))
+    ref = orc.matmul(a[0], np.ascontiguousarray(k.transpose(0, 2, 1)))
+    assert rel(val(got), val(ref)) <= TOL[dt]
+    v = g.randn((20,), dt)
+    got = host(mt.matmul(dev(a[0, 0]), dev(v)))
+    assert rel(val(got), val(orc.matmul(a[0, 0], v.reshape(20, 1)).reshape(33))) <= TOL[dt]
+
+
+@pytest.mark.parametrize("dt", ["float32", "float16"])
+def test_addmm_and_baddbmm(dt):
+    g = Gen(32)
+    inp = g.randn((40,), dt)
+    m1 = g.randn((25, 30), dt)
+    m2 = g.randn((30, 40), dt)
+    got = host(mt.addmm(dev(inp), dev(m1), dev(m2), beta=0.5, alpha=2.0))
+    assert rel(val(got), val(orc.addmm(inp, m1, m2, 0.5, 2.0))) <= TOL[dt]
+    bi = g.randn((4, 25, 40), dt)
+    b1 = g.randn((4, 25, 30), dt)
+    b2 = g.randn((4, 30, 40), dt)
+    got = host(mt.baddbmm(dev(bi), dev(b1), dev(b2), beta=1.0, alpha=0.25))
+    ref = np.stack([orc.addmm(bi[i], b1[i], b2[i], 1.0, 0.25) for i in range(4)])
+    assert rel(val(got), val(ref)) <= TOL[dt]
+
+
+CONV_CASES = [
+    dict(B=2, C=32, H=16, W=16, O=48, k=3, stride=1, padding=1, dilation=1, groups=1),
+    dict(B=1, C=40, H=15, W=13, O=24, k=3, stride=2, padding=1, dilation=1, groups=1),
+    dict(B=2, C=4, H=12, W=12, O=32, k=3, stride=1, padding=1, dilation=1, groups=1),
+    dict(B=2, C=32, H=9, W=11, O=4, k=3, stride=1, padding=1, dilation=1, groups=1),
+    dict(B=1, C=64, H=8, W=8, O=64, k=1, stride=1, padding=0, dilation=1, groups=1),
+    dict(B=1, C=12, H=10, W=10, O=8, k=3, stride=1, padding=2, dilation=2, groups=1),
+    dict(B=1, C=8, H=7, W=9, O=6, k=3, stride=1, padding=1, dilation=1, groups=2),
+]
+
+
+@pytest.mark.parametrize("dt", ["float32", "float16"])
+@pytest.mark.parametrize("cfg", CONV_CASES, ids=lambda c: f"C{c['C']}O{c['O']}k{c['k']}s{c['stride']}d{c['dilation']}g{c['groups']}")
+def test_conv2d(dt, cfg):
+    g = Gen(41 + cfg["C"])
+    x = g.randn((cfg["B"], cfg["C"], cfg["H"], cfg["W"]), dt)
+    w = g.randn((cfg["O"], cfg["C"] // cfg["groups"], cfg["k"], cfg["k"]), dt, 1.0 / np.sqrt(cfg["C"] * 9))
+    b = g.randn((cfg["O"],), dt)
+    kw = dict(stride=cfg["stride"], padding=cfg["padding"], dilation=cfg["dilation"], groups=cfg["groups"])
+    got = host(F.conv2d(dev(x), dev(w), dev(b), **kw))
+    assert rel(val(got), val(orc.conv2d(x, w, b, **kw))) <= TOL[dt]
+
+
+@pytest.mark.parametrize("dt", ["float32", "float16"])
+def test_conv2d_residual_epilogue(dt):
+    g = Gen(51)
+    x = g.randn((2, 16, 10, 10), dt)
+    w = g.randn((16, 16, 3, 3), dt, 0.1)
+    b = g.randn((16,), dt)
+    got = host(F.conv2d_residual(dev(x), dev(w), dev(b), dev(x), padding=1))
+    ref = orc.binary(x, orc.conv2d(x, w, b, padding=1), "add")
+    assert rel(val(got), val(ref)) <= TOL[dt]
+
+
+# ------------------------------------------------------------------ attention
+
+
+@pytest.mark.parametrize("dt", ["float16", "float32"])
+@pytest.mark.parametrize("Lq,Lk,E", [(256, 256, 40), (300, 77, 40), (130, 130, 80), (64, 200, 160), (33, 17, 64), (5, 9, 7)])
+def test_sdpa(dt, Lq, Lk, E):
+    g = Gen(Lq + Lk + E)
+    q = g.randn((2, 3, Lq, E), dt)
+    k = g.randn((2, 3, Lk, E), dt)
+    v = g.randn((2, 3, Lk, E), dt)
+    got = host(F.scaled_dot_product_attention(dev(q), dev(k), dev(v)))
+    assert rel(val(got), val(orc.sdpa(q, k, v))) <= TOL[dt]
+
+
+@pytest.mark.parametrize("dt", ["float16", "float32"])
+def test_sdpa_masks_causal_scale(dt):
+    g = Gen(61)
+    q = g.randn((2, 4, 70, 40), dt)
+    k = g.randn((2, 4, 90, 40), dt)
+    v = g.randn((2, 4, 90, 40), dt)
+    rng = np.random.default_rng(0)
+    bmask = rng.random((2, 1, 70, 90)) > 0.4
+    bmask[..., 0] = True
+    amask = (rng.standard_normal((70, 90)) * 2).astype(np.float32)
+    cases = [
+        dict(attn_mask=bmask, is_causal=False, scale=None),
+        dict(attn_mask=amask, is_causal=False, scale=0.2),
+        dict(attn_mask=None, is_causal=True, scale=None),
+        dict(attn_mask=bmask, is_causal=True, scale=0.3),
+    ]
+    for c in cases:
+        m = c["attn_mask"]
+        md = None if m is None else mt.from_numpy(m).to("cuda")
+        got = host(F.scaled_dot_product_attention(dev(q), dev(k), dev(v), attn_mask=md, is_causal=c["is_causal"],
+                                                  scale=c["scale"]))
+        ref = orc.sdpa(q, k, v, m, c["is_causal"], c["scale"])
+        assert rel(val(got), val(ref)) <= TOL[dt], c
+
+
+def test_sdpa_fully_masked_row_is_nan_and_gqa():
+    g = Gen(62)
+    q = g.randn((1, 4, 40, 40), "float16")
+    k = g.randn((1, 2, 50, 40), "float16")
+    v = g.randn((1, 2, 50, 40), "float16")
+    m = np.ones((40, 50), bool)
+    m[7, :] = False
+    out = host(F.scaled_dot_product_attention(dev(q), dev(k), dev(v), attn_mask=mt.from_numpy(m).to("cuda"),
+                                              enable_gqa=True))
+    kr = np.repeat(k, 2, axis=1)
+    vr = np.repeat(v, 2, axis=1)
+    ref = orc.sdpa(q, kr, vr, m)
+    assert rel(val(out), val(ref)) <= 1e-2
+
+
+def test_sd_cross_attention_scenario_fixture():
+    """Reference scenario tests/compat/test_tensor_ops.py:2105-2158 in fp16 on the GPU."""
+    c = closed_form.sd_cross_attention_inputs()
+    exp = np.load(os.path.join(HERE, "golden", "sd_cross_attention_2x64x77x320.npz"))["attended"]
+    h = lambda a: dev(orc.f2h(a))  # noqa: E731
+    q = F.linear(h(c["hidden"]), h(c["qw"]), h(c["bias"])).reshape(2, 64, 8, 40).transpose(1, 2).reshape(16, 64, 40)
+    k = F.linear(h(c["enc"]), h(c["kw"]), h(c["bias"])).reshape(2, 77, 8, 40).transpose(1, 2).reshape(16, 77, 40)
+    v = F.linear(h(c["enc"]), h(c["vw"]), h(c["bias"])).reshape(2, 77, 8, 40).transpose(1, 2).reshape(16, 77, 40)
+    att = F.scaled_dot_product_attention(q, k, v, attn_mask=mt.from_numpy(c["mask"]).to("cuda"), scale=0.125)
+    assert np.allclose(orc.h2f(host(att)), exp, rtol=4e-3, atol=4e-3)  # the reference test's tolerance
+
+
+# ------------------------------------------------------------------ normalisation / softmax
+
+
+@pytest.mark.parametrize("dt", ["float32", "float16"])
+@pytest.mark.parametrize("shape,groups", [((2, 64, 16, 16), 32), ((1, 40, 7, 9), 8), ((3, 32, 5), 4), ((2, 320, 64, 64), 32)])
+def test_group_norm(dt, shape, groups):
+    g = Gen(71 + shape[1])
+    x = g.randn(shape, dt)
+    w = g.randn((shape[1],), dt)
+    b = g.randn((shape[1],), dt)
+    got = host(F.group_norm(dev(x), groups, dev(w), dev(b), 1e-5))
+    ref = orc.group_norm(x, groups, w, b, 1e-5)
+    assert rel(val(got), val(ref)) <= TOL[dt]
+    got = host(F.group_norm_silu(dev(x), groups, dev(w), dev(b), 1e-5))
+    assert rel(val(got), val(orc.silu(ref))) <= TOL[dt]
+
+
+def test_sd_group_norm_scenario_fixture():
+    hidden, w, b = closed_form.sd_group_norm_inputs()
+    exp = np.load(os.path.join(HERE, "golden", "sd_group_norm_1x320x16x16.npz"))["y"]
+    got = host(F.group_norm(dev(orc.f2h(hidden)), 32, dev(orc.f2h(w)), dev(orc.f2h(b)), eps=1e-5))
+    assert np.allclose(orc.h2f(got), exp, rtol=3e-3, atol=3e-3)
+    got32 = host(F.group_norm(dev(hidden), 32, dev(w), dev(b), eps=1e-5))
+    assert np.allclose(got32, exp, rtol=1e-4, atol=1e-4)
+
+
+@pytest.mark.parametrize("dt", ["float32", "float16"])
+@pytest.mark.parametrize("rows,n", [(2048, 320), (77, 768), (50, 1280), (13, 3000), (9, 100)])
+def test_layer_norm(dt, rows, n):
+    g = Gen(81 + n)
+    x = g.randn((rows, n), dt, 2.0)
+    w = g.randn((n,), dt)
+    b = g.randn((n,), dt)
+    got = host(F.layer_norm(dev(x), (n,), dev(w), dev(b), 1e-5))
+    assert rel(val(got), val(orc.layer_norm(x, n, w, b, 1e-5))) <= TOL[dt]
+
+
+@pytest.mark.parametrize("dt", ["float32", "float16"])
+@pytest.mark.parametrize("shape", [(4, 3, 77), (64, 1024), (2, 5000), (3, 4, 4096), (7,)])
+def test_softmax(dt, shape):
+    g = Gen(91 + shape[-1])
+    x = g.randn(shape, dt, 3.0)
+    got = host(F.softmax(dev(x), dim=-1))
+    assert rel(val(got), val(orc.softmax_lastdim(x))) <= TOL[dt]
+
+
+def test_softmax_other_dim():
+    g = Gen(92)
+    x = g.randn((5, 6, 7), "float32")
+    got = host(F.softmax(dev(x), dim=1))
+    e = np.exp(x.astype(np.float64) - x.max(1, keepdims=True))
+    assert rel(got, e / e.sum(1, keepdims=True)) <= 1e-6
+
+
+# ------------------------------------------------------------------ glue + graphs
+
+
+def test_cat_and_upsample():
+    g = Gen(101)
+    a = g.randn((2, 3, 4, 5), "float16")
+    b = g.randn((2, 6, 4, 5), "float16")
+    got = host(mt.cat([dev(a), dev(b)], dim=1))
+    assert np.array_equal(got, np.concatenate([a, b], axis=1))
+    got = host(F.interpolate(dev(a), scale_factor=2, mode="nearest"))
+    assert np.array_equal(got, a.repeat(2, axis=2).repeat(2, axis=3))
+
+
+def test_graph_capture_replay_matches_eager():
+    g = Gen(111)
+    x = dev(g.randn((2, 32, 8, 8), "float16"))
+    w = dev(g.randn((32, 32, 3, 3), "float16", 0.05))
+    gamma = dev(g.randn((32,), "float16"))
+    beta = dev(g.randn((32,), "float16"))
+
+    def step():
+        h = F.group_norm_silu(x, 8, gamma, beta)
+        return F.conv2d_residual(h, w, None, x, padding=1)
+
+    eager = host(step())
+    step()  # warm the allocator cache so capture reuses blocks
+    graph = mt.cuda.CUDAGraph()
+    graph.capture_begin()
+    out = step()
+    graph.capture_end()
+    for _ in range(3):
+        graph.replay()
+        mt.cuda.synchronize()
+        assert np.array_equal(host(out), eager)
+        _ = host(step())  # eager work between replays
+    graph.reset()
