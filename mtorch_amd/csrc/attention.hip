@@ -1,19 +1,23 @@
 // scaled_dot_product_attention: flash-style fused kernel on MFMA (fp16) and a wave-per-query
 // kernel for fp32 and shapes outside the MFMA instances.
 //
-// MFMA kernel layout.  A workgroup is 4 wave64s; each wave owns 32 queries of one (batch, head).
-// Per 32-key tile it computes the transposed score block S^T = K . Q^T with
-// v_mfma_f32_32x32x16_f16, so lane l holds the scores of query (l % 32) against 16 keys in its
-// accumulator: the online-softmax max/sum of a query is an in-register reduction plus one
-// exchange with lane l^32.  Those same accumulator registers, converted to fp16, are exactly the
-// B operand of O^T += V^T . P^T (register r <-> key 8*(r/4) + 4*(l/32) + r%4 in both products),
-// so P never leaves registers.  K is staged in LDS row-major and V transposed (keys contiguous).
-// Softmax statistics and the output accumulator are fp32; fully masked rows end as 0/0 = NaN,
-// as the reference's softmax of an all -inf row does (tensor.cpp:30429-30442).
+// MFMA kernel layout.  A workgroup is 4 wave64s; each wave owns 32 queries of one (batch, head)
+// and the workgroup walks the keys in 64-key tiles.  Per 32-key half-tile a wave computes the
+// transposed score block S^T = K . Q^T with v_mfma_f32_32x32x16_f16, so lane l holds the scores
+// of query (l % 32) against 16 keys: a query's online-softmax max/sum is an in-register
+// reduction plus one exchange with lane l^32.  Those accumulator registers, converted to fp16,
+// are exactly the B operand of O^T += V^T . P^T (register r <-> key 8*(r/4) + 4*(l/32) + r%4 in
+// both products), so P never leaves registers.  K is staged in LDS row-major and V transposed
+// (keys contiguous); the next tile's K/V are fetched into registers with 16-byte range-checked
+// buffer loads while the current tile is multiplied.  Scores are kept in log2 units
+// (scale * log2 e folded in) so the exponentials are single v_exp_f32.  Softmax statistics and
+// the output accumulator are fp32; fully masked rows end as 0/0 = NaN, as the reference's
+// softmax of an all -inf row does (tensor.cpp:30429-30442).
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
 #include <cmath>
+#include <cstdlib>
 
 #include "common.h"
 
@@ -23,6 +27,8 @@ namespace {
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 typedef _Float16 halfx8 __attribute__((ext_vector_type(8)));
 typedef _Float16 halfx4 __attribute__((ext_vector_type(4)));
+
+constexpr float kLog2e = 1.4426950408889634f;
 
 struct FlashArgs {
   const void* q;
@@ -47,13 +53,31 @@ __device__ __forceinline__ float mask_value(const FlashArgs& a, int64_t b, int64
   return score + reinterpret_cast<const float*>(a.mask)[off];
 }
 
-template <int DK>
-__global__ __launch_bounds__(256) void flash_fwd_f16_kernel(const FlashArgs a) {
-  constexpr int NSTEP = DK / 16;          // K-dim MFMA steps of the score product
-  constexpr int DVB = (DK + 31) / 32;     // 32-row output blocks of O^T
-  constexpr int KP = DK + 8;              // LDS pitch of the K tile (halves)
-  constexpr int VP = 32 + 8;              // LDS pitch of the transposed V tile (halves)
-  __shared__ __align__(16) uint16_t Ks[32 * KP];
+__device__ __forceinline__ uint4 bload(const __amdgpu_buffer_rsrc_t& r, uint32_t off) {
+  return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
+}
+
+constexpr uint32_t kOOB = 0x80000000u;
+
+// DK: head dim padded to a multiple of 16 (QK^T K-steps); the value dim is covered by
+// DVB = ceil(DK/32) 32-row blocks.  VEC: E and Ev are multiples of 8 and every row stride a
+// multiple of 8 elements with 16-byte aligned bases, so K/V/Q move in 16-byte chunks.
+// MASK: the mask kind (MTHIP_MASK_*) fixed at compile time, or -1 to read it at run time.
+// WAVES: wave64s per workgroup (32 queries each); short sequences use fewer so more
+// workgroups spread over the CUs.
+template <int DK, bool VEC, int MASK, int WAVES>
+__global__ __launch_bounds__(64 * WAVES) void flash_fwd_f16_kernel(const FlashArgs a) {
+  constexpr int NT = 64 * WAVES;
+  constexpr int NSTEP = DK / 16;
+  constexpr int DVB = (DK + 31) / 32;
+  constexpr int BKV = 64;
+  constexpr int KP = DK + 8;    // LDS pitch of the K tile (halves)
+  constexpr int VP = BKV + 8;   // LDS pitch of the transposed V tile (halves)
+  constexpr int KCHR = DK / 8;  // 16-byte chunks per K row
+  constexpr int VCHR = DVB * 4; // 16-byte chunks per V row (DVB*32 dims)
+  constexpr int KCH = (BKV * KCHR + NT - 1) / NT;
+  constexpr int VCH = (BKV * VCHR + NT - 1) / NT;
+  __shared__ __align__(16) uint16_t Ks[BKV * KP];
   __shared__ __align__(16) uint16_t Vt[DVB * 32 * VP];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -61,7 +85,8 @@ __global__ __launch_bounds__(256) void flash_fwd_f16_kernel(const FlashArgs a) {
   const int64_t bh = blockIdx.y;
   const int64_t b = bh / a.H, head = bh - b * a.H;
   const int64_t kvh = head / (a.H / a.Hk);
-  const int64_t q = (int64_t)blockIdx.x * 128 + wave * 32 + col;
+  const int64_t q = (int64_t)blockIdx.x * (32 * WAVES) + wave * 32 + col;
+  const int Lk = (int)a.Lk, E = (int)a.E, Ev = (int)a.Ev;
   const uint16_t* Q = reinterpret_cast<const uint16_t*>(a.q) + b * a.qs[0] + head * a.qs[1];
   const uint16_t* K = reinterpret_cast<const uint16_t*>(a.k) + b * a.ks[0] + kvh * a.ks[1];
   const uint16_t* V = reinterpret_cast<const uint16_t*>(a.v) + b * a.vs[0] + kvh * a.vs[1];
@@ -70,14 +95,80 @@ __global__ __launch_bounds__(256) void flash_fwd_f16_kernel(const FlashArgs a) {
   halfx8 qf[NSTEP];
 #pragma unroll
   for (int st = 0; st < NSTEP; ++st) {
+    const int d0 = st * 16 + hh * 8;
+    if constexpr (VEC) {
+      uint4 r = make_uint4(0, 0, 0, 0);
+      if (q < a.Lq && d0 < E) r = *reinterpret_cast<const uint4*>(Q + q * a.qs[2] + d0);
+      qf[st] = __builtin_bit_cast(halfx8, r);
+    } else {
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int64_t d = st * 16 + hh * 8 + j;
-      uint16_t bits = 0;
-      if (q < a.Lq && d < a.E) bits = Q[q * a.qs[2] + d];
-      qf[st][j] = __builtin_bit_cast(_Float16, bits);
+      for (int j = 0; j < 8; ++j) {
+        uint16_t bits = 0;
+        if (q < a.Lq && d0 + j < E) bits = Q[q * a.qs[2] + d0 + j];
+        qf[st][j] = __builtin_bit_cast(_Float16, bits);
+      }
     }
   }
+
+  // K/V staging: chunk c of this thread covers row (c / CHR) and dims 8*(c % CHR) of the tile.
+  const __amdgpu_buffer_rsrc_t k_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)K, (short)0, (int)(((int64_t)(Lk > 0 ? Lk - 1 : 0) * a.ks[2] + E) * 2), 0x00020000);
+  const __amdgpu_buffer_rsrc_t v_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)V, (short)0, (int)(((int64_t)(Lk > 0 ? Lk - 1 : 0) * a.vs[2] + Ev) * 2), 0x00020000);
+  uint4 kreg[KCH], vreg[VCH];
+  auto fetch = [&](int kv0) {
+    if constexpr (VEC) {
+#pragma unroll
+      for (int i = 0; i < KCH; ++i) {
+        const int c = tid + i * NT;
+        const int key = c / KCHR, d0 = (c % KCHR) * 8;
+        const bool ok = c < BKV * KCHR && kv0 + key < Lk && d0 < E;
+        kreg[i] = bload(k_rsrc, ok ? (uint32_t)(((int64_t)(kv0 + key) * a.ks[2] + d0) * 2) : kOOB);
+      }
+      // V chunks go key-fastest across lanes so the transposed LDS writes below hit
+      // consecutive addresses (d-fastest lanes would land 2*VP bytes apart: same banks).
+#pragma unroll
+      for (int i = 0; i < VCH; ++i) {
+        const int c = tid + i * NT;
+        const int key = c % BKV, d0 = (c / BKV) * 8;
+        const bool ok = c < BKV * VCHR && kv0 + key < Lk && d0 < Ev;
+        vreg[i] = bload(v_rsrc, ok ? (uint32_t)(((int64_t)(kv0 + key) * a.vs[2] + d0) * 2) : kOOB);
+      }
+    }
+  };
+  auto stage = [&](int kv0) {
+    if constexpr (VEC) {
+#pragma unroll
+      for (int i = 0; i < KCH; ++i) {
+        const int c = tid + i * NT;
+        if (c < BKV * KCHR) *reinterpret_cast<uint4*>(&Ks[(c / KCHR) * KP + (c % KCHR) * 8]) = kreg[i];
+      }
+#pragma unroll
+      for (int i = 0; i < VCH; ++i) {
+        const int c = tid + i * NT;
+        if (c < BKV * VCHR) {
+          const int key = c % BKV, d0 = (c / BKV) * 8;
+          uint16_t h[8];
+          __builtin_memcpy(h, &vreg[i], 16);
+#pragma unroll
+          for (int j = 0; j < 8; ++j) Vt[(d0 + j) * VP + key] = h[j];
+        }
+      }
+    } else {
+      for (int idx = tid; idx < BKV * DK; idx += NT) {
+        const int key = idx / DK, d = idx - key * DK;
+        uint16_t bits = 0;
+        if (kv0 + key < Lk && d < E) bits = K[(int64_t)(kv0 + key) * a.ks[2] + d];
+        Ks[key * KP + d] = bits;
+      }
+      for (int idx = tid; idx < BKV * DVB * 32; idx += NT) {
+        const int key = idx / (DVB * 32), d = idx - key * (DVB * 32);
+        uint16_t bits = 0;
+        if (kv0 + key < Lk && d < Ev) bits = V[(int64_t)(kv0 + key) * a.vs[2] + d];
+        Vt[d * VP + key] = bits;
+      }
+    }
+  };
 
   floatx16 acc[DVB];
 #pragma unroll
@@ -85,60 +176,73 @@ __global__ __launch_bounds__(256) void flash_fwd_f16_kernel(const FlashArgs a) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[i][r] = 0.0f;
   float m_run = -INFINITY, l_run = 0.0f;
-  const float log2e = 1.4426950408889634f;
+  const float sl2 = a.scale * kLog2e;
+  const bool qok = q < a.Lq;
+  const int mask_kind = MASK >= 0 ? MASK : a.mask_kind;
+  // This lane's mask row (query q of head `head`), addressed per key by one 32-bit multiply.
+  const uint8_t* mrow_b = nullptr;
+  const uint16_t* mrow_h = nullptr;
+  const float* mrow_f = nullptr;
+  const int mk = (int)a.ms[3];
+  if (mask_kind != MTHIP_MASK_NONE && qok) {
+    const int64_t off = b * a.ms[0] + head * a.ms[1] + q * a.ms[2];
+    if (mask_kind == MTHIP_MASK_BOOL)
+      mrow_b = reinterpret_cast<const uint8_t*>(a.mask) + off;
+    else if (a.mask_dtype == MTHIP_F16)
+      mrow_h = reinterpret_cast<const uint16_t*>(a.mask) + off;
+    else
+      mrow_f = reinterpret_cast<const float*>(a.mask) + off;
+  }
 
-  for (int64_t kv0 = 0; kv0 < a.Lk; kv0 += 32) {
-    __syncthreads();  // the previous tile has been consumed by every wave
-    // Stage K[kv0 .. kv0+32) -> Ks[key][d] (zero beyond Lk / E).
-    for (int idx = tid; idx < 32 * DK; idx += 256) {
-      const int key = idx / DK, d = idx - key * DK;
-      uint16_t bits = 0;
-      if (kv0 + key < a.Lk && d < a.E) bits = K[(kv0 + key) * a.ks[2] + d];
-      Ks[key * KP + d] = bits;
-    }
-    // Stage V transposed -> Vt[d][key].
-    for (int idx = tid; idx < 32 * DVB * 32; idx += 256) {
-      const int key = idx / (DVB * 32), d = idx - key * (DVB * 32);
-      uint16_t bits = 0;
-      if (kv0 + key < a.Lk && d < a.Ev) bits = V[(kv0 + key) * a.vs[2] + d];
-      Vt[d * VP + key] = bits;
-    }
+  fetch(0);
+  for (int kv0 = 0; kv0 < Lk; kv0 += BKV) {
+    __syncthreads();  // every wave is done with the previous tile
+    stage(kv0);
     __syncthreads();
+    if (kv0 + BKV < Lk) fetch(kv0 + BKV);  // next tile's loads overlap this tile's math
 
-    floatx16 s;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) s[r] = 0.0f;
-#pragma unroll
-    for (int st = 0; st < NSTEP; ++st) {
-      const halfx8 kf = *reinterpret_cast<const halfx8*>(&Ks[col * KP + st * 16 + hh * 8]);
-      s = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[st], s, 0, 0, 0);
-    }
-
-    // Scale, causal, mask, key bounds; tile max of this query.
+    float s[2][16];
     float mx = -INFINITY;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int64_t key = kv0 + 8 * (r >> 2) + 4 * hh + (r & 3);
-      float v = s[r] * a.scale;
-      if (key >= a.Lk) {
-        v = -INFINITY;
-      } else {
-        if (a.causal && key > q) v = -INFINITY;
-        if (q < a.Lq) v = mask_value(a, b, head, q, key, v);
+    for (int sb = 0; sb < 2; ++sb) {
+      floatx16 t;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) t[r] = 0.0f;
+#pragma unroll
+      for (int st = 0; st < NSTEP; ++st) {
+        const halfx8 kf = *reinterpret_cast<const halfx8*>(&Ks[(sb * 32 + col) * KP + st * 16 + hh * 8]);
+        t = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[st], t, 0, 0, 0);
       }
-      s[r] = v;
-      mx = fmaxf(mx, v);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int key = kv0 + sb * 32 + 8 * (r >> 2) + 4 * hh + (r & 3);
+        float v = t[r] * sl2;
+        if (key >= Lk) {
+          v = -INFINITY;
+        } else {
+          if (a.causal && key > q) v = -INFINITY;
+          if (mask_kind == MTHIP_MASK_BOOL) {
+            if (qok && !mrow_b[key * mk]) v = -INFINITY;
+          } else if (mask_kind == MTHIP_MASK_ADD && qok) {
+            v += (mrow_h ? h2f_bits(mrow_h[key * mk]) : mrow_f[key * mk]) * kLog2e;
+          }
+        }
+        s[sb][r] = v;
+        mx = fmaxf(mx, v);
+      }
     }
     mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
     const float m_new = fmaxf(m_run, mx);
     const float m_use = m_new == -INFINITY ? 0.0f : m_new;
-    const float alpha = exp2f((m_run - m_use) * log2e);
+    const float alpha = exp2f(m_run - m_use);
     float psum = 0.0f;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      s[r] = exp2f((s[r] - m_use) * log2e);
-      psum += s[r];
-    }
+    for (int sb = 0; sb < 2; ++sb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        s[sb][r] = exp2f(s[sb][r] - m_use);
+        psum += s[sb][r];
+      }
     psum += __shfl_xor(psum, 32, 64);
     l_run = l_run * alpha + psum;
     m_run = m_new;
@@ -147,32 +251,47 @@ __global__ __launch_bounds__(256) void flash_fwd_f16_kernel(const FlashArgs a) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][r] *= alpha;
 
-    // O^T += V^T . P^T over two 16-key steps.
+    // O^T += V^T . P^T, four 16-key steps.
 #pragma unroll
-    for (int st = 0; st < 2; ++st) {
-      halfx8 pf;
+    for (int sb = 0; sb < 2; ++sb) {
 #pragma unroll
-      for (int j = 0; j < 8; ++j) pf[j] = (_Float16)s[st * 8 + j];
+      for (int st = 0; st < 2; ++st) {
+        halfx8 pf;
 #pragma unroll
-      for (int i = 0; i < DVB; ++i) {
-        const uint16_t* vrow = &Vt[(i * 32 + col) * VP + st * 16 + hh * 4];
-        const halfx4 lo = *reinterpret_cast<const halfx4*>(vrow);
-        const halfx4 hi = *reinterpret_cast<const halfx4*>(vrow + 8);
-        const halfx8 vf = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-        acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf, acc[i], 0, 0, 0);
+        for (int j = 0; j < 8; ++j) pf[j] = (_Float16)s[sb][st * 8 + j];
+#pragma unroll
+        for (int i = 0; i < DVB; ++i) {
+          const uint16_t* vrow = &Vt[(i * 32 + col) * VP + sb * 32 + st * 16 + hh * 4];
+          const halfx4 lo = *reinterpret_cast<const halfx4*>(vrow);
+          const halfx4 hi = *reinterpret_cast<const halfx4*>(vrow + 8);
+          const halfx8 vf = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+          acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf, acc[i], 0, 0, 0);
+        }
       }
     }
   }
 
-  if (q >= a.Lq) return;
+  if (!qok) return;
   uint16_t* O = reinterpret_cast<uint16_t*>(a.o) + (bh * a.Lq + q) * a.Ev;
   const float inv_l = 1.0f / l_run;
+  const bool zero_l = l_run == 0.0f;  // fully masked row: 0/0 = NaN like the reference
 #pragma unroll
   for (int i = 0; i < DVB; ++i)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int64_t d = i * 32 + 8 * (r >> 2) + 4 * hh + (r & 3);
-      if (d < a.Ev) O[d] = f2h_bits(l_run == 0.0f ? acc[i][r] / l_run : acc[i][r] * inv_l);
+    for (int g = 0; g < 4; ++g) {
+      const int d0 = i * 32 + 8 * g + 4 * hh;
+      if (d0 >= Ev) continue;
+      float v[4];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) v[t] = zero_l ? acc[i][4 * g + t] / l_run : acc[i][4 * g + t] * inv_l;
+      if (d0 + 4 <= Ev && ((((uintptr_t)(O + d0)) & 7) == 0)) {
+        uint2 u;
+        u.x = (uint32_t)f2h_fast(v[0]) | ((uint32_t)f2h_fast(v[1]) << 16);
+        u.y = (uint32_t)f2h_fast(v[2]) | ((uint32_t)f2h_fast(v[3]) << 16);
+        *reinterpret_cast<uint2*>(O + d0) = u;
+      } else {
+        for (int t = 0; t < 4 && d0 + t < Ev; ++t) O[d0 + t] = f2h_fast(v[t]);
+      }
     }
 }
 
@@ -228,6 +347,45 @@ __global__ __launch_bounds__(256) void attention_rowwise_kernel(const FlashArgs 
   }
 }
 
+template <int DK, int WAVES>
+void launch_flash_w(const FlashArgs& a, int64_t bh, hipStream_t s, bool vec) {
+  const dim3 grid((unsigned)ceil_div(a.Lq, 32 * WAVES), (unsigned)bh);
+  const dim3 block(64 * WAVES);
+  if (!vec) {
+    hipLaunchKernelGGL((flash_fwd_f16_kernel<DK, false, -1, WAVES>), grid, block, 0, s, a);
+  } else if (a.mask_kind == MTHIP_MASK_NONE) {
+    hipLaunchKernelGGL((flash_fwd_f16_kernel<DK, true, MTHIP_MASK_NONE, WAVES>), grid, block, 0, s, a);
+  } else if (a.mask_kind == MTHIP_MASK_BOOL) {
+    hipLaunchKernelGGL((flash_fwd_f16_kernel<DK, true, MTHIP_MASK_BOOL, WAVES>), grid, block, 0, s, a);
+  } else {
+    hipLaunchKernelGGL((flash_fwd_f16_kernel<DK, true, MTHIP_MASK_ADD, WAVES>), grid, block, 0, s, a);
+  }
+}
+
+// 4 waves (128 queries) per workgroup when that gives at least one workgroup per CU,
+// otherwise two waves so short sequences spread over twice as many workgroups.  (A single
+// wave per workgroup stages the whole K/V tile alone and needs more registers than the
+// extra workgroups win back.)
+// MTHIP_FLASH_WAVES=2|4 overrides the choice (for tuning).
+int flash_waves_override() {
+  static const int v = [] {
+    const char* e = std::getenv("MTHIP_FLASH_WAVES");
+    return e ? std::atoi(e) : 0;
+  }();
+  return v;
+}
+
+template <int DK>
+void launch_flash(const FlashArgs& a, int64_t bh, hipStream_t s, bool vec) {
+  const int forced = flash_waves_override();
+  if (forced == 4 || (forced != 2 && ceil_div(a.Lq, 128) * bh >= 256))
+    launch_flash_w<DK, 4>(a, bh, s, vec);
+  else
+    launch_flash_w<DK, 2>(a, bh, s, vec);
+}
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
 }  // namespace
 }  // namespace mthip
 
@@ -275,28 +433,28 @@ extern "C" int mthip_sdpa(int device, int dtype, const void* q, const int64_t* q
   a.causal = is_causal;
   a.scale = (float)(scale > 0.0 ? scale : 1.0 / std::sqrt((double)E));
   const int64_t bh = B * H;
-  if (dtype == MTHIP_F16 && Lk > 0) {
-    const int64_t dmax = std::max(E, Ev);
-    dim3 grid((unsigned)ceil_div(Lq, 128), (unsigned)bh);
-    bool launched = true;
+  const int64_t dmax = std::max(E, Ev);
+  // One head's K and V must be addressable by 32-bit buffer offsets.
+  const bool small_heads = ((Lk > 0 ? Lk - 1 : 0) * std::max(ks[2], vs[2]) + dmax) * 2 < (int64_t(1) << 31);
+  if (dtype == MTHIP_F16 && Lk > 0 && dmax <= 160 && small_heads) {
+    const bool vec = E % 8 == 0 && Ev % 8 == 0 && qs[2] % 8 == 0 && ks[2] % 8 == 0 && vs[2] % 8 == 0 &&
+                     qs[0] % 8 == 0 && qs[1] % 8 == 0 && ks[0] % 8 == 0 && ks[1] % 8 == 0 && vs[0] % 8 == 0 &&
+                     vs[1] % 8 == 0 && aligned16(q) && aligned16(k) && aligned16(v);
     if (dmax <= 32)
-      hipLaunchKernelGGL(flash_fwd_f16_kernel<32>, grid, dim3(256), 0, s, a);
+      launch_flash<32>(a, bh, s, vec);
     else if (dmax <= 48)
-      hipLaunchKernelGGL(flash_fwd_f16_kernel<48>, grid, dim3(256), 0, s, a);
+      launch_flash<48>(a, bh, s, vec);
     else if (dmax <= 64)
-      hipLaunchKernelGGL(flash_fwd_f16_kernel<64>, grid, dim3(256), 0, s, a);
+      launch_flash<64>(a, bh, s, vec);
     else if (dmax <= 80)
-      hipLaunchKernelGGL(flash_fwd_f16_kernel<80>, grid, dim3(256), 0, s, a);
+      launch_flash<80>(a, bh, s, vec);
     else if (dmax <= 128)
-      hipLaunchKernelGGL(flash_fwd_f16_kernel<128>, grid, dim3(256), 0, s, a);
-    else if (dmax <= 160)
-      hipLaunchKernelGGL(flash_fwd_f16_kernel<160>, grid, dim3(256), 0, s, a);
+      launch_flash<128>(a, bh, s, vec);
     else
-      launched = false;
-    if (launched) return check_launch("flash_fwd_f16_kernel");
+      launch_flash<160>(a, bh, s, vec);
+    return check_launch("flash_fwd_f16_kernel");
   }
   dim3 grid((unsigned)ceil_div(Lq, 4), (unsigned)bh);
-  const int64_t dmax = std::max(E, Ev);
   if (dtype == MTHIP_F16) {
     if (dmax <= 64)
       hipLaunchKernelGGL((attention_rowwise_kernel<uint16_t, 1>), grid, dim3(256), 0, s, a);

@@ -67,6 +67,22 @@ __device__ __forceinline__ uint16_t f2h_bits(float value) {
   return (uint16_t)(sign | (rounded >= 0x7c00u ? 0x7c00u : rounded));
 }
 
+// Same rounding rule as f2h_bits, cheaper for the common case.  In the normal half range
+// (biased float exponent 113..142) the hardware conversion rounds to nearest-even; it differs
+// from half-away-from-zero only on exact ties whose kept LSB is 0 (discarded bits == 0x1000
+// with bit 13 clear), where one ulp is added to the magnitude.  Everything else (subnormal
+// halves, overflow, inf/NaN) takes the integer restatement.
+__device__ __forceinline__ uint16_t f2h_fast(float value) {
+  const uint32_t bits = __float_as_uint(value);
+  const uint32_t e = (bits >> 23) & 0xffu;
+  if (e - 113u <= 29u) {
+    uint16_t h = __builtin_bit_cast(uint16_t, (_Float16)value);
+    h += (uint16_t)((bits & 0x3fffu) == 0x1000u);
+    return h;
+  }
+  return f2h_bits(value);
+}
+
 // Exact widening; finite values and infinities match tensor.cpp:317-344 bit for bit.
 __device__ __forceinline__ float h2f_bits(uint16_t h) {
   return (float)__builtin_bit_cast(_Float16, h);
@@ -95,8 +111,8 @@ struct Elem<float> {
 template <>
 struct Elem<uint16_t> {
   static __device__ __forceinline__ float load(const uint16_t* p, int64_t i) { return h2f_bits(p[i]); }
-  static __device__ __forceinline__ void store(uint16_t* p, int64_t i, float v) { p[i] = f2h_bits(v); }
-  static __device__ __forceinline__ float round_trip(float v) { return h2f_bits(f2h_bits(v)); }
+  static __device__ __forceinline__ void store(uint16_t* p, int64_t i, float v) { p[i] = f2h_fast(v); }
+  static __device__ __forceinline__ float round_trip(float v) { return h2f_bits(f2h_fast(v)); }
 };
 
 }  // namespace mthip

@@ -151,7 +151,12 @@ int run_conv(int device, int dtype, const void* x, const void* w, const void* b,
     a.dh = dh;
     a.dw = dw;
     a.vec_ok = 1;  // packed buffers: rows are whole chunks, bases come from the allocator
-    rc = launch_conv_gemm(dtype, a, s);
+    a.a_bytes = O * K * (int64_t)sizeof(T);
+    a.b_bytes = B * HW * Cp * (int64_t)sizeof(T);
+    if (a.a_bytes >= (int64_t(1) << 31) || a.b_bytes >= (int64_t(1) << 31))
+      rc = fail(MTHIP_ERR_UNSUPPORTED, "mthip_conv2d: operands above 2 GiB are not supported");
+    else
+      rc = launch_conv_gemm(dtype, a, s);
   }
   // Stream-ordered frees: the blocks are only reused by work enqueued after this conv.
   mthip_free(device, xp);

@@ -90,10 +90,10 @@ __global__ void cast_f32_f16_kernel(const float* __restrict__ src, uint16_t* __r
     const float4 a = reinterpret_cast<const float4*>(src)[2 * v];
     const float4 b = reinterpret_cast<const float4*>(src)[2 * v + 1];
     uint4 out;
-    out.x = (uint32_t)f2h_bits(a.x) | ((uint32_t)f2h_bits(a.y) << 16);
-    out.y = (uint32_t)f2h_bits(a.z) | ((uint32_t)f2h_bits(a.w) << 16);
-    out.z = (uint32_t)f2h_bits(b.x) | ((uint32_t)f2h_bits(b.y) << 16);
-    out.w = (uint32_t)f2h_bits(b.z) | ((uint32_t)f2h_bits(b.w) << 16);
+    out.x = (uint32_t)f2h_fast(a.x) | ((uint32_t)f2h_fast(a.y) << 16);
+    out.y = (uint32_t)f2h_fast(a.z) | ((uint32_t)f2h_fast(a.w) << 16);
+    out.z = (uint32_t)f2h_fast(b.x) | ((uint32_t)f2h_fast(b.y) << 16);
+    out.w = (uint32_t)f2h_fast(b.z) | ((uint32_t)f2h_fast(b.w) << 16);
     reinterpret_cast<uint4*>(dst)[v] = out;
   }
   for (int64_t i = nvec * 8 + (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)

@@ -2,6 +2,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cstdlib>
 
 #include "gemm_core.h"
 
@@ -13,6 +14,11 @@ namespace {
 enum TileKind { T128x128, T128x64, T64x128, T64x64 };
 
 TileKind pick_tile(int64_t M, int64_t N, int64_t batch) {
+  // MTHIP_GEMM_TILE=0..3 forces a tile shape (tuning sweeps); unset selects by problem size.
+  if (const char* force = std::getenv("MTHIP_GEMM_TILE")) {
+    const int t = std::atoi(force);
+    if (t >= 0 && t <= 3) return static_cast<TileKind>(t);
+  }
   auto tiles = [&](int64_t bm, int64_t bn) { return ceil_div(M, bm) * ceil_div(N, bn) * batch; };
   if (tiles(128, 128) >= 256) return T128x128;
   if (tiles(128, 64) >= 256) return N <= 64 || M >= N ? T128x64 : T64x128;
@@ -20,43 +26,78 @@ TileKind pick_tile(int64_t M, int64_t N, int64_t batch) {
   return T64x64;
 }
 
-template <typename T, int MODE, int EPI>
-int launch_gemm(const GemmArgs& a, int64_t batch, hipStream_t s) {
+template <typename T, int MODE, int EPI, bool FAST>
+int launch_gemm_fast(const GemmArgs& a, int64_t batch, hipStream_t s) {
   const TileKind tk = pick_tile(a.M, a.N, batch);
-  constexpr int BK = sizeof(T) == 2 ? 32 : 16;
   auto grid = [&](int bm, int bn) {
     return dim3((unsigned)ceil_div(a.N, bn), (unsigned)ceil_div(a.M, bm), (unsigned)batch);
   };
   MTHIP_REQUIRE(batch <= 65535, "gemm: batch must be <= 65535");
+  MTHIP_REQUIRE(ceil_div(a.M, 64) <= 65535, "gemm: M too large");
   switch (tk) {
     case T128x128:
-      MTHIP_REQUIRE(ceil_div(a.M, 128) <= 65535, "gemm: M too large");
-      hipLaunchKernelGGL((gemm_kernel<T, 128, 128, BK, 2, MODE, EPI>), grid(128, 128), dim3(256), 0, s, a);
+      hipLaunchKernelGGL((gemm_kernel<T, 128, 128, 2, MODE, EPI, FAST>), grid(128, 128), dim3(256), 0, s, a);
       break;
     case T128x64:
-      MTHIP_REQUIRE(ceil_div(a.M, 128) <= 65535, "gemm: M too large");
-      hipLaunchKernelGGL((gemm_kernel<T, 128, 64, BK, 2, MODE, EPI>), grid(128, 64), dim3(256), 0, s, a);
+      hipLaunchKernelGGL((gemm_kernel<T, 128, 64, 2, MODE, EPI, FAST>), grid(128, 64), dim3(256), 0, s, a);
       break;
     case T64x128:
-      MTHIP_REQUIRE(ceil_div(a.M, 64) <= 65535, "gemm: M too large");
-      hipLaunchKernelGGL((gemm_kernel<T, 64, 128, BK, 2, MODE, EPI>), grid(64, 128), dim3(256), 0, s, a);
+      hipLaunchKernelGGL((gemm_kernel<T, 64, 128, 2, MODE, EPI, FAST>), grid(64, 128), dim3(256), 0, s, a);
       break;
     default:
-      MTHIP_REQUIRE(ceil_div(a.M, 64) <= 65535, "gemm: M too large");
-      hipLaunchKernelGGL((gemm_kernel<T, 64, 64, BK, 2, MODE, EPI>), grid(64, 64), dim3(256), 0, s, a);
+      hipLaunchKernelGGL((gemm_kernel<T, 64, 64, 2, MODE, EPI, FAST>), grid(64, 64), dim3(256), 0, s, a);
       break;
   }
   return check_launch("gemm_kernel");
 }
 
+template <typename T, int MODE, int EPI>
+int launch_gemm(const GemmArgs& a, int64_t batch, hipStream_t s) {
+  return launch_gemm_fast<T, MODE, EPI, false>(a, batch, s);
+}
+
 bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+// dst[b][r][c] = c < cols ? src[b*sbs + r*lds + c] : 0 for c < ldd: stages an operand whose
+// rows are not whole 16-byte chunks into a zero-padded, aligned copy.
+template <typename T>
+__global__ void pad_rows_kernel(const T* __restrict__ src, T* __restrict__ dst, int64_t rows, int64_t cols,
+                                int64_t lds, int64_t sbs, int64_t ldd) {
+  const int64_t b = blockIdx.y;
+  const int64_t n = rows * ldd;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+    const int64_t r = i / ldd, c = i - r * ldd;
+    dst[b * n + i] = c < cols ? src[b * sbs + r * lds + c] : T(0);
+  }
+}
+
+// Stages `rows x cols` (row stride lds, batch stride sbs, `batches` copies) into a fresh
+// buffer with rows padded to `ldd` elements.  Returns 0 and the buffer (owned by the caller).
+template <typename T>
+int pad_operand(int device, hipStream_t s, const void* src, int64_t batches, int64_t rows, int64_t cols, int64_t lds,
+                int64_t sbs, int64_t ldd, void** out) {
+  if (int rc = mthip_malloc(device, (size_t)(batches * rows * ldd) * sizeof(T), out)) return rc;
+  const int64_t n = rows * ldd;
+  const unsigned g = (unsigned)std::min<int64_t>(std::max<int64_t>(ceil_div(n, 256), 1), 2048);
+  hipLaunchKernelGGL(pad_rows_kernel<T>, dim3(g, (unsigned)batches), dim3(256), 0, s, (const T*)src, (T*)*out, rows,
+                     cols, lds, sbs, ldd);
+  return check_launch("pad_rows_kernel");
+}
+
+constexpr int64_t kMaxBufferBytes = (int64_t(1) << 31) - 1;
 
 }  // namespace
 
 // Shared with conv.hip.
 int launch_conv_gemm(int dtype, const GemmArgs& a, hipStream_t s) {
-  if (dtype == MTHIP_F16) return launch_gemm<uint16_t, MODE_CONV, EPI_CONV>(a, 1, s);
-  return launch_gemm<float, MODE_CONV, EPI_CONV>(a, 1, s);
+  // With the padded channel count a multiple of BK, no K tile straddles two filter taps.
+  if (dtype == MTHIP_F16) {
+    if (a.Cp % Mfma<uint16_t>::BK == 0) return launch_gemm_fast<uint16_t, MODE_CONV, EPI_CONV, true>(a, 1, s);
+    return launch_gemm_fast<uint16_t, MODE_CONV, EPI_CONV, false>(a, 1, s);
+  }
+  if (a.Cp % Mfma<float>::BK == 0) return launch_gemm_fast<float, MODE_CONV, EPI_CONV, true>(a, 1, s);
+  return launch_gemm_fast<float, MODE_CONV, EPI_CONV, false>(a, 1, s);
 }
 
 }  // namespace mthip
@@ -91,13 +132,40 @@ int mthip_linear(int device, int dtype, const void* x, int64_t lda, const void* 
   a.residual = residual;
   a.ld_res = ld_res;
   const int vec = dtype == MTHIP_F16 ? 8 : 4;
-  a.vec_ok = aligned16(x) && aligned16(w) && lda % vec == 0 && ldw % vec == 0;
-  if (K == 0) {
-    // Empty reduction: the reference still adds the bias (and applies the tail ops).
-    a.K = 0;
+  const int64_t es = dtype == MTHIP_F16 ? 2 : 4;
+  const bool vec_ok = aligned16(x) && aligned16(w) && lda % vec == 0 && ldw % vec == 0 && K % vec == 0;
+  void* xp = nullptr;
+  void* wp = nullptr;
+  if (!vec_ok) {
+    // Zero-padded aligned copies of both operands (K rounded up to a whole chunk).
+    const int64_t Kp = ceil_div(K, vec) * vec;
+    int rc = dtype == MTHIP_F16 ? pad_operand<uint16_t>(device, s, x, 1, M, K, lda, 0, Kp, &xp)
+                                : pad_operand<float>(device, s, x, 1, M, K, lda, 0, Kp, &xp);
+    if (rc == MTHIP_OK)
+      rc = dtype == MTHIP_F16 ? pad_operand<uint16_t>(device, s, w, 1, N, K, ldw, 0, Kp, &wp)
+                              : pad_operand<float>(device, s, w, 1, N, K, ldw, 0, Kp, &wp);
+    if (rc != MTHIP_OK) {
+      mthip_free(device, xp);
+      return rc;
+    }
+    a.a = xp;
+    a.b = wp;
+    a.lda = a.ldb = Kp;
+    a.K = Kp;
   }
-  if (dtype == MTHIP_F16) return launch_gemm<uint16_t, MODE_NT, EPI_LINEAR>(a, 1, s);
-  return launch_gemm<float, MODE_NT, EPI_LINEAR>(a, 1, s);
+  a.vec_ok = 1;
+  a.a_bytes = ((M - 1) * a.lda + a.K) * es;
+  a.b_bytes = ((N - 1) * a.ldb + a.K) * es;
+  int rc;
+  if (a.a_bytes > kMaxBufferBytes || a.b_bytes > kMaxBufferBytes)
+    rc = fail(MTHIP_ERR_UNSUPPORTED, "mthip_linear: operands above 2 GiB are not supported");
+  else if (dtype == MTHIP_F16)
+    rc = launch_gemm<uint16_t, MODE_NT, EPI_LINEAR>(a, 1, s);
+  else
+    rc = launch_gemm<float, MODE_NT, EPI_LINEAR>(a, 1, s);
+  mthip_free(device, xp);  // stream-ordered: reused only by later work
+  mthip_free(device, wp);
+  return rc;
 }
 
 int mthip_gemm(int device, int dtype, int64_t batch, int64_t M, int64_t N, int64_t K, const void* a_ptr, int64_t lda,
@@ -130,14 +198,52 @@ int mthip_gemm(int device, int dtype, int64_t batch, int64_t M, int64_t N, int64
   a.c_in_cs = c_in_cs;
   a.stride_c_in = stride_c_in;
   const int vec = dtype == MTHIP_F16 ? 8 : 4;
-  a.vec_ok = aligned16(a_ptr) && aligned16(b_ptr) && lda % vec == 0 && ldb % vec == 0 && stride_a % vec == 0 &&
-             stride_b % vec == 0;
-  if (b_trans) {
-    if (dtype == MTHIP_F16) return launch_gemm<uint16_t, MODE_NT, EPI_GEMM>(a, batch, s);
-    return launch_gemm<float, MODE_NT, EPI_GEMM>(a, batch, s);
+  const int64_t es = dtype == MTHIP_F16 ? 2 : 4;
+  const int64_t b_cols = b_trans ? K : N;   // contiguous extent of a B row
+  const int64_t b_rows = b_trans ? N : K;
+  bool a_ok = aligned16(a_ptr) && lda % vec == 0 && stride_a % vec == 0 && K % vec == 0;
+  bool b_ok = aligned16(b_ptr) && ldb % vec == 0 && stride_b % vec == 0 && b_cols % vec == 0;
+  void* ap = nullptr;
+  void* bp = nullptr;
+  int rc = MTHIP_OK;
+  if (!a_ok || !b_ok) {
+    // Zero-padded aligned copies; K (and, for a [K, N] B, N) rounded up to whole chunks.
+    const int64_t Kp = ceil_div(K, vec) * vec;
+    const int64_t a_batches = stride_a == 0 ? 1 : batch, b_batches = stride_b == 0 ? 1 : batch;
+    rc = dtype == MTHIP_F16 ? pad_operand<uint16_t>(device, s, a_ptr, a_batches, M, K, lda, stride_a, Kp, &ap)
+                            : pad_operand<float>(device, s, a_ptr, a_batches, M, K, lda, stride_a, Kp, &ap);
+    const int64_t bcp = ceil_div(b_cols, vec) * vec;
+    if (rc == MTHIP_OK)
+      rc = dtype == MTHIP_F16 ? pad_operand<uint16_t>(device, s, b_ptr, b_batches, b_rows, b_cols, ldb, stride_b, bcp, &bp)
+                              : pad_operand<float>(device, s, b_ptr, b_batches, b_rows, b_cols, ldb, stride_b, bcp, &bp);
+    if (rc == MTHIP_OK) {
+      a.a = ap;
+      a.lda = Kp;
+      a.stride_a = stride_a == 0 ? 0 : M * Kp;
+      a.b = bp;
+      a.ldb = bcp;
+      a.stride_b = stride_b == 0 ? 0 : b_rows * bcp;
+      // K-padding of a [K, N] B adds zero rows: extend K only when both operands carry it.
+      if (b_trans) a.K = Kp;
+    }
   }
-  if (dtype == MTHIP_F16) return launch_gemm<uint16_t, MODE_NN, EPI_GEMM>(a, batch, s);
-  return launch_gemm<float, MODE_NN, EPI_GEMM>(a, batch, s);
+  if (rc == MTHIP_OK) {
+    a.vec_ok = 1;
+    a.a_bytes = ((M - 1) * a.lda + a.K) * es;
+    a.b_bytes = b_trans ? ((N - 1) * a.ldb + a.K) * es : ((K - 1) * a.ldb + ceil_div(N, vec) * vec) * es;
+    if (a.a_bytes > kMaxBufferBytes || a.b_bytes > kMaxBufferBytes) {
+      rc = fail(MTHIP_ERR_UNSUPPORTED, "mthip_gemm: operands above 2 GiB per batch are not supported");
+    } else if (b_trans) {
+      rc = dtype == MTHIP_F16 ? launch_gemm<uint16_t, MODE_NT, EPI_GEMM>(a, batch, s)
+                              : launch_gemm<float, MODE_NT, EPI_GEMM>(a, batch, s);
+    } else {
+      rc = dtype == MTHIP_F16 ? launch_gemm<uint16_t, MODE_NN, EPI_GEMM>(a, batch, s)
+                              : launch_gemm<float, MODE_NN, EPI_GEMM>(a, batch, s);
+    }
+  }
+  mthip_free(device, ap);
+  mthip_free(device, bp);
+  return rc;
 }
 
 }  // extern "C"
