@@ -185,11 +185,26 @@ int mthip_gemm(int device, int dtype, int64_t batch, int64_t M, int64_t N, int64
  * NCHW contiguous in and out -- mtorch::conv2d (tensor.cpp:26490-27528; py_conv2d
  * module.cpp:6912-6961).  groups == 1 runs as an implicit GEMM on MFMA (fp16: fp32
  * accumulate); the residual, when given, is added after the conv result is narrowed.
- * `workspace` may be NULL (the library allocates). */
+ * Staging buffers come from the library's caching allocator. */
 int mthip_conv2d(int device, int dtype, const void* x, const void* w, const void* b, void* y,
                  int64_t B, int64_t C, int64_t H, int64_t W, int64_t O, int64_t KH, int64_t KW,
                  int64_t stride_h, int64_t stride_w, int64_t pad_h, int64_t pad_w,
                  int64_t dil_h, int64_t dil_w, int64_t groups, const void* residual);
+
+/* Packed conv weight for the groups == 1 implicit GEMM: wp[O][KH][KW][Cp], Cp = C rounded up
+ * to 8 (F16) or 4 (F32) channels, zero filled.  The packed copy plays the role of the
+ * reference's per-Storage weight caches (tensor.h:65-78, filled by the CPU conv/linear fast
+ * paths): the caller keeps it while the weight storage's version is unchanged and passes it
+ * to mthip_conv2d_prepacked, which then skips the per-call repack.
+ * mthip_conv2d_packed_bytes returns the size of wp in bytes (-1 for a bad dtype). */
+int64_t mthip_conv2d_packed_bytes(int dtype, int64_t O, int64_t C, int64_t KH, int64_t KW);
+int mthip_conv2d_pack_weight(int device, int dtype, const void* w, void* wp,
+                             int64_t O, int64_t C, int64_t KH, int64_t KW);
+/* mthip_conv2d (groups == 1) with a weight packed by mthip_conv2d_pack_weight. */
+int mthip_conv2d_prepacked(int device, int dtype, const void* x, const void* wp, const void* b, void* y,
+                           int64_t B, int64_t C, int64_t H, int64_t W, int64_t O, int64_t KH, int64_t KW,
+                           int64_t stride_h, int64_t stride_w, int64_t pad_h, int64_t pad_w,
+                           int64_t dil_h, int64_t dil_w, const void* residual);
 
 /* ===================================================================== attention */
 

@@ -59,6 +59,10 @@ _SIGNATURES = {
                           _int, _c_void_p, _i64, _i64, _dbl, _dbl, _c_void_p, _i64, _i64, _i64]),
     "mthip_conv2d": (_int, [_int, _int, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i64, _i64,
                             _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _c_void_p]),
+    "mthip_conv2d_packed_bytes": (_i64, [_int, _i64, _i64, _i64, _i64]),
+    "mthip_conv2d_pack_weight": (_int, [_int, _int, _c_void_p, _c_void_p, _i64, _i64, _i64, _i64]),
+    "mthip_conv2d_prepacked": (_int, [_int, _int, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i64,
+                                      _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _c_void_p]),
     "mthip_sdpa": (_int, [_int, _int, _c_void_p, _i64p, _c_void_p, _i64p, _c_void_p, _i64p, _c_void_p,
                           _i64, _i64, _i64, _i64, _i64, _i64, _i64, _int, _int, _c_void_p, _i64p, _int, _dbl]),
     "mthip_group_norm": (_int, [_int, _int, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i64,

@@ -188,12 +188,14 @@ def fill_(t: Tensor, value) -> None:
             view[...] = _random.float_to_half_bits(np.array([value], dtype=np.float32))[0]
         else:
             view[...] = value
+        t._storage.version += 1
         return
     if not t.is_contiguous():
         raise unsupported("fill_ on a non-contiguous view", "cuda")
     n = t.numel()
     if n:
         _lib.check(_L().mthip_fill(t._dev(), t.dtype.code, t.data_ptr(), n, float(value)))
+    t._storage.version += 1
 
 
 # ------------------------------------------------------------------------------ elementwise
@@ -585,9 +587,34 @@ def conv2d(x: Tensor, w: Tensor, b: Tensor = None, stride=1, padding=0, dilation
             raise ValueError("conv2d residual must have the output shape")
         rc = residual.contiguous()
     if out.numel():
-        _lib.check(_L().mthip_conv2d(dev, x.dtype.code, xc.data_ptr(), wc.data_ptr(), _ptr(bc), out.data_ptr(), B, C,
-                                     H, W, O, KH, KW, sh, sw, ph, pw, dh, dw, groups, _ptr(rc)))
+        if groups == 1:
+            wp = _conv_packed_weight(wc, dev, O, C, KH, KW)
+            _lib.check(_L().mthip_conv2d_prepacked(dev, x.dtype.code, xc.data_ptr(), wp, _ptr(bc), out.data_ptr(), B,
+                                                   C, H, W, O, KH, KW, sh, sw, ph, pw, dh, dw, _ptr(rc)))
+        else:
+            _lib.check(_L().mthip_conv2d(dev, x.dtype.code, xc.data_ptr(), wc.data_ptr(), _ptr(bc), out.data_ptr(), B,
+                                         C, H, W, O, KH, KW, sh, sw, ph, pw, dh, dw, groups, _ptr(rc)))
     return out.squeeze(0) if unbatched else out
+
+
+def _conv_packed_weight(w: Tensor, dev: int, O: int, C: int, KH: int, KW: int) -> int:
+    """Device pointer of w (contiguous [O, C, KH, KW]) packed for mthip_conv2d_prepacked.  The
+    packed copy lives on w's storage, keyed by the view and tagged with the storage version, so
+    it is rebuilt only after an in-place write to the weight (the role of the reference's
+    Storage weight caches, tensor.h:65-78)."""
+    st = w._storage
+    key = ("conv2d", w._offset, O, C, KH, KW)
+    if st.packs is None:
+        st.packs = {}
+    hit = st.packs.get(key)
+    if hit is not None and hit[0] == st.version:
+        return hit[1].ptr
+    L = _L()
+    nbytes = L.mthip_conv2d_packed_bytes(w.dtype.code, O, C, KH, KW)
+    buf = T._DeviceBuffer(nbytes, dev)
+    _lib.check(L.mthip_conv2d_pack_weight(dev, w.dtype.code, w.data_ptr(), buf.ptr, O, C, KH, KW))
+    st.packs[key] = (st.version, buf)
+    return buf.ptr
 
 
 # ------------------------------------------------------------------------------ attention

@@ -234,13 +234,19 @@ class _DeviceBuffer:
 
 
 class Storage:
-    __slots__ = ("dtype", "device", "numel", "host", "buf", "version")
+    """Bytes shared by views (tensor.h:60-85).  `version` counts in-place writes; `packs` holds
+    derived device layouts of this storage (the packed conv weight), each tagged with the
+    version it was built from -- the device counterpart of the reference's per-Storage weight
+    caches (tensor.h:65-78)."""
+
+    __slots__ = ("dtype", "device", "numel", "host", "buf", "version", "packs")
 
     def __init__(self, dt: dtype, numel: _builtins.int, dev: device, host=None, zero=False):
         self.dtype = dt
         self.device = dev
         self.numel = numel
         self.version = 0
+        self.packs = None
         if dev.type == "cpu":
             self.host = host if host is not None else (np.zeros(numel, dtype=dt.np) if zero else np.empty(numel, dtype=dt.np))
             self.buf = None

@@ -40,6 +40,25 @@ int check_launch(const char* what);
 
 __host__ __device__ inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
+// Division of a 32-bit unsigned value by a run-time invariant d >= 1 as a multiply-high, add
+// and shift (Granlund & Montgomery, "Division by invariant integers using multiplication",
+// PLDI 1994, round-up variant): with l = ceil(log2 d) and m = floor(2^32 (2^l - d) / d) + 1,
+// n / d = (mulhi(n, m) + n) >> l for every n < 2^32.  Kernels divide tile and pixel indices
+// this way instead of through the ~100-instruction generic division.
+struct FastDiv {
+  uint32_t d, m, l;
+  FastDiv() = default;
+  __host__ explicit FastDiv(uint32_t divisor) : d(divisor), m(0), l(0) {
+    while ((uint64_t(1) << l) < (uint64_t)d) ++l;
+    m = (uint32_t)(((uint64_t(1) << 32) * ((uint64_t(1) << l) - d)) / d + 1);
+  }
+  __device__ __forceinline__ uint32_t div(uint32_t n) const {
+    const uint64_t t = __umulhi(n, m);
+    return (uint32_t)((t + n) >> l);
+  }
+  __device__ __forceinline__ uint32_t mod(uint32_t n) const { return n - div(n) * d; }
+};
+
 // ---- device fp16 conversion ------------------------------------------------------------
 // mtorch's float_to_half_bits (tensor.cpp:276-315) rounds the magnitude half-away-from-zero
 // (add 0x1000 then drop 13 bits), shifts subnormals before rounding and flushes anything
@@ -67,20 +86,26 @@ __device__ __forceinline__ uint16_t f2h_bits(float value) {
   return (uint16_t)(sign | (rounded >= 0x7c00u ? 0x7c00u : rounded));
 }
 
-// Same rounding rule as f2h_bits, cheaper for the common case.  In the normal half range
-// (biased float exponent 113..142) the hardware conversion rounds to nearest-even; it differs
-// from half-away-from-zero only on exact ties whose kept LSB is 0 (discarded bits == 0x1000
-// with bit 13 clear), where one ulp is added to the magnitude.  Everything else (subnormal
-// halves, overflow, inf/NaN) takes the integer restatement.
+// Bit-identical to f2h_bits for every input, branch-free and short (it is inlined into every
+// narrowing store).  mtorch's rule is round-to-nearest with ties away from zero, overflowing to
+// inf; the hardware conversion (v_cvt_f16_f32, with fp16 subnormals) rounds to nearest-even
+// and overflows the same way.  The two differ only on exact ties whose kept LSB is 0, where
+// RNE keeps the smaller magnitude: with sh discarded significand bits (13 for normal halves,
+// up to 24 for the smallest subnormal, biased float exponent 102..142), such a tie has
+// significand & (2^(sh+1) - 1) == 2^(sh-1), and one ulp is added to the magnitude.  NaNs keep
+// the top payload bits as mtorch does (the hardware would set the quiet bit).
 __device__ __forceinline__ uint16_t f2h_fast(float value) {
   const uint32_t bits = __float_as_uint(value);
-  const uint32_t e = (bits >> 23) & 0xffu;
-  if (e - 113u <= 29u) {
-    uint16_t h = __builtin_bit_cast(uint16_t, (_Float16)value);
-    h += (uint16_t)((bits & 0x3fffu) == 0x1000u);
-    return h;
-  }
-  return f2h_bits(value);
+  const uint32_t raw = (bits >> 23) & 0xffu;
+  uint32_t h = __builtin_bit_cast(uint16_t, (_Float16)value);
+  const int d = 126 - (int)raw;
+  const uint32_t sh = (uint32_t)(d < 13 ? 13 : (d > 24 ? 24 : d));
+  const uint32_t sig = (bits & 0x7fffffu) | 0x800000u;
+  const bool tie_even = (sig & ((2u << sh) - 1u)) == (1u << (sh - 1u));
+  h += (raw - 102u <= 40u && tie_even) ? 1u : 0u;
+  const uint32_t payload = (bits & 0x7fffffu) >> 13;
+  const uint32_t nan_bits = ((bits >> 16) & 0x8000u) | 0x7c00u | (payload != 0u ? payload : 0x200u);
+  return (uint16_t)((bits & 0x7fffffffu) > 0x7f800000u ? nan_bits : h);
 }
 
 // Exact widening; finite values and infinities match tensor.cpp:317-344 bit for bit.

@@ -13,7 +13,7 @@
 
 namespace mthip {
 
-int launch_conv_gemm(int dtype, const GemmArgs& a, hipStream_t s);
+int launch_conv_gemm(int device, int dtype, const GemmArgs& a, hipStream_t s);
 
 namespace {
 
@@ -91,42 +91,33 @@ __global__ void conv_direct_kernel(const T* __restrict__ x, const T* __restrict_
 }
 
 template <typename T>
-int run_conv(int device, int dtype, const void* x, const void* w, const void* b, void* y, int64_t B, int64_t C,
-             int64_t H, int64_t W, int64_t O, int64_t KH, int64_t KW, int64_t sh, int64_t sw, int64_t ph, int64_t pw,
-             int64_t dh, int64_t dw, int64_t groups, const void* residual, hipStream_t s) {
+int launch_pack_weight(const void* w, void* wp, int64_t O, int64_t C, int64_t KH, int64_t KW, hipStream_t s) {
+  const int64_t Cp = ceil_div(C, Mfma<T>::VEC) * Mfma<T>::VEC;
+  const int64_t n = O * KH * KW * Cp;
+  hipLaunchKernelGGL(pack_weight_kernel<T>, dim3((unsigned)std::max<int64_t>(1, std::min<int64_t>(ceil_div(n, 256), 4096))),
+                     dim3(256), 0, s, (const T*)w, (T*)wp, O, C, Cp, KH, KW);
+  return check_launch("pack_weight_kernel");
+}
+
+// groups == 1 with a packed weight: stage x as NHWC, then the implicit GEMM.
+template <typename T>
+int run_conv_gemm(int device, int dtype, const void* x, const void* wp, const void* b, void* y, int64_t B, int64_t C,
+                  int64_t H, int64_t W, int64_t O, int64_t KH, int64_t KW, int64_t sh, int64_t sw, int64_t ph,
+                  int64_t pw, int64_t dh, int64_t dw, const void* residual, hipStream_t s) {
   const int64_t OH = (H + 2 * ph - dh * (KH - 1) - 1) / sh + 1;
   const int64_t OW = (W + 2 * pw - dw * (KW - 1) - 1) / sw + 1;
-  if (B == 0 || O == 0 || OH <= 0 || OW <= 0) return MTHIP_OK;
-  if (groups != 1) {
-    const int64_t n = B * O * OH * OW;
-    const unsigned g = (unsigned)std::min<int64_t>(ceil_div(n, 256), 8192);
-    hipLaunchKernelGGL(conv_direct_kernel<T>, dim3(g), dim3(256), 0, s, (const T*)x, (const T*)w, (const T*)b,
-                       (const T*)residual, (T*)y, B, C, H, W, O, KH, KW, OH, OW, sh, sw, ph, pw, dh, dw, groups);
-    return check_launch("conv_direct_kernel");
-  }
+  if (B == 0 || OH <= 0 || OW <= 0) return MTHIP_OK;
   constexpr int VEC = Mfma<T>::VEC;
   const int64_t Cp = ceil_div(C, VEC) * VEC;
   const int64_t HW = H * W;
   const int64_t K = KH * KW * Cp;
+  if (O * K * (int64_t)sizeof(T) >= (int64_t(1) << 31) || B * HW * Cp * (int64_t)sizeof(T) >= (int64_t(1) << 31))
+    return fail(MTHIP_ERR_UNSUPPORTED, "mthip_conv2d: operands above 2 GiB are not supported");
   void* xp = nullptr;
-  void* wp = nullptr;
   if (int rc = mthip_malloc(device, (size_t)(B * HW * Cp) * sizeof(T), &xp)) return rc;
-  if (int rc = mthip_malloc(device, (size_t)(O * K) * sizeof(T), &wp)) {
-    mthip_free(device, xp);
-    return rc;
-  }
-  int rc = MTHIP_OK;
-  {
-    dim3 grid((unsigned)ceil_div(HW, 32), (unsigned)ceil_div(Cp, 32), (unsigned)B);
-    hipLaunchKernelGGL(nchw_to_nhwc_pad_kernel<T>, grid, dim3(256), 0, s, (const T*)x, (T*)xp, C, Cp, HW);
-    rc = check_launch("nchw_to_nhwc_pad_kernel");
-  }
-  if (rc == MTHIP_OK) {
-    const int64_t n = O * K;
-    hipLaunchKernelGGL(pack_weight_kernel<T>, dim3((unsigned)std::min<int64_t>(ceil_div(n, 256), 4096)), dim3(256), 0, s,
-                       (const T*)w, (T*)wp, O, C, Cp, KH, KW);
-    rc = check_launch("pack_weight_kernel");
-  }
+  dim3 grid((unsigned)ceil_div(HW, 32), (unsigned)ceil_div(Cp, 32), (unsigned)B);
+  hipLaunchKernelGGL(nchw_to_nhwc_pad_kernel<T>, grid, dim3(256), 0, s, (const T*)x, (T*)xp, C, Cp, HW);
+  int rc = check_launch("nchw_to_nhwc_pad_kernel");
   if (rc == MTHIP_OK) {
     GemmArgs a{};
     a.M = O;
@@ -150,16 +141,34 @@ int run_conv(int device, int dtype, const void* x, const void* w, const void* b,
     a.pw = pw;
     a.dh = dh;
     a.dw = dw;
-    a.vec_ok = 1;  // packed buffers: rows are whole chunks, bases come from the allocator
     a.a_bytes = O * K * (int64_t)sizeof(T);
     a.b_bytes = B * HW * Cp * (int64_t)sizeof(T);
-    if (a.a_bytes >= (int64_t(1) << 31) || a.b_bytes >= (int64_t(1) << 31))
-      rc = fail(MTHIP_ERR_UNSUPPORTED, "mthip_conv2d: operands above 2 GiB are not supported");
-    else
-      rc = launch_conv_gemm(dtype, a, s);
+    rc = launch_conv_gemm(device, dtype, a, s);
   }
-  // Stream-ordered frees: the blocks are only reused by work enqueued after this conv.
-  mthip_free(device, xp);
+  mthip_free(device, xp);  // stream-ordered: reused only by work enqueued after this conv
+  return rc;
+}
+
+template <typename T>
+int run_conv(int device, int dtype, const void* x, const void* w, const void* b, void* y, int64_t B, int64_t C,
+             int64_t H, int64_t W, int64_t O, int64_t KH, int64_t KW, int64_t sh, int64_t sw, int64_t ph, int64_t pw,
+             int64_t dh, int64_t dw, int64_t groups, const void* residual, hipStream_t s) {
+  const int64_t OH = (H + 2 * ph - dh * (KH - 1) - 1) / sh + 1;
+  const int64_t OW = (W + 2 * pw - dw * (KW - 1) - 1) / sw + 1;
+  if (B == 0 || O == 0 || OH <= 0 || OW <= 0) return MTHIP_OK;
+  if (groups != 1) {
+    const int64_t n = B * O * OH * OW;
+    const unsigned g = (unsigned)std::min<int64_t>(ceil_div(n, 256), 8192);
+    hipLaunchKernelGGL(conv_direct_kernel<T>, dim3(g), dim3(256), 0, s, (const T*)x, (const T*)w, (const T*)b,
+                       (const T*)residual, (T*)y, B, C, H, W, O, KH, KW, OH, OW, sh, sw, ph, pw, dh, dw, groups);
+    return check_launch("conv_direct_kernel");
+  }
+  const int64_t Cp = ceil_div(C, Mfma<T>::VEC) * Mfma<T>::VEC;
+  void* wp = nullptr;
+  if (int rc = mthip_malloc(device, (size_t)(O * KH * KW * Cp) * sizeof(T), &wp)) return rc;
+  int rc = launch_pack_weight<T>(w, wp, O, C, KH, KW, s);
+  if (rc == MTHIP_OK)
+    rc = run_conv_gemm<T>(device, dtype, x, wp, b, y, B, C, H, W, O, KH, KW, sh, sw, ph, pw, dh, dw, residual, s);
   mthip_free(device, wp);
   return rc;
 }
@@ -186,4 +195,39 @@ extern "C" int mthip_conv2d(int device, int dtype, const void* x, const void* w,
                               dil_h, dil_w, groups, residual, s);
   return run_conv<float>(device, dtype, x, w, b, y, B, C, H, W, O, KH, KW, stride_h, stride_w, pad_h, pad_w, dil_h,
                          dil_w, groups, residual, s);
+}
+
+extern "C" int64_t mthip_conv2d_packed_bytes(int dtype, int64_t O, int64_t C, int64_t KH, int64_t KW) {
+  if (dtype != MTHIP_F16 && dtype != MTHIP_F32) return -1;
+  const int64_t vec = dtype == MTHIP_F16 ? 8 : 4;
+  return O * KH * KW * ceil_div(C, vec) * vec * (dtype == MTHIP_F16 ? 2 : 4);
+}
+
+extern "C" int mthip_conv2d_pack_weight(int device, int dtype, const void* w, void* wp, int64_t O, int64_t C,
+                                        int64_t KH, int64_t KW) {
+  MTHIP_REQUIRE(dtype == MTHIP_F16 || dtype == MTHIP_F32, "mthip_conv2d_pack_weight: dtype must be F16 or F32");
+  MTHIP_REQUIRE(O > 0 && C > 0 && KH > 0 && KW > 0, "mthip_conv2d_pack_weight: bad extents");
+  hipStream_t s = stream_for(device);
+  if (!s) return MTHIP_ERR_HIP;
+  if (int rc = use_device(device)) return rc;
+  return dtype == MTHIP_F16 ? launch_pack_weight<uint16_t>(w, wp, O, C, KH, KW, s)
+                            : launch_pack_weight<float>(w, wp, O, C, KH, KW, s);
+}
+
+extern "C" int mthip_conv2d_prepacked(int device, int dtype, const void* x, const void* wp, const void* b, void* y,
+                                      int64_t B, int64_t C, int64_t H, int64_t W, int64_t O, int64_t KH, int64_t KW,
+                                      int64_t stride_h, int64_t stride_w, int64_t pad_h, int64_t pad_w, int64_t dil_h,
+                                      int64_t dil_w, const void* residual) {
+  MTHIP_REQUIRE(dtype == MTHIP_F16 || dtype == MTHIP_F32, "mthip_conv2d_prepacked: dtype must be F16 or F32");
+  MTHIP_REQUIRE(B >= 0 && C > 0 && H > 0 && W > 0 && O > 0 && KH > 0 && KW > 0, "mthip_conv2d_prepacked: bad extents");
+  MTHIP_REQUIRE(stride_h > 0 && stride_w > 0 && dil_h > 0 && dil_w > 0 && pad_h >= 0 && pad_w >= 0,
+                "mthip_conv2d_prepacked: bad stride/padding/dilation");
+  hipStream_t s = stream_for(device);
+  if (!s) return MTHIP_ERR_HIP;
+  if (int rc = use_device(device)) return rc;
+  if (dtype == MTHIP_F16)
+    return run_conv_gemm<uint16_t>(device, dtype, x, wp, b, y, B, C, H, W, O, KH, KW, stride_h, stride_w, pad_h,
+                                   pad_w, dil_h, dil_w, residual, s);
+  return run_conv_gemm<float>(device, dtype, x, wp, b, y, B, C, H, W, O, KH, KW, stride_h, stride_w, pad_h, pad_w,
+                              dil_h, dil_w, residual, s);
 }

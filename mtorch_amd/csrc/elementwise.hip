@@ -3,7 +3,8 @@
 //
 // Contiguous inputs run through grid-stride loops that move 16 bytes per lane per step;
 // strided and broadcast inputs go through a rank-collapsed index walk.  Every narrowing to
-// fp16 uses f2h_bits (mtorch's half-away-from-zero rule).
+// fp16 follows mtorch's half-away-from-zero rule (f2h_bits, or its branch-free equivalent
+// f2h_fast in the vectorised paths).
 #include <hip/hip_runtime.h>
 
 #include <algorithm>

@@ -9,8 +9,8 @@
 namespace mthip {
 namespace {
 
-// Tile shape per problem: large 128x128 tiles when they alone fill the 256 CUs at least
-// once, otherwise narrower tiles so small SD shapes (N = 320, few rows) still spread out.
+// Tile shape per problem.  With the persistent grid, 64x64 tiles (4 resident workgroups per
+// CU) measured fastest on every SD-UNet shape; the larger tiles stay selectable for sweeps.
 enum TileKind { T128x128, T128x64, T64x128, T64x64 };
 
 TileKind pick_tile(int64_t M, int64_t N, int64_t batch) {
@@ -19,41 +19,138 @@ TileKind pick_tile(int64_t M, int64_t N, int64_t batch) {
     const int t = std::atoi(force);
     if (t >= 0 && t <= 3) return static_cast<TileKind>(t);
   }
-  auto tiles = [&](int64_t bm, int64_t bn) { return ceil_div(M, bm) * ceil_div(N, bn) * batch; };
-  if (tiles(128, 128) >= 256) return T128x128;
-  if (tiles(128, 64) >= 256) return N <= 64 || M >= N ? T128x64 : T64x128;
-  if (tiles(64, 128) >= 256) return T64x128;
+  (void)M;
+  (void)N;
+  (void)batch;
   return T64x64;
 }
 
-template <typename T, int MODE, int EPI, bool FAST>
-int launch_gemm_fast(const GemmArgs& a, int64_t batch, hipStream_t s) {
-  const TileKind tk = pick_tile(a.M, a.N, batch);
-  auto grid = [&](int bm, int bn) {
-    return dim3((unsigned)ceil_div(a.N, bn), (unsigned)ceil_div(a.M, bm), (unsigned)batch);
-  };
-  MTHIP_REQUIRE(batch <= 65535, "gemm: batch must be <= 65535");
-  MTHIP_REQUIRE(ceil_div(a.M, 64) <= 65535, "gemm: M too large");
-  switch (tk) {
-    case T128x128:
-      hipLaunchKernelGGL((gemm_kernel<T, 128, 128, 2, MODE, EPI, FAST>), grid(128, 128), dim3(256), 0, s, a);
-      break;
-    case T128x64:
-      hipLaunchKernelGGL((gemm_kernel<T, 128, 64, 2, MODE, EPI, FAST>), grid(128, 64), dim3(256), 0, s, a);
-      break;
-    case T64x128:
-      hipLaunchKernelGGL((gemm_kernel<T, 64, 128, 2, MODE, EPI, FAST>), grid(64, 128), dim3(256), 0, s, a);
-      break;
-    default:
-      hipLaunchKernelGGL((gemm_kernel<T, 64, 64, 2, MODE, EPI, FAST>), grid(64, 64), dim3(256), 0, s, a);
-      break;
+// Tuning switches for sweeps: MTHIP_GEMM_SPLITK=0 disables K splitting, MTHIP_GEMM_PERSIST=0
+// launches one workgroup per unit, MTHIP_GEMM_XCD=0/1 forces the plain / XCD-contiguous unit
+// order (default: chosen per problem), MTHIP_GEMM_SPLIT_TARGET sets the split-K units per CU.
+int env_flag(const char* name, int dflt) {
+  const char* e = std::getenv(name);
+  return e ? std::atoi(e) : dflt;
+}
+bool splitk_enabled() { return env_flag("MTHIP_GEMM_SPLITK", 1) != 0; }
+bool persist_enabled() { return env_flag("MTHIP_GEMM_PERSIST", 1) != 0; }
+int xcd_mode() { return env_flag("MTHIP_GEMM_XCD", 2); }
+int split_target() { return std::max(1, env_flag("MTHIP_GEMM_SPLIT_TARGET", 4)); }
+
+int cu_count(int device) {
+  static int cached[64] = {0};
+  if (device < 0 || device >= 64) return 256;
+  if (cached[device] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess || n < 1) n = 256;
+    cached[device] = n;
   }
-  return check_launch("gemm_kernel");
+  return cached[device];
+}
+
+// Resident workgroups per CU of one kernel instance (registers and LDS decide it).
+template <typename T, int BM, int BN, int MODE, int EPI, int ACT, bool FAST>
+int resident_per_cu() {
+  static const int v = [] {
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, gemm_kernel<T, BM, BN, 2, MODE, EPI, ACT, FAST>, 256, 0) !=
+            hipSuccess ||
+        n < 1)
+      n = 1;
+    return n;
+  }();
+  return v;
+}
+
+// Sizes the persistent grid, splits K when the output tiles cannot fill the chip, launches the
+// GEMM (and the slice reduction).
+template <typename T, int BM, int BN, int MODE, int EPI, int ACT, bool FAST>
+int launch_tile(int device, GemmArgs a, int64_t batch, hipStream_t s) {
+  constexpr int BK = Mfma<T>::BK;
+  a.tiles_m = ceil_div(a.M, BM);
+  a.tiles_n = ceil_div(a.N, BN);
+  const int64_t nk = std::max<int64_t>(ceil_div(a.K, BK), 1);
+  const int64_t tiles = a.tiles_m * a.tiles_n * batch;
+  const int64_t slots = (int64_t)cu_count(device) * resident_per_cu<T, BM, BN, MODE, EPI, ACT, FAST>();
+  int64_t ksplit = 1;
+  // Split K only for single-batch problems with fewer tiles than about `split_target` units
+  // per CU, into enough slices to reach that, each slice keeping >= 16 K tiles: every slice
+  // costs an fp32 M x N write and read in the reduction, which only long K amortises (the
+  // 3x3 convs at 1280 channels gain 4x; linears with K = 1280 already lose at 2 slices).
+  const int64_t target = (int64_t)cu_count(device) * split_target();
+  if (batch == 1 && tiles < target && nk >= 32 && splitk_enabled())
+    ksplit = std::max<int64_t>(1, std::min<int64_t>(std::min<int64_t>(ceil_div(target, tiles), nk / 16), 16));
+  a.kt_per_split = ceil_div(nk, ksplit);
+  a.ksplit = ceil_div(nk, a.kt_per_split);  // no empty slice
+  a.units = tiles * a.ksplit;
+  MTHIP_REQUIRE(a.units < (int64_t(1) << 31) && a.N < (int64_t(1) << 31) && a.M < (int64_t(1) << 31),
+                "gemm: problem too large (tiles, rows or columns beyond 2^31)");
+  a.div_tiles_n = FastDiv((uint32_t)a.tiles_n);
+  a.div_tiles_m = FastDiv((uint32_t)a.tiles_m);
+  a.div_ksplit = FastDiv((uint32_t)a.ksplit);
+  if (MODE == MODE_CONV) {
+    a.div_ohw = FastDiv((uint32_t)(a.OH * a.OW));
+    a.div_ow = FastDiv((uint32_t)a.OW);
+  }
+  int64_t g = persist_enabled() ? std::min(a.units, slots) : a.units;
+  if (g > 8 && g < a.units) g = g / 8 * 8;  // a multiple of 8 keeps each XCD on its own run of tiles
+  // Unit order and L2 reuse: dealt round-robin, XCD x sees output columns tn = x (mod 8) when
+  // tiles_n % 8 == 0 (so reads 1/8 of B and all of A); XCD-contiguous, it sees a band of rows
+  // (1/8 of A, all of B).  Take the smaller per-XCD footprint.
+  const int xm = xcd_mode();
+  a.xcd_remap = xm == 0 ? 0 : xm == 1 ? 1 : (a.N < a.M || a.tiles_n % 8 != 0) ? 1 : 0;
+  void* ws = nullptr;
+  if (a.ksplit > 1) {
+    a.ld_partial = ceil_div(a.N, 4) * 4;
+    if (int rc = mthip_malloc(device, (size_t)(a.ksplit * a.M * a.ld_partial) * sizeof(float), &ws)) return rc;
+    a.partial = static_cast<float*>(ws);
+  }
+  hipLaunchKernelGGL((gemm_kernel<T, BM, BN, 2, MODE, EPI, ACT, FAST>), dim3((unsigned)g), dim3(256), 0, s, a);
+  int rc = check_launch("gemm_kernel");
+  if (rc == MTHIP_OK && a.ksplit > 1) {
+    const int64_t work = a.M * ceil_div(a.N, 4);
+    const unsigned rg = (unsigned)std::min<int64_t>(ceil_div(work, 256), 8192);
+    hipLaunchKernelGGL((gemm_splitk_reduce_kernel<T, EPI, ACT>), dim3(rg), dim3(256), 0, s, a);
+    rc = check_launch("gemm_splitk_reduce_kernel");
+  }
+  if (ws) mthip_free(device, ws);  // stream-ordered: reused only by later work
+  return rc;
+}
+
+template <typename T, int MODE, int EPI, int ACT, bool FAST>
+int launch_gemm_tiles(int device, const GemmArgs& a, int64_t batch, hipStream_t s) {
+  switch (pick_tile(a.M, a.N, batch)) {
+    case T128x128:
+      return launch_tile<T, 128, 128, MODE, EPI, ACT, FAST>(device, a, batch, s);
+    case T128x64:
+      return launch_tile<T, 128, 64, MODE, EPI, ACT, FAST>(device, a, batch, s);
+    case T64x128:
+      return launch_tile<T, 64, 128, MODE, EPI, ACT, FAST>(device, a, batch, s);
+    default:
+      return launch_tile<T, 64, 64, MODE, EPI, ACT, FAST>(device, a, batch, s);
+  }
+}
+
+template <typename T, int MODE, int EPI, bool FAST>
+int launch_gemm_fast(int device, const GemmArgs& a, int64_t batch, hipStream_t s) {
+  if constexpr (EPI == EPI_LINEAR) {
+    switch (a.act) {
+      case MTHIP_ACT_GELU:
+        return launch_gemm_tiles<T, MODE, EPI, MTHIP_ACT_GELU, FAST>(device, a, batch, s);
+      case MTHIP_ACT_GELU_TANH:
+        return launch_gemm_tiles<T, MODE, EPI, MTHIP_ACT_GELU_TANH, FAST>(device, a, batch, s);
+      case MTHIP_ACT_SILU:
+        return launch_gemm_tiles<T, MODE, EPI, MTHIP_ACT_SILU, FAST>(device, a, batch, s);
+      default:
+        break;
+    }
+  }
+  return launch_gemm_tiles<T, MODE, EPI, MTHIP_ACT_NONE, FAST>(device, a, batch, s);
 }
 
 template <typename T, int MODE, int EPI>
-int launch_gemm(const GemmArgs& a, int64_t batch, hipStream_t s) {
-  return launch_gemm_fast<T, MODE, EPI, false>(a, batch, s);
+int launch_gemm(int device, const GemmArgs& a, int64_t batch, hipStream_t s) {
+  return launch_gemm_fast<T, MODE, EPI, false>(device, a, batch, s);
 }
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
@@ -90,14 +187,14 @@ constexpr int64_t kMaxBufferBytes = (int64_t(1) << 31) - 1;
 }  // namespace
 
 // Shared with conv.hip.
-int launch_conv_gemm(int dtype, const GemmArgs& a, hipStream_t s) {
+int launch_conv_gemm(int device, int dtype, const GemmArgs& a, hipStream_t s) {
   // With the padded channel count a multiple of BK, no K tile straddles two filter taps.
   if (dtype == MTHIP_F16) {
-    if (a.Cp % Mfma<uint16_t>::BK == 0) return launch_gemm_fast<uint16_t, MODE_CONV, EPI_CONV, true>(a, 1, s);
-    return launch_gemm_fast<uint16_t, MODE_CONV, EPI_CONV, false>(a, 1, s);
+    if (a.Cp % Mfma<uint16_t>::BK == 0) return launch_gemm_fast<uint16_t, MODE_CONV, EPI_CONV, true>(device, a, 1, s);
+    return launch_gemm_fast<uint16_t, MODE_CONV, EPI_CONV, false>(device, a, 1, s);
   }
-  if (a.Cp % Mfma<float>::BK == 0) return launch_gemm_fast<float, MODE_CONV, EPI_CONV, true>(a, 1, s);
-  return launch_gemm_fast<float, MODE_CONV, EPI_CONV, false>(a, 1, s);
+  if (a.Cp % Mfma<float>::BK == 0) return launch_gemm_fast<float, MODE_CONV, EPI_CONV, true>(device, a, 1, s);
+  return launch_gemm_fast<float, MODE_CONV, EPI_CONV, false>(device, a, 1, s);
 }
 
 }  // namespace mthip
@@ -153,16 +250,15 @@ int mthip_linear(int device, int dtype, const void* x, int64_t lda, const void* 
     a.lda = a.ldb = Kp;
     a.K = Kp;
   }
-  a.vec_ok = 1;
   a.a_bytes = ((M - 1) * a.lda + a.K) * es;
   a.b_bytes = ((N - 1) * a.ldb + a.K) * es;
   int rc;
   if (a.a_bytes > kMaxBufferBytes || a.b_bytes > kMaxBufferBytes)
     rc = fail(MTHIP_ERR_UNSUPPORTED, "mthip_linear: operands above 2 GiB are not supported");
   else if (dtype == MTHIP_F16)
-    rc = launch_gemm<uint16_t, MODE_NT, EPI_LINEAR>(a, 1, s);
+    rc = launch_gemm<uint16_t, MODE_NT, EPI_LINEAR>(device, a, 1, s);
   else
-    rc = launch_gemm<float, MODE_NT, EPI_LINEAR>(a, 1, s);
+    rc = launch_gemm<float, MODE_NT, EPI_LINEAR>(device, a, 1, s);
   mthip_free(device, xp);  // stream-ordered: reused only by later work
   mthip_free(device, wp);
   return rc;
@@ -228,17 +324,16 @@ int mthip_gemm(int device, int dtype, int64_t batch, int64_t M, int64_t N, int64
     }
   }
   if (rc == MTHIP_OK) {
-    a.vec_ok = 1;
-    a.a_bytes = ((M - 1) * a.lda + a.K) * es;
+      a.a_bytes = ((M - 1) * a.lda + a.K) * es;
     a.b_bytes = b_trans ? ((N - 1) * a.ldb + a.K) * es : ((K - 1) * a.ldb + ceil_div(N, vec) * vec) * es;
     if (a.a_bytes > kMaxBufferBytes || a.b_bytes > kMaxBufferBytes) {
       rc = fail(MTHIP_ERR_UNSUPPORTED, "mthip_gemm: operands above 2 GiB per batch are not supported");
     } else if (b_trans) {
-      rc = dtype == MTHIP_F16 ? launch_gemm<uint16_t, MODE_NT, EPI_GEMM>(a, batch, s)
-                              : launch_gemm<float, MODE_NT, EPI_GEMM>(a, batch, s);
+      rc = dtype == MTHIP_F16 ? launch_gemm<uint16_t, MODE_NT, EPI_GEMM>(device, a, batch, s)
+                              : launch_gemm<float, MODE_NT, EPI_GEMM>(device, a, batch, s);
     } else {
-      rc = dtype == MTHIP_F16 ? launch_gemm<uint16_t, MODE_NN, EPI_GEMM>(a, batch, s)
-                              : launch_gemm<float, MODE_NN, EPI_GEMM>(a, batch, s);
+      rc = dtype == MTHIP_F16 ? launch_gemm<uint16_t, MODE_NN, EPI_GEMM>(device, a, batch, s)
+                              : launch_gemm<float, MODE_NN, EPI_GEMM>(device, a, batch, s);
     }
   }
   mthip_free(device, ap);

@@ -10,12 +10,23 @@
 // registers, four consecutive columns n -- the memory-contiguous direction of every output
 // here -- so results leave in 8/16-byte stores.
 //
-// K advances in BK-wide tiles through two LDS buffers fed by two register stages: the global
-// loads of tile k+2 are issued before the MFMAs of tile k, tile k+1 (requested one tile
-// earlier) is written to the other LDS buffer after them, and one barrier per tile suffices.
-// Loads are range-checked buffer loads from precomputed per-thread offsets; the implicit
-// im2col of the conv mode derives the (ky, kx, channel) of a tile once per tile (uniform
-// across the workgroup) when the padded channel count is a multiple of BK.
+// Work decomposition.  The problem is cut into units = (batch, K slice, output tile).  The
+// grid is persistent (about one wave of resident workgroups); workgroup w takes units w,
+// w + G, w + 2G, ...  and treats its units' K tiles as one flat stream: the global loads of
+// step s+2 are issued while step s is multiplied, also across unit boundaries, so a unit's
+// first tiles arrive while the previous unit is still computing and storing.  (SD shapes have
+// K = 320..2560, i.e. 5..40 K tiles per unit: without this the load latency at each unit's
+// start dominates.)  Units are numbered so that each XCD (workgroups are dealt to the 8 XCDs
+// round-robin) walks a contiguous run of output tiles, which share A rows in its L2.
+//
+// K advances in BK-wide tiles through two LDS buffers fed by two register stages; one barrier
+// per step suffices.  Loads are range-checked buffer loads from precomputed per-thread
+// offsets; the implicit im2col of the conv mode derives the (ky, kx, channel) of a tile once
+// per tile (uniform across the workgroup) when the padded channel count is a multiple of BK.
+//
+// When the output tiles alone cannot fill the chip and K is long (the 1280-channel convs at
+// 8x8 and 16x16), K is split into slices whose fp32 partial tiles go to a workspace;
+// gemm_splitk_reduce_kernel then sums the slices in a fixed order and applies the epilogue.
 //
 // The B operand has three sources (MODE): a k-contiguous [N, K] matrix (linear weights, x.W^T),
 // an n-contiguous [K, N] matrix (matmul; transposed while staging), or an implicit im2col of an
@@ -83,31 +94,149 @@ struct GemmArgs {
   int64_t c_in_rs, c_in_cs, stride_c_in;
   // MODE_CONV: B[n = output pixel, k = (ky, kx, c)] gathered from x_nhwc[img, iy, ix, Cp]
   int64_t H, W, Cp, OH, OW, KW, sh, sw, ph, pw, dh, dw;
-  int vec_ok;  // every A/B chunk may be read as one aligned 16-byte load
   // Extent (bytes) of the A and B buffers as seen from one batch's base; buffer loads beyond
   // it return zeros.  Must stay below 2^31.
   int64_t a_bytes, b_bytes;
+  // Work decomposition, filled by the launcher (gemm.hip).
+  int64_t tiles_m, tiles_n;  // output tiles per batch
+  int64_t ksplit;            // K slices per output tile (1: no split)
+  int64_t kt_per_split;      // K tiles per slice (the last slice may hold fewer)
+  int64_t units;             // batch * ksplit * tiles_m * tiles_n
+  float* partial;            // ksplit > 1: fp32 slices [ksplit][M][ld_partial]
+  int64_t ld_partial;        // N rounded up to a multiple of 4
+  // Divisors of the index arithmetic (units, pixels and N stay below 2^31).
+  FastDiv div_tiles_n, div_tiles_m, div_ksplit, div_ohw, div_ow;
+  int xcd_remap;  // 1: number units XCD-contiguously (see decode_unit)
 };
 
-// Narrowed store of 4 consecutive outputs (8 bytes fp16 / 16 bytes fp32) when aligned.
+// Stores the first nv (1..4) of 4 consecutive outputs, narrowed once each; one 8-byte (fp16)
+// or 16-byte (fp32) store when all four are valid and aligned.
 template <typename T>
-__device__ __forceinline__ void store4(T* p, const float v[4], bool vec) {
-  if (vec) {
-    if constexpr (sizeof(T) == 2) {
-      uint2 u;
-      u.x = (uint32_t)f2h_fast(v[0]) | ((uint32_t)f2h_fast(v[1]) << 16);
-      u.y = (uint32_t)f2h_fast(v[2]) | ((uint32_t)f2h_fast(v[3]) << 16);
-      *reinterpret_cast<uint2*>(p) = u;
+__device__ __forceinline__ void store_cols(T* p, const float (&v)[4], int nv) {
+  if constexpr (sizeof(T) == 2) {
+    uint32_t h[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) h[t] = f2h_fast(v[t]);
+    if (nv == 4 && ((uintptr_t)p & 7) == 0) {
+      *reinterpret_cast<uint2*>(p) = make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
     } else {
-      *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+        if (t < nv) p[t] = (uint16_t)h[t];
     }
   } else {
+    if (nv == 4 && ((uintptr_t)p & 15) == 0) {
+      *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
+    } else {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) Elem<T>::store(p, j, v[j]);
+      for (int t = 0; t < 4; ++t)
+        if (t < nv) p[t] = v[t];
+    }
   }
 }
 
-template <typename T, int BM, int BN, int WGM, int MODE, int EPI, bool CONV_FAST>
+// Epilogue for C[row][col0 .. col0+3] of batch bz (row < M checked by the caller; columns
+// past N are skipped).  v holds the fp32 dot products.  Values are narrowed once, except where
+// a fused activation or residual needs the narrowed intermediate that the unfused op sequence
+// would have produced.  ACT (EPI_LINEAR only) is the fused activation, fixed at compile time.
+template <typename T, int EPI, int ACT>
+__device__ __forceinline__ void emit4(const GemmArgs& args, int64_t bz, int row, int col0, float (&v)[4]) {
+  const int N = (int)args.N;
+  if (col0 >= N) return;
+  const int nv = N - col0 < 4 ? N - col0 : 4;  // valid columns (1..4)
+  T* Cptr = reinterpret_cast<T*>(args.c);
+  if constexpr (EPI == EPI_LINEAR) {
+    const T* bias = reinterpret_cast<const T*>(args.bias);
+    const T* res = args.residual ? reinterpret_cast<const T*>(args.residual) + (int64_t)row * args.ld_res : nullptr;
+    if (bias) {
+#pragma unroll
+      for (int t = 0; t < 4; ++t) v[t] += t < nv ? Elem<T>::load(bias, col0 + t) : 0.0f;
+    }
+    if (ACT != MTHIP_ACT_NONE || res) {
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        float x = Elem<T>::round_trip(v[t]);
+        if constexpr (ACT != MTHIP_ACT_NONE) x = apply_act<T>(ACT, x);
+        if (res) x = Elem<T>::round_trip(x) + (t < nv ? Elem<T>::load(res, col0 + t) : 0.0f);
+        v[t] = x;
+      }
+    }
+    store_cols<T>(Cptr + (int64_t)row * args.ldc + col0, v, nv);
+  } else if constexpr (EPI == EPI_GEMM) {
+    const T* cin = reinterpret_cast<const T*>(args.c_in);
+    const T* cinrow = cin ? cin + bz * args.stride_c_in + (int64_t)row * args.c_in_rs : nullptr;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      float x = v[t] * args.alpha;
+      if (cinrow && t < nv)
+        x = Elem<T>::round_trip(args.beta * Elem<T>::load(cinrow, (int64_t)(col0 + t) * args.c_in_cs)) + x;
+      v[t] = x;
+    }
+    store_cols<T>(Cptr + bz * args.stride_c + (int64_t)row * args.ldc + col0, v, nv);
+  } else {
+    // conv: row = output channel, col = output pixel (image-major); NCHW store.
+    const int M = (int)args.M;
+    const int OHW = (int)(args.OH * args.OW);
+    const T* bias = reinterpret_cast<const T*>(args.bias);
+    const T* res = reinterpret_cast<const T*>(args.residual);
+    const float bv = bias ? Elem<T>::load(bias, row) : 0.0f;
+    if (OHW % 4 == 0) {
+      // col0 is a multiple of 4, so the 4 pixels lie in one image and are contiguous.
+      const int img = (int)args.div_ohw.div((uint32_t)col0);
+      const int64_t addr = ((int64_t)img * M + row) * OHW + (col0 - img * OHW);
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        float x = v[t] + bv;
+        if (res) x = Elem<T>::round_trip(x) + (t < nv ? Elem<T>::load(res, addr + t) : 0.0f);
+        v[t] = x;
+      }
+      store_cols<T>(Cptr + addr, v, nv);
+    } else {
+      for (int t = 0; t < nv; ++t) {
+        const int c = col0 + t;
+        const int im = (int)args.div_ohw.div((uint32_t)c), px = c - im * OHW;
+        const int64_t addr = ((int64_t)im * M + row) * OHW + px;
+        float x = v[t] + bv;
+        if (res) x = Elem<T>::round_trip(x) + Elem<T>::load(res, addr);
+        Elem<T>::store(Cptr, addr, x);
+      }
+    }
+  }
+}
+
+// One unit of work: an output tile of one batch over one K slice.
+struct GemmUnit {
+  int64_t m0, n0, bz;
+  int64_t split;  // K slice index
+  int64_t kt0;    // first K tile
+  int64_t nkt;    // K tiles in this slice (>= 1)
+};
+
+template <int BM, int BN>
+__device__ __forceinline__ GemmUnit decode_unit(const GemmArgs& args, uint32_t u, uint32_t nk_total) {
+  // XCD-contiguous numbering: workgroups w = x (mod 8) run on XCD x and take units u = x (mod 8)
+  // (the grid size is a multiple of 8).  Remapping q = (u % 8) * (U / 8) + u / 8 hands XCD x the
+  // contiguous range [x*U/8, (x+1)*U/8) of tiles; the U % 8 tail keeps q = u (a bijection).
+  const uint32_t U = (uint32_t)args.units, U8 = U / 8;
+  const uint32_t q = (args.xcd_remap && u < 8 * U8) ? (u % 8) * U8 + u / 8 : u;
+  const uint32_t t1 = args.div_tiles_n.div(q);
+  const uint32_t tn = q - t1 * args.div_tiles_n.d;
+  const uint32_t t2 = args.div_tiles_m.div(t1);
+  const uint32_t tm = t1 - t2 * args.div_tiles_m.d;
+  const uint32_t bz = args.div_ksplit.div(t2);
+  GemmUnit un;
+  un.split = t2 - bz * args.div_ksplit.d;
+  un.bz = bz;
+  un.m0 = (int64_t)tm * BM;
+  un.n0 = (int64_t)tn * BN;
+  un.kt0 = un.split * args.kt_per_split;
+  const int64_t left = (int64_t)nk_total - un.kt0;
+  un.nkt = left < args.kt_per_split ? left : args.kt_per_split;
+  if (un.nkt < 1) un.nkt = 1;  // K == 0: one all-zero step, so the unit still gets its epilogue
+  return un;
+}
+
+template <typename T, int BM, int BN, int WGM, int MODE, int EPI, int ACT, bool CONV_FAST>
 __global__ __launch_bounds__(256) void gemm_kernel(const GemmArgs args) {
   constexpr int BK = Mfma<T>::BK;
   constexpr int VEC = Mfma<T>::VEC, LDK = BK + Mfma<T>::PAD;
@@ -128,65 +257,81 @@ __global__ __launch_bounds__(256) void gemm_kernel(const GemmArgs args) {
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave % WGM, wn = wave / WGM;
-  const int64_t bz = blockIdx.z;
-  const int64_t m0 = (int64_t)blockIdx.y * BM, n0 = (int64_t)blockIdx.x * BN;
   const int kc = (tid % CH_PER_ROW) * VEC;  // k offset of this thread's chunks within a tile
+  const uint32_t G = gridDim.x;
+  const uint32_t nk_total = (uint32_t)ceil_div(args.K, BK);
 
-  // ---- per-thread loader state ------------------------------------------------------
+  // ---- loader state (the unit whose tiles are being fetched) --------------------------
   // Every global read is a buffer load whose byte offset is either the chunk's address or
   // kOOB: the buffer's range check returns zeros for the latter, so rows past M/N, chunks past
-  // K and the conv's padding taps need no branches (a branch here makes the compiler wait for
-  // every outstanding load before the LDS stores, serialising the prefetch).
+  // K, the conv's padding taps and fetches past the last unit need no branches (a branch here
+  // makes the compiler wait for every outstanding load before the LDS stores, serialising the
+  // prefetch).
   constexpr uint32_t kOOB = 0x80000000u;
   constexpr int ES = (int)sizeof(T);
-  const __amdgpu_buffer_rsrc_t a_rsrc = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)(reinterpret_cast<const T*>(args.a) + bz * args.stride_a), (short)0, (int)args.a_bytes, 0x00020000);
-  const __amdgpu_buffer_rsrc_t b_rsrc = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)(reinterpret_cast<const T*>(args.b) + (MODE == MODE_CONV ? 0 : bz * args.stride_b)), (short)0,
-      (int)args.b_bytes, 0x00020000);
+  __amdgpu_buffer_rsrc_t a_rsrc, b_rsrc;
   uint32_t a_off[A_CH];
-#pragma unroll
-  for (int i = 0; i < A_CH; ++i) {
-    const int64_t row = m0 + (tid + i * 256) / CH_PER_ROW;
-    a_off[i] = row < args.M ? (uint32_t)((row * args.lda + kc) * ES) : kOOB;
-  }
   uint32_t b_off[MODE == MODE_NN ? 1 : B_CH];
   int conv_iy[MODE == MODE_CONV ? B_CH : 1], conv_ix[MODE == MODE_CONV ? B_CH : 1];
-  if constexpr (MODE == MODE_NT) {
+  uint32_t l_u = blockIdx.x;  // loader cursor: unit, K tile within the unit
+  int64_t l_k = 0;
+  GemmUnit lun{};
+  int64_t l_n0 = 0;
+
+  auto set_loader = [&]() {
+    lun = decode_unit<BM, BN>(args, l_u, nk_total);
+    l_n0 = lun.n0;
+    a_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(reinterpret_cast<const T*>(args.a) + lun.bz * args.stride_a), (short)0, (int)args.a_bytes, 0x00020000);
+    b_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(reinterpret_cast<const T*>(args.b) + (MODE == MODE_CONV ? 0 : lun.bz * args.stride_b)), (short)0,
+        (int)args.b_bytes, 0x00020000);
 #pragma unroll
-    for (int i = 0; i < B_CH; ++i) {
-      const int64_t row = n0 + (tid + i * 256) / CH_PER_ROW;
-      b_off[i] = row < args.N ? (uint32_t)((row * args.ldb + kc) * ES) : kOOB;
+    for (int i = 0; i < A_CH; ++i) {
+      const int64_t row = lun.m0 + (tid + i * 256) / CH_PER_ROW;
+      a_off[i] = row < args.M ? ((uint32_t)row * (uint32_t)args.lda + (uint32_t)kc) * (uint32_t)ES : kOOB;
     }
-  } else if constexpr (MODE == MODE_CONV) {
-    const int64_t OHW = args.OH * args.OW;
+    if constexpr (MODE == MODE_NT) {
 #pragma unroll
-    for (int i = 0; i < B_CH; ++i) {
-      const int64_t p = n0 + (tid + i * 256) / CH_PER_ROW;
-      const bool ok = p < args.N;
-      const int64_t pp = ok ? p : 0;
-      const int64_t img = pp / OHW, pix = pp - img * OHW;
-      const int oy = (int)(pix / args.OW), ox = (int)(pix - (pix / args.OW) * args.OW);
-      // rows past N get an origin no tap can reach, so every tap tests out of bounds
-      conv_iy[i] = ok ? oy * (int)args.sh - (int)args.ph : -(1 << 28);
-      conv_ix[i] = ox * (int)args.sw - (int)args.pw;
-      // element offset of x_nhwc[img, iy0, ix0, kc] (iy0/ix0 may lie in the padding; only
-      // in-bounds taps are ever turned into a real offset)
-      b_off[i] = (uint32_t)((((img * args.H) * args.W) * args.Cp) + kc);
+      for (int i = 0; i < B_CH; ++i) {
+        const int64_t row = lun.n0 + (tid + i * 256) / CH_PER_ROW;
+        b_off[i] = row < args.N ? ((uint32_t)row * (uint32_t)args.ldb + (uint32_t)kc) * (uint32_t)ES : kOOB;
+      }
+    } else if constexpr (MODE == MODE_CONV) {
+#pragma unroll
+      for (int i = 0; i < B_CH; ++i) {
+        const int64_t p = lun.n0 + (tid + i * 256) / CH_PER_ROW;
+        const bool ok = p < args.N;
+        const uint32_t pp = ok ? (uint32_t)p : 0u;
+        const uint32_t img = args.div_ohw.div(pp), pix = pp - img * args.div_ohw.d;
+        const uint32_t oyu = args.div_ow.div(pix);
+        const int oy = (int)oyu, ox = (int)(pix - oyu * args.div_ow.d);
+        // rows past N get an origin no tap can reach, so every tap tests out of bounds
+        conv_iy[i] = ok ? oy * (int)args.sh - (int)args.ph : -(1 << 28);
+        conv_ix[i] = ox * (int)args.sw - (int)args.pw;
+        // element offset of x_nhwc[img, iy0, ix0, kc] (iy0/ix0 may lie in the padding; only
+        // in-bounds taps are ever turned into a real offset)
+        b_off[i] = (img * (uint32_t)args.H * (uint32_t)args.W) * (uint32_t)args.Cp + (uint32_t)kc;
+      }
     }
-  }
+  };
+  if (l_u < args.units) set_loader();
 
   constexpr int NRB = MODE == MODE_NN ? B_CH_NN : B_CH;
-  // Two register stages: tile k+2 is requested while tile k is multiplied, so every global
-  // load has two tiles of MFMA work (plus a barrier) to arrive.
+  // Two register stages: step s+2 is requested while step s is multiplied, so every global
+  // load has two steps of MFMA work (plus a barrier) to arrive.
   uint4 ra0[A_CH], rb0[NRB], ra1[A_CH], rb1[NRB];
 
   auto bload = [&](const __amdgpu_buffer_rsrc_t& r, uint32_t off) -> uint4 {
     return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
   };
 
-  auto load_tiles = [&](int64_t k0, uint4(&ra)[A_CH], uint4(&rb)[NRB]) {
-    const bool kin = k0 + kc < args.K;  // K % VEC == 0: a chunk is entirely in or out
+  // Fetches the loader cursor's tile into (ra, rb) and advances the cursor.  Past the last
+  // unit every offset is kOOB (the loads return zeros and are never consumed).
+  auto load_next = [&](uint4(&ra)[A_CH], uint4(&rb)[NRB]) {
+    const bool live = l_u < args.units;
+    const int64_t k0 = (lun.kt0 + l_k) * BK;
+    const bool kin = live && k0 + kc < args.K;  // K % VEC == 0: a chunk is entirely in or out
     const uint32_t kb = (uint32_t)(k0 * ES);
 #pragma unroll
     for (int i = 0; i < A_CH; ++i) ra[i] = bload(a_rsrc, (kin && a_off[i] != kOOB) ? a_off[i] + kb : kOOB);
@@ -197,8 +342,8 @@ __global__ __launch_bounds__(256) void gemm_kernel(const GemmArgs args) {
 #pragma unroll
       for (int i = 0; i < B_CH_NN; ++i) {
         const int c = tid + i * 256;
-        const int64_t k = k0 + c / NB_CH_ROW, n = n0 + (c % NB_CH_ROW) * VEC;
-        const bool ok = k < args.K && n < args.N;  // N % VEC == 0: chunks are whole
+        const int64_t k = k0 + c / NB_CH_ROW, n = l_n0 + (c % NB_CH_ROW) * VEC;
+        const bool ok = live && k < args.K && n < args.N;  // N % VEC == 0: chunks are whole
         rb[i] = bload(b_rsrc, ok ? (uint32_t)((k * args.ldb + n) * ES) : kOOB);
       }
     } else {
@@ -223,6 +368,12 @@ __global__ __launch_bounds__(256) void gemm_kernel(const GemmArgs args) {
         const uint32_t off = (b_off[i] + (uint32_t)((iy * W + ix) * Cp + ch)) * (uint32_t)ES;
         rb[i] = bload(b_rsrc, ok ? off : kOOB);
       }
+    }
+    // advance (uniform across the workgroup)
+    if (live && ++l_k == lun.nkt) {
+      l_k = 0;
+      l_u += G;
+      if (l_u < args.units) set_loader();
     }
   };
 
@@ -252,14 +403,16 @@ __global__ __launch_bounds__(256) void gemm_kernel(const GemmArgs args) {
   };
 
   floatx16 acc[FM][FN];
+  auto zero_acc = [&]() {
 #pragma unroll
-  for (int i = 0; i < FM; ++i)
+    for (int i = 0; i < FM; ++i)
 #pragma unroll
-    for (int j = 0; j < FN; ++j)
+      for (int j = 0; j < FN; ++j)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+        for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+  };
+  zero_acc();
 
-  const int64_t nk = ceil_div(args.K, BK);
   auto compute = [&](int buf) {
     const T* a_base = &As[buf][(wm * WM + (lane & 31)) * LDK];
     const T* b_base = &Bs[buf][(wn * WN + (lane & 31)) * LDK];
@@ -272,148 +425,98 @@ __global__ __launch_bounds__(256) void gemm_kernel(const GemmArgs args) {
           acc[i][j] = Mfma<T>::fma(b_base + j * 32 * LDK, a_base + i * 32 * LDK, kk, lane, acc[i][j]);
     }
   };
-  load_tiles(0, ra0, rb0);
-  if (nk > 1) load_tiles(BK, ra1, rb1);
-  store_tiles(0, ra0, rb0);
-  __syncthreads();
-  for (int64_t kt = 0; kt < nk; kt += 2) {
-    // even tile kt in buffer 0; tile kt+1 is landing in stage 1
-    if (kt + 2 < nk) load_tiles((kt + 2) * BK, ra0, rb0);
-    compute(0);
-    if (kt + 1 < nk) store_tiles(1, ra1, rb1);
-    __syncthreads();
-    if (kt + 1 >= nk) break;
-    // odd tile kt+1 in buffer 1; tile kt+2 is landing in stage 0
-    if (kt + 3 < nk) load_tiles((kt + 3) * BK, ra1, rb1);
-    compute(1);
-    if (kt + 2 < nk) store_tiles(0, ra0, rb0);
-    __syncthreads();
-  }
 
-  // ---- epilogue.  Fragment (i, j), register r of lane l holds C[row][col] with
-  //      row = m0 + wm*WM + i*32 + l%32,
+  // ---- epilogue of the compute cursor's unit.  Fragment (i, j), register r of lane l holds
+  //      C[row][col] with row = m0 + wm*WM + i*32 + l%32,
   //      col = n0 + wn*WN + j*32 + 8*(r/4) + 4*(l/32) + r%4     (4 consecutive cols per r/4).
-  // Values are narrowed once, except where a fused activation or residual needs the narrowed
-  // intermediate the unfused op sequence would have produced.
-  T* Cptr = reinterpret_cast<T*>(args.c);
-  const int M = (int)args.M, N = (int)args.N;
   const int lane_col = 4 * (lane >> 5);
+  auto finish_unit = [&](const GemmUnit& un) {
+    const int M = (int)args.M;
 #pragma unroll
-  for (int i = 0; i < FM; ++i) {
-    const int row = (int)m0 + wm * WM + i * 32 + (lane & 31);
-    if (row >= M) continue;
-    if constexpr (EPI == EPI_LINEAR) {
-      const T* bias = reinterpret_cast<const T*>(args.bias);
-      const T* res = args.residual ? reinterpret_cast<const T*>(args.residual) + (int64_t)row * args.ld_res : nullptr;
-      T* crow = Cptr + (int64_t)row * args.ldc;
-      const bool plain = args.act == 0 && res == nullptr;
+    for (int i = 0; i < FM; ++i) {
+      const int row = (int)un.m0 + wm * WM + i * 32 + (lane & 31);
+      const bool row_ok = row < M;
 #pragma unroll
       for (int j = 0; j < FN; ++j) {
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
-          const int col0 = (int)n0 + wn * WN + j * 32 + 8 * g + lane_col;
-          if (col0 >= N) continue;
+          const int col0 = (int)un.n0 + wn * WN + j * 32 + 8 * g + lane_col;
           float v[4];
 #pragma unroll
           for (int t = 0; t < 4; ++t) v[t] = acc[i][j][4 * g + t];
-          if (col0 + 4 <= N) {
-            if (bias) {
-#pragma unroll
-              for (int t = 0; t < 4; ++t) v[t] += Elem<T>::load(bias, col0 + t);
-            }
-            if (!plain) {
-#pragma unroll
-              for (int t = 0; t < 4; ++t) {
-                float x = Elem<T>::round_trip(v[t]);
-                if (args.act) x = apply_act<T>(args.act, x);
-                if (res) x = Elem<T>::round_trip(x) + Elem<T>::load(res, col0 + t);
-                v[t] = x;
-              }
-            }
-            store4<T>(crow + col0, v, ((uintptr_t)(crow + col0) & (4 * sizeof(T) - 1)) == 0);
-          } else {
-            for (int t = 0; t < 4 && col0 + t < N; ++t) {
-              float x = v[t];
-              if (bias) x += Elem<T>::load(bias, col0 + t);
-              if (!plain) {
-                x = Elem<T>::round_trip(x);
-                if (args.act) x = apply_act<T>(args.act, x);
-                if (res) x = Elem<T>::round_trip(x) + Elem<T>::load(res, col0 + t);
-              }
-              Elem<T>::store(crow, col0 + t, x);
-            }
-          }
-        }
-      }
-    } else if constexpr (EPI == EPI_GEMM) {
-      const T* cin = reinterpret_cast<const T*>(args.c_in);
-      T* crow = Cptr + bz * args.stride_c + (int64_t)row * args.ldc;
-      const T* cinrow = cin ? cin + bz * args.stride_c_in + (int64_t)row * args.c_in_rs : nullptr;
-#pragma unroll
-      for (int j = 0; j < FN; ++j) {
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const int col0 = (int)n0 + wn * WN + j * 32 + 8 * g + lane_col;
-          if (col0 >= N) continue;
-          float v[4];
-#pragma unroll
-          for (int t = 0; t < 4; ++t) {
-            float x = acc[i][j][4 * g + t] * args.alpha;
-            if (cinrow && col0 + t < N)
-              x = Elem<T>::round_trip(args.beta * Elem<T>::load(cinrow, (int64_t)(col0 + t) * args.c_in_cs)) + x;
-            v[t] = x;
-          }
-          if (col0 + 4 <= N) {
-            store4<T>(crow + col0, v, ((uintptr_t)(crow + col0) & (4 * sizeof(T) - 1)) == 0);
-          } else {
-            for (int t = 0; t < 4 && col0 + t < N; ++t) Elem<T>::store(crow, col0 + t, v[t]);
-          }
-        }
-      }
-    } else {
-      // conv: row = output channel, col = output pixel (image-major); NCHW store.
-      const int OHW = (int)(args.OH * args.OW);
-      const T* bias = reinterpret_cast<const T*>(args.bias);
-      const T* res = reinterpret_cast<const T*>(args.residual);
-      const float bv = bias ? Elem<T>::load(bias, row) : 0.0f;
-#pragma unroll
-      for (int j = 0; j < FN; ++j) {
-        // A fragment's 32 pixels lie in one image when OHW is a multiple of 32 (every SD
-        // level); one division per fragment then addresses all of them.
-        const int frag0 = (int)n0 + wn * WN + j * 32;
-        if (frag0 >= N) continue;
-        if (OHW % 32 == 0) {
-          const int img = frag0 / OHW;
-          const int64_t base = ((int64_t)img * M + row) * OHW + (frag0 - img * OHW) + lane_col;
-#pragma unroll
-          for (int g = 0; g < 4; ++g) {
-            if (frag0 + 8 * g + lane_col >= N) continue;
-            float v[4];
-            const int64_t addr = base + 8 * g;
-#pragma unroll
-            for (int t = 0; t < 4; ++t) {
-              float x = acc[i][j][4 * g + t] + bv;
-              if (res) x = Elem<T>::round_trip(x) + Elem<T>::load(res, addr + t);
-              v[t] = x;
-            }
-            store4<T>(Cptr + addr, v, ((uintptr_t)(Cptr + addr) & (4 * sizeof(T) - 1)) == 0);
-          }
-        } else {
-#pragma unroll
-          for (int g = 0; g < 4; ++g) {
-            for (int t = 0; t < 4; ++t) {
-              const int c = frag0 + 8 * g + lane_col + t;
-              if (c >= N) break;
-              const int im = c / OHW, px = c - im * OHW;
-              const int64_t addr = ((int64_t)im * M + row) * OHW + px;
-              float x = acc[i][j][4 * g + t] + bv;
-              if (res) x = Elem<T>::round_trip(x) + Elem<T>::load(res, addr);
-              Elem<T>::store(Cptr, addr, x);
+          if (row_ok) {
+            if (args.ksplit > 1) {
+              if (col0 < (int)args.N)
+                *reinterpret_cast<float4*>(args.partial + (un.split * args.M + row) * args.ld_partial + col0) =
+                    make_float4(v[0], v[1], v[2], v[3]);
+            } else {
+              emit4<T, EPI, ACT>(args, un.bz, row, col0, v);
             }
           }
         }
       }
     }
+  };
+
+  // compute cursor
+  uint32_t c_u = blockIdx.x;
+  int64_t c_k = 0;
+  if (c_u >= args.units) return;  // (the launcher sizes the grid to at most `units`)
+  GemmUnit cun = decode_unit<BM, BN>(args, c_u, nk_total);
+  // Multiplies the step in LDS buffer `buf`; at a unit's last K tile writes its results and
+  // moves on.  Returns false after the workgroup's last unit.
+  auto step = [&](int buf) -> bool {
+    compute(buf);
+    if (++c_k == cun.nkt) {
+      finish_unit(cun);
+      zero_acc();
+      c_k = 0;
+      c_u += G;
+      if (c_u >= args.units) return false;
+      cun = decode_unit<BM, BN>(args, c_u, nk_total);
+    }
+    return true;
+  };
+
+  load_next(ra0, rb0);
+  load_next(ra1, rb1);
+  store_tiles(0, ra0, rb0);
+  __syncthreads();
+  while (true) {
+    // even step in buffer 0; the next step is landing in stage 1
+    load_next(ra0, rb0);
+    if (!step(0)) break;
+    store_tiles(1, ra1, rb1);
+    __syncthreads();
+    // odd step in buffer 1; the next step is landing in stage 0
+    load_next(ra1, rb1);
+    if (!step(1)) break;
+    store_tiles(0, ra0, rb0);
+    __syncthreads();
+  }
+}
+
+// Sums the K slices of a split GEMM in slice order and applies the epilogue; one thread per
+// 4 consecutive outputs of a row.
+template <typename T, int EPI, int ACT>
+__global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(const GemmArgs args) {
+  const int64_t n4 = ceil_div(args.N, 4);
+  const int64_t total = args.M * n4;
+  const int64_t slice = args.M * args.ld_partial;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
+    const int row = (int)(i / n4);
+    const int col0 = (int)(i - (int64_t)row * n4) * 4;
+    const float* p = args.partial + (int64_t)row * args.ld_partial + col0;
+    float4 s = *reinterpret_cast<const float4*>(p);
+    for (int64_t k = 1; k < args.ksplit; ++k) {
+      const float4 t = *reinterpret_cast<const float4*>(p + k * slice);
+      s.x += t.x;
+      s.y += t.y;
+      s.z += t.z;
+      s.w += t.w;
+    }
+    float v[4] = {s.x, s.y, s.z, s.w};
+    emit4<T, EPI, ACT>(args, 0, row, col0, v);
   }
 }
 

@@ -255,6 +255,68 @@ def test_conv2d(dt, cfg):
     assert rel(val(got), val(orc.conv2d(x, w, b, **kw))) <= TOL[dt]
 
 
+def test_fp16_narrowing_in_gemm_epilogue_is_exact():
+    """K = 1 makes every output an exact fp32 product x*w, so the only rounding is the fp16
+    narrowing in the epilogue: it must reproduce mtorch's half-away-from-zero rule bit for bit
+    on every finite half times factors that create ties (normal and subnormal results) and
+    overflow."""
+    bits = np.arange(65536, dtype=np.uint16)
+    finite = bits[(bits & 0x7C00) != 0x7C00]
+    factors = np.array([1.0, 1.0 + 2.0**-10, 1.5, 0.75 + 2.0**-11, 3.0, 2.0**-10, 2.0**-13 * 3, 2.0**-20,
+                        1.0 + 2.0**-5, 0.1, 2.0**10 + 1.0, 33.0], dtype=np.float32)
+    x = finite.reshape(-1, 1)
+    w = orc.f2h(factors).reshape(-1, 1)
+    got = host(F.linear(dev(x), dev(w)))
+    ref = orc.linear(x, w)
+    assert got.dtype == np.uint16 and np.array_equal(got, ref)
+
+
+@pytest.mark.parametrize("dt", ["float32", "float16"])
+def test_split_k_paths(dt):
+    """Shapes whose output tiles cannot fill the chip while K is long take the split-K path
+    (fp32 slices reduced in order, then the epilogue): conv with bias + residual, linear with a
+    fused activation + residual and a ragged N, and a 2-D addmm."""
+    g = Gen(61)
+    x = g.randn((1, 256, 4, 4), dt)
+    w = g.randn((96, 256, 3, 3), dt, 1.0 / 48)
+    b = g.randn((96,), dt)
+    r = g.randn((1, 96, 4, 4), dt)
+    got = host(F.conv2d_residual(dev(x), dev(w), dev(b), dev(r), padding=1))
+    ref = orc.binary(orc.conv2d(x, w, b, padding=1), r, "add")
+    assert rel(val(got), val(ref)) <= TOL[dt]
+    xl = g.randn((8, 2048), dt)
+    wl = g.randn((70, 2048), dt, 1.0 / 45)
+    bl = g.randn((70,), dt)
+    rl = g.randn((8, 70), dt)
+    lin = orc.linear(xl, wl, bl)
+    assert rel(val(host(F.linear_gelu(dev(xl), dev(wl), dev(bl)))), val(orc.gelu(lin))) <= TOL[dt]
+    got = host(F.linear_residual(dev(xl), dev(wl), dev(bl), dev(rl)))
+    assert rel(val(got), val(orc.binary(lin, rl, "add"))) <= TOL[dt]
+    inp = g.randn((36,), dt)
+    m1 = g.randn((8, 4096), dt)
+    m2 = g.randn((4096, 36), dt, 1.0 / 64)
+    got = host(mt.addmm(dev(inp), dev(m1), dev(m2), beta=0.5, alpha=1.5))
+    assert rel(val(got), val(orc.addmm(inp, m1, m2, 0.5, 1.5))) <= TOL[dt]
+
+
+@pytest.mark.parametrize("dt", ["float32", "float16"])
+def test_conv2d_packed_weight_follows_inplace_writes(dt):
+    """The packed weight cached on the weight's storage is rebuilt after copy_/fill_."""
+    g = Gen(62)
+    x = g.randn((2, 24, 9, 9), dt)
+    w1 = g.randn((16, 24, 3, 3), dt, 0.1)
+    w2 = g.randn((16, 24, 3, 3), dt, 0.1)
+    xd, wd = dev(x), dev(w1)
+    first = host(F.conv2d(xd, wd, padding=1))
+    assert np.array_equal(first, host(F.conv2d(xd, wd, padding=1)))
+    assert rel(val(first), val(orc.conv2d(x, w1, None, padding=1))) <= TOL[dt]
+    wd.copy_(dev(w2))
+    assert rel(val(host(F.conv2d(xd, wd, padding=1))), val(orc.conv2d(x, w2, None, padding=1))) <= TOL[dt]
+    wd.fill_(0.25)
+    w3 = np.full_like(w2, orc.f2h(np.float32(0.25))[0] if dt == "float16" else 0.25)
+    assert rel(val(host(F.conv2d(xd, wd, padding=1))), val(orc.conv2d(x, w3, None, padding=1))) <= TOL[dt]
+
+
 @pytest.mark.parametrize("dt", ["float32", "float16"])
 def test_conv2d_residual_epilogue(dt):
     g = Gen(51)
