@@ -17,7 +17,6 @@
 
 #include <algorithm>
 #include <cmath>
-#include <cstdlib>
 
 #include "common.h"
 
@@ -63,8 +62,7 @@ constexpr uint32_t kOOB = 0x80000000u;
 // DVB = ceil(DK/32) 32-row blocks.  VEC: E and Ev are multiples of 8 and every row stride a
 // multiple of 8 elements with 16-byte aligned bases, so K/V/Q move in 16-byte chunks.
 // MASK: the mask kind (MTHIP_MASK_*) fixed at compile time, or -1 to read it at run time.
-// WAVES: wave64s per workgroup (32 queries each); short sequences use fewer so more
-// workgroups spread over the CUs.
+// WAVES: wave64s per workgroup (32 queries each).
 template <int DK, bool VEC, int MASK, int WAVES>
 __global__ __launch_bounds__(64 * WAVES) void flash_fwd_f16_kernel(const FlashArgs a) {
   constexpr int NT = 64 * WAVES;
@@ -362,26 +360,12 @@ void launch_flash_w(const FlashArgs& a, int64_t bh, hipStream_t s, bool vec) {
   }
 }
 
-// 4 waves (128 queries) per workgroup when that gives at least one workgroup per CU,
-// otherwise two waves so short sequences spread over twice as many workgroups.  (A single
-// wave per workgroup stages the whole K/V tile alone and needs more registers than the
-// extra workgroups win back.)
-// MTHIP_FLASH_WAVES=2|4 overrides the choice (for tuning).
-int flash_waves_override() {
-  static const int v = [] {
-    const char* e = std::getenv("MTHIP_FLASH_WAVES");
-    return e ? std::atoi(e) : 0;
-  }();
-  return v;
-}
-
+// 4 waves (128 queries) per workgroup.  Measured on every SD shape (self/cross attention at
+// 64x64, 32x32, 16x16 latents), 4 waves were at least as fast as 2 even where they leave CUs
+// idle: each wave then stages a quarter of the K/V tile, and the shared tile serves 128 queries.
 template <int DK>
 void launch_flash(const FlashArgs& a, int64_t bh, hipStream_t s, bool vec) {
-  const int forced = flash_waves_override();
-  if (forced == 4 || (forced != 2 && ceil_div(a.Lq, 128) * bh >= 256))
-    launch_flash_w<DK, 4>(a, bh, s, vec);
-  else
-    launch_flash_w<DK, 2>(a, bh, s, vec);
+  launch_flash_w<DK, 4>(a, bh, s, vec);
 }
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }

@@ -139,7 +139,10 @@ int mthip_device_info(int device, char* name, size_t name_len, int* cu_count, si
   hipDeviceProp_t prop;
   MTHIP_CHECK_HIP(hipGetDeviceProperties(&prop, device));
   if (name && name_len) {
-    std::snprintf(name, name_len, "%s (%s)", prop.name, prop.gcnArchName);
+    // The marketing name comes from libdrm's amdgpu.ids table and is empty where that file is
+    // missing; the architecture name and CU count always identify the part.
+    std::snprintf(name, name_len, "%s (%s, %d CUs)", prop.name[0] ? prop.name : "AMD GPU", prop.gcnArchName,
+                  prop.multiProcessorCount);
   }
   if (cu_count) *cu_count = prop.multiProcessorCount;
   if (total_mem) *total_mem = prop.totalGlobalMem;
