@@ -205,6 +205,15 @@ int mthip_conv2d_prepacked(int device, int dtype, const void* x, const void* wp,
                            int64_t B, int64_t C, int64_t H, int64_t W, int64_t O, int64_t KH, int64_t KW,
                            int64_t stride_h, int64_t stride_w, int64_t pad_h, int64_t pad_w,
                            int64_t dil_h, int64_t dil_w, const void* residual);
+/* The same conv with the input already channels-last: x_nhwc[B][H][W][Cp] (Cp as for the
+ * packed weight, channels C..Cp-1 zero), e.g. as written by mthip_group_norm_nhwc; the output
+ * (and residual) stay NCHW.  This is the GroupNorm -> SiLU -> conv hand-off of every SD ResNet
+ * block: the normalised activation is written once, in the layout the conv reads, instead of
+ * NCHW plus a transposing copy.  Launches only the GEMM. */
+int mthip_conv2d_nhwc(int device, int dtype, const void* x_nhwc, const void* wp, const void* b, void* y,
+                      int64_t B, int64_t C, int64_t H, int64_t W, int64_t O, int64_t KH, int64_t KW,
+                      int64_t stride_h, int64_t stride_w, int64_t pad_h, int64_t pad_w,
+                      int64_t dil_h, int64_t dil_w, const void* residual);
 
 /* ===================================================================== attention */
 
@@ -233,6 +242,11 @@ int mthip_sdpa(int device, int dtype, const void* q, const int64_t* qs, const vo
 int mthip_group_norm(int device, int dtype, const void* x, const void* weight, const void* bias,
                      void* y, int64_t B, int64_t C, int64_t inner, int64_t groups, double eps,
                      int fuse_silu);
+/* The same values written channels-last for mthip_conv2d_nhwc: y_nhwc[B][HW][Cp], Cp = C
+ * rounded up to 8 (F16) or 4 (F32) channels, the padding channels zero.  x stays NCHW. */
+int mthip_group_norm_nhwc(int device, int dtype, const void* x, const void* weight, const void* bias,
+                          void* y_nhwc, int64_t B, int64_t C, int64_t HW, int64_t groups, double eps,
+                          int fuse_silu);
 
 /* layer_norm over the trailing N elements of contiguous x[rows, N] (tensor.cpp:17386-17708;
  * py_layer_norm module.cpp:7461-7516); weight/bias [N] or NULL.  fp16 uses the two-pass

@@ -63,10 +63,14 @@ _SIGNATURES = {
     "mthip_conv2d_pack_weight": (_int, [_int, _int, _c_void_p, _c_void_p, _i64, _i64, _i64, _i64]),
     "mthip_conv2d_prepacked": (_int, [_int, _int, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i64,
                                       _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _c_void_p]),
+    "mthip_conv2d_nhwc": (_int, [_int, _int, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i64,
+                                 _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _c_void_p]),
     "mthip_sdpa": (_int, [_int, _int, _c_void_p, _i64p, _c_void_p, _i64p, _c_void_p, _i64p, _c_void_p,
                           _i64, _i64, _i64, _i64, _i64, _i64, _i64, _int, _int, _c_void_p, _i64p, _int, _dbl]),
     "mthip_group_norm": (_int, [_int, _int, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i64,
                                 _i64, _dbl, _int]),
+    "mthip_group_norm_nhwc": (_int, [_int, _int, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i64,
+                                     _i64, _dbl, _int]),
     "mthip_layer_norm": (_int, [_int, _int, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i64, _dbl]),
     "mthip_softmax_lastdim": (_int, [_int, _int, _c_void_p, _c_void_p, _i64, _i64, _int]),
     "mthip_generator_create": (_c_void_p, [ctypes.c_uint64]),

@@ -530,12 +530,10 @@ def _pair(v, name):
     return v
 
 
-def conv2d(x: Tensor, w: Tensor, b: Tensor = None, stride=1, padding=0, dilation=1, groups=1,
-           residual: Tensor = None) -> Tensor:
-    """mtorch::conv2d (tensor.cpp:26490-27528), binding py_conv2d (module.cpp:6912-6961);
-    string padding resolved as the Python layer's _conv2d does (mtorch/__init__.py:3280-3287)."""
-    _same_dtype("conv2d", [x, w, b], "tensors")
-    dev = _gpu("conv2d", x, w, b, residual)
+def _conv2d_plan(x: Tensor, w: Tensor, b: Tensor, stride, padding, dilation, groups):
+    """Argument checks and output geometry of mtorch::conv2d (tensor.cpp:26490-26560,
+    conv2d_output_size :25941, normalize_conv2d_pair :25901); string padding resolved as the
+    Python layer's _conv2d does (mtorch/__init__.py:3280-3287)."""
     if x.dim() not in (3, 4):
         raise ValueError("conv2d expects a 3-D or 4-D input tensor")
     if w.dim() != 4:
@@ -547,8 +545,7 @@ def conv2d(x: Tensor, w: Tensor, b: Tensor = None, stride=1, padding=0, dilation
     if sh <= 0 or sw <= 0 or dh <= 0 or dw <= 0:
         raise ValueError("conv2d stride and dilation must be positive")
     unbatched = x.dim() == 3
-    xb = x.unsqueeze(0) if unbatched else x
-    B, C, H, W = xb.shape
+    B, C, H, W = ([1] + list(x.shape)) if unbatched else list(x.shape)
     O, Cg, KH, KW = w.shape
     if isinstance(padding, str):
         if padding == "valid":
@@ -577,24 +574,76 @@ def conv2d(x: Tensor, w: Tensor, b: Tensor = None, stride=1, padding=0, dilation
     if OH <= 0 or OW <= 0:
         raise ValueError("conv2d output size must be positive")
     _float_dtype("conv2d", x.dtype)
-    xc = xb.contiguous()
+    return dict(B=B, C=C, H=H, W=W, O=O, KH=KH, KW=KW, sh=sh, sw=sw, ph=ph, pw=pw, dh=dh, dw=dw, OH=OH, OW=OW,
+                unbatched=unbatched)
+
+
+def conv2d(x: Tensor, w: Tensor, b: Tensor = None, stride=1, padding=0, dilation=1, groups=1,
+           residual: Tensor = None) -> Tensor:
+    """mtorch::conv2d (tensor.cpp:26490-27528), binding py_conv2d (module.cpp:6912-6961).
+    `residual` (same shape as the output) is added after the conv result is narrowed."""
+    _same_dtype("conv2d", [x, w, b], "tensors")
+    dev = _gpu("conv2d", x, w, b, residual)
+    p = _conv2d_plan(x, w, b, stride, padding, dilation, groups)
+    B, C, H, W, O, KH, KW = p["B"], p["C"], p["H"], p["W"], p["O"], p["KH"], p["KW"]
+    geo = (p["sh"], p["sw"], p["ph"], p["pw"], p["dh"], p["dw"])
+    xc = (x.unsqueeze(0) if p["unbatched"] else x).contiguous()
     wc = w.contiguous()
-    bc = b.contiguous() if b is not None else None
-    out = _empty([B, O, OH, OW], x.dtype, dev)
-    rc = None
-    if residual is not None:
-        if list(residual.shape) != list(out.shape):
-            raise ValueError("conv2d residual must have the output shape")
-        rc = residual.contiguous()
+    bc = _contig(b)
+    out = _empty([B, O, p["OH"], p["OW"]], x.dtype, dev)
+    rc = _conv_residual(residual, out)
     if out.numel():
         if groups == 1:
             wp = _conv_packed_weight(wc, dev, O, C, KH, KW)
             _lib.check(_L().mthip_conv2d_prepacked(dev, x.dtype.code, xc.data_ptr(), wp, _ptr(bc), out.data_ptr(), B,
-                                                   C, H, W, O, KH, KW, sh, sw, ph, pw, dh, dw, _ptr(rc)))
+                                                   C, H, W, O, KH, KW, *geo, _ptr(rc)))
         else:
             _lib.check(_L().mthip_conv2d(dev, x.dtype.code, xc.data_ptr(), wc.data_ptr(), _ptr(bc), out.data_ptr(), B,
-                                         C, H, W, O, KH, KW, sh, sw, ph, pw, dh, dw, groups, _ptr(rc)))
-    return out.squeeze(0) if unbatched else out
+                                         C, H, W, O, KH, KW, *geo, groups, _ptr(rc)))
+    return out.squeeze(0) if p["unbatched"] else out
+
+
+def _contig(t):
+    return t.contiguous() if t is not None else None
+
+
+def _conv_residual(residual, out):
+    if residual is None:
+        return None
+    if list(residual.shape) != list(out.shape):
+        raise ValueError("conv2d residual must have the output shape")
+    return residual.contiguous()
+
+
+def group_norm_silu_conv2d(x: Tensor, num_groups: int, gn_weight: Tensor, gn_bias: Tensor, eps, w: Tensor,
+                           b: Tensor = None, stride=1, padding=0, dilation=1, residual: Tensor = None) -> Tensor:
+    """conv2d(silu(group_norm(x, num_groups, gn_weight, gn_bias, eps)), w, b, ...) (+ residual):
+    the GroupNorm -> SiLU -> conv chain of an SD ResNet block (the reference runs it as three
+    ops, tensor.cpp:18643, 16480, 26490).  On the device the normalised activation is written
+    once, channels-last, in the layout the implicit-GEMM conv reads (mthip_group_norm_nhwc then
+    mthip_conv2d_nhwc); values equal the unfused sequence's."""
+    _same_dtype("group_norm", [x, gn_weight, gn_bias], "tensors")
+    _same_dtype("conv2d", [x, w, b], "tensors")
+    dev = _gpu("group_norm_silu_conv2d", x, gn_weight, gn_bias, w, b, residual)
+    if x.dim() != 4:
+        raise ValueError("group_norm_silu_conv2d expects a 4-D input tensor")
+    _group_norm_check(x, num_groups, gn_weight, gn_bias)
+    p = _conv2d_plan(x, w, b, stride, padding, dilation, 1)
+    B, C, H, W, O, KH, KW = p["B"], p["C"], p["H"], p["W"], p["O"], p["KH"], p["KW"]
+    out = _empty([B, O, p["OH"], p["OW"]], x.dtype, dev)
+    rc = _conv_residual(residual, out)
+    if out.numel():
+        L = _L()
+        vec = 8 if x.dtype is T.float16 else 4
+        Cp = -(-C // vec) * vec
+        xn = T._DeviceBuffer(B * H * W * Cp * x.dtype.itemsize, dev)
+        _lib.check(L.mthip_group_norm_nhwc(dev, x.dtype.code, x.contiguous().data_ptr(), _ptr(_contig(gn_weight)),
+                                           _ptr(_contig(gn_bias)), xn.ptr, B, C, H * W, num_groups, float(eps), 1))
+        wp = _conv_packed_weight(w.contiguous(), dev, O, C, KH, KW)
+        _lib.check(L.mthip_conv2d_nhwc(dev, x.dtype.code, xn.ptr, wp, _ptr(_contig(b)), out.data_ptr(), B, C, H, W, O,
+                                       KH, KW, p["sh"], p["sw"], p["ph"], p["pw"], p["dh"], p["dw"], _ptr(rc)))
+        del xn  # stream-ordered free: reused only by later work
+    return out
 
 
 def _conv_packed_weight(w: Tensor, dev: int, O: int, C: int, KH: int, KW: int) -> int:
@@ -744,18 +793,15 @@ def scaled_dot_product_attention(query: Tensor, key: Tensor, value: Tensor, attn
 # ------------------------------------------------------------------------------ normalisation
 
 
-def group_norm(x: Tensor, num_groups: int, weight: Tensor = None, bias: Tensor = None, eps=1e-5,
-               fuse_silu=False) -> Tensor:
-    """mtorch::group_norm (tensor.cpp:18643-18963), binding py_group_norm (module.cpp:7646-7693)."""
-    _same_dtype("group_norm", [x, weight, bias], "tensors")
-    dev = _gpu("group_norm", x, weight, bias)
+def _group_norm_check(x: Tensor, num_groups: int, weight: Tensor, bias: Tensor):
+    """Argument checks of mtorch::group_norm (tensor.cpp:18643-18700; binding module.cpp:7646-7693)."""
     if not x.dtype.is_floating_point:
         raise ValueError("group_norm expects a floating point input")
     if x.dim() < 2:
         raise ValueError("group_norm expected input rank of at least 2")
     if num_groups <= 0:
         raise ValueError("group_norm num_groups must be positive")
-    B, C = x.shape[0], x.shape[1]
+    C = x.shape[1]
     if C % num_groups != 0:
         raise ValueError("group_norm num_channels must be divisible by num_groups")
     inner = T._numel(x.shape[2:])
@@ -766,12 +812,21 @@ def group_norm(x: Tensor, num_groups: int, weight: Tensor = None, bias: Tensor =
     if bias is not None and list(bias.shape) != [C]:
         raise ValueError("group_norm bias must have shape [C]")
     _float_dtype("group_norm", x.dtype)
+    return inner
+
+
+def group_norm(x: Tensor, num_groups: int, weight: Tensor = None, bias: Tensor = None, eps=1e-5,
+               fuse_silu=False) -> Tensor:
+    """mtorch::group_norm (tensor.cpp:18643-18963), binding py_group_norm (module.cpp:7646-7693)."""
+    _same_dtype("group_norm", [x, weight, bias], "tensors")
+    dev = _gpu("group_norm", x, weight, bias)
+    inner = _group_norm_check(x, num_groups, weight, bias)
+    B, C = x.shape[0], x.shape[1]
     xc = x.contiguous()
     out = _empty(x.shape, x.dtype, dev)
     if out.numel():
-        _lib.check(_L().mthip_group_norm(dev, x.dtype.code, xc.data_ptr(), _ptr(weight and weight.contiguous()),
-                                         _ptr(bias and bias.contiguous()), out.data_ptr(), B, C, inner, num_groups,
-                                         float(eps), 1 if fuse_silu else 0))
+        _lib.check(_L().mthip_group_norm(dev, x.dtype.code, xc.data_ptr(), _ptr(_contig(weight)), _ptr(_contig(bias)),
+                                         out.data_ptr(), B, C, inner, num_groups, float(eps), 1 if fuse_silu else 0))
     return out
 
 
@@ -800,8 +855,8 @@ def layer_norm(x: Tensor, normalized_shape, weight: Tensor = None, bias: Tensor 
     xc = x.contiguous()
     out = _empty(x.shape, x.dtype, dev)
     if out.numel():
-        _lib.check(_L().mthip_layer_norm(dev, x.dtype.code, xc.data_ptr(), _ptr(weight and weight.contiguous()),
-                                         _ptr(bias and bias.contiguous()), out.data_ptr(), rows, N, float(eps)))
+        _lib.check(_L().mthip_layer_norm(dev, x.dtype.code, xc.data_ptr(), _ptr(_contig(weight)),
+                                         _ptr(_contig(bias)), out.data_ptr(), rows, N, float(eps)))
     return out
 
 

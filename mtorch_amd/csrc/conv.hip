@@ -99,6 +99,45 @@ int launch_pack_weight(const void* w, void* wp, int64_t O, int64_t C, int64_t KH
   return check_launch("pack_weight_kernel");
 }
 
+// The implicit GEMM over an input already staged channels-last: xp[B][H][W][Cp].
+template <typename T>
+int run_conv_gemm_nhwc(int device, int dtype, const void* xp, const void* wp, const void* b, void* y, int64_t B,
+                       int64_t C, int64_t H, int64_t W, int64_t O, int64_t KH, int64_t KW, int64_t sh, int64_t sw,
+                       int64_t ph, int64_t pw, int64_t dh, int64_t dw, const void* residual, hipStream_t s) {
+  const int64_t OH = (H + 2 * ph - dh * (KH - 1) - 1) / sh + 1;
+  const int64_t OW = (W + 2 * pw - dw * (KW - 1) - 1) / sw + 1;
+  if (B == 0 || OH <= 0 || OW <= 0) return MTHIP_OK;
+  const int64_t Cp = ceil_div(C, Mfma<T>::VEC) * Mfma<T>::VEC;
+  const int64_t K = KH * KW * Cp;
+  if (O * K * (int64_t)sizeof(T) >= (int64_t(1) << 31) || B * H * W * Cp * (int64_t)sizeof(T) >= (int64_t(1) << 31))
+    return fail(MTHIP_ERR_UNSUPPORTED, "mthip_conv2d: operands above 2 GiB are not supported");
+  GemmArgs a{};
+  a.M = O;
+  a.N = B * OH * OW;
+  a.K = K;
+  a.a = wp;
+  a.lda = K;
+  a.b = xp;
+  a.c = y;
+  a.bias = b;
+  a.residual = residual;
+  a.H = H;
+  a.W = W;
+  a.Cp = Cp;
+  a.OH = OH;
+  a.OW = OW;
+  a.KW = KW;
+  a.sh = sh;
+  a.sw = sw;
+  a.ph = ph;
+  a.pw = pw;
+  a.dh = dh;
+  a.dw = dw;
+  a.a_bytes = O * K * (int64_t)sizeof(T);
+  a.b_bytes = B * H * W * Cp * (int64_t)sizeof(T);
+  return launch_conv_gemm(device, dtype, a, s);
+}
+
 // groups == 1 with a packed weight: stage x as NHWC, then the implicit GEMM.
 template <typename T>
 int run_conv_gemm(int device, int dtype, const void* x, const void* wp, const void* b, void* y, int64_t B, int64_t C,
@@ -107,44 +146,18 @@ int run_conv_gemm(int device, int dtype, const void* x, const void* wp, const vo
   const int64_t OH = (H + 2 * ph - dh * (KH - 1) - 1) / sh + 1;
   const int64_t OW = (W + 2 * pw - dw * (KW - 1) - 1) / sw + 1;
   if (B == 0 || OH <= 0 || OW <= 0) return MTHIP_OK;
-  constexpr int VEC = Mfma<T>::VEC;
-  const int64_t Cp = ceil_div(C, VEC) * VEC;
+  const int64_t Cp = ceil_div(C, Mfma<T>::VEC) * Mfma<T>::VEC;
   const int64_t HW = H * W;
-  const int64_t K = KH * KW * Cp;
-  if (O * K * (int64_t)sizeof(T) >= (int64_t(1) << 31) || B * HW * Cp * (int64_t)sizeof(T) >= (int64_t(1) << 31))
+  if (B * HW * Cp * (int64_t)sizeof(T) >= (int64_t(1) << 31))
     return fail(MTHIP_ERR_UNSUPPORTED, "mthip_conv2d: operands above 2 GiB are not supported");
   void* xp = nullptr;
   if (int rc = mthip_malloc(device, (size_t)(B * HW * Cp) * sizeof(T), &xp)) return rc;
   dim3 grid((unsigned)ceil_div(HW, 32), (unsigned)ceil_div(Cp, 32), (unsigned)B);
   hipLaunchKernelGGL(nchw_to_nhwc_pad_kernel<T>, grid, dim3(256), 0, s, (const T*)x, (T*)xp, C, Cp, HW);
   int rc = check_launch("nchw_to_nhwc_pad_kernel");
-  if (rc == MTHIP_OK) {
-    GemmArgs a{};
-    a.M = O;
-    a.N = B * OH * OW;
-    a.K = K;
-    a.a = wp;
-    a.lda = K;
-    a.b = xp;
-    a.c = y;
-    a.bias = b;
-    a.residual = residual;
-    a.H = H;
-    a.W = W;
-    a.Cp = Cp;
-    a.OH = OH;
-    a.OW = OW;
-    a.KW = KW;
-    a.sh = sh;
-    a.sw = sw;
-    a.ph = ph;
-    a.pw = pw;
-    a.dh = dh;
-    a.dw = dw;
-    a.a_bytes = O * K * (int64_t)sizeof(T);
-    a.b_bytes = B * HW * Cp * (int64_t)sizeof(T);
-    rc = launch_conv_gemm(device, dtype, a, s);
-  }
+  if (rc == MTHIP_OK)
+    rc = run_conv_gemm_nhwc<T>(device, dtype, xp, wp, b, y, B, C, H, W, O, KH, KW, sh, sw, ph, pw, dh, dw, residual,
+                               s);
   mthip_free(device, xp);  // stream-ordered: reused only by work enqueued after this conv
   return rc;
 }
@@ -230,4 +243,24 @@ extern "C" int mthip_conv2d_prepacked(int device, int dtype, const void* x, cons
                                    pad_w, dil_h, dil_w, residual, s);
   return run_conv_gemm<float>(device, dtype, x, wp, b, y, B, C, H, W, O, KH, KW, stride_h, stride_w, pad_h, pad_w,
                               dil_h, dil_w, residual, s);
+}
+
+extern "C" int mthip_conv2d_nhwc(int device, int dtype, const void* x_nhwc, const void* wp, const void* b, void* y,
+                                 int64_t B, int64_t C, int64_t H, int64_t W, int64_t O, int64_t KH, int64_t KW,
+                                 int64_t stride_h, int64_t stride_w, int64_t pad_h, int64_t pad_w, int64_t dil_h,
+                                 int64_t dil_w, const void* residual) {
+  MTHIP_REQUIRE(dtype == MTHIP_F16 || dtype == MTHIP_F32, "mthip_conv2d_nhwc: dtype must be F16 or F32");
+  MTHIP_REQUIRE(B >= 0 && C > 0 && H > 0 && W > 0 && O > 0 && KH > 0 && KW > 0, "mthip_conv2d_nhwc: bad extents");
+  MTHIP_REQUIRE(stride_h > 0 && stride_w > 0 && dil_h > 0 && dil_w > 0 && pad_h >= 0 && pad_w >= 0,
+                "mthip_conv2d_nhwc: bad stride/padding/dilation");
+  MTHIP_REQUIRE(((uintptr_t)x_nhwc & 15) == 0 && ((uintptr_t)wp & 15) == 0,
+                "mthip_conv2d_nhwc: x_nhwc and wp must be 16-byte aligned");
+  hipStream_t s = stream_for(device);
+  if (!s) return MTHIP_ERR_HIP;
+  if (int rc = use_device(device)) return rc;
+  if (dtype == MTHIP_F16)
+    return run_conv_gemm_nhwc<uint16_t>(device, dtype, x_nhwc, wp, b, y, B, C, H, W, O, KH, KW, stride_h, stride_w,
+                                        pad_h, pad_w, dil_h, dil_w, residual, s);
+  return run_conv_gemm_nhwc<float>(device, dtype, x_nhwc, wp, b, y, B, C, H, W, O, KH, KW, stride_h, stride_w, pad_h,
+                                   pad_w, dil_h, dil_w, residual, s);
 }

@@ -40,7 +40,43 @@ __device__ __forceinline__ float block_sum256(float v, float* scratch /* [4] */)
 }
 
 // ------------------------------------------------------------------------------ group_norm
+// 16-byte vector of T as floats.
 template <typename T>
+struct Vec16 {
+  static constexpr int N = 16 / sizeof(T);
+  static __device__ __forceinline__ void load(const T* p, float (&f)[N]) {
+    const uint4 r = *reinterpret_cast<const uint4*>(p);
+    if constexpr (sizeof(T) == 2) {
+      const uint32_t w[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        f[2 * j] = h2f_bits((uint16_t)(w[j] & 0xffffu));
+        f[2 * j + 1] = h2f_bits((uint16_t)(w[j] >> 16));
+      }
+    } else {
+      f[0] = __uint_as_float(r.x);
+      f[1] = __uint_as_float(r.y);
+      f[2] = __uint_as_float(r.z);
+      f[3] = __uint_as_float(r.w);
+    }
+  }
+  static __device__ __forceinline__ void store(T* p, const float (&f)[N]) {
+    uint4 r;
+    if constexpr (sizeof(T) == 2) {
+      uint32_t w[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) w[j] = (uint32_t)f2h_fast(f[2 * j]) | ((uint32_t)f2h_fast(f[2 * j + 1]) << 16);
+      r = make_uint4(w[0], w[1], w[2], w[3]);
+    } else {
+      r = make_uint4(__float_as_uint(f[0]), __float_as_uint(f[1]), __float_as_uint(f[2]), __float_as_uint(f[3]));
+    }
+    *reinterpret_cast<uint4*>(p) = r;
+  }
+};
+
+// Per-chunk (sum, sum of squares) of one (sample, group) range.  VECT: the range and the chunk
+// bounds are whole 16-byte vectors.
+template <typename T, bool VECT>
 __global__ __launch_bounds__(256) void group_norm_stats_kernel(const T* __restrict__ x, float2* __restrict__ partial,
                                                                int64_t group_size, int64_t chunk, int splits) {
   __shared__ float red[8];
@@ -50,10 +86,23 @@ __global__ __launch_bounds__(256) void group_norm_stats_kernel(const T* __restri
   const int64_t end = min(begin + chunk, group_size);
   const T* base = x + bg * group_size;
   float s = 0.0f, ss = 0.0f;
-  for (int64_t i = begin + threadIdx.x; i < end; i += 256) {
-    const float v = Elem<T>::load(base, i);
-    s += v;
-    ss += v * v;
+  if constexpr (VECT) {
+    constexpr int V = Vec16<T>::N;
+    for (int64_t i = begin + (int64_t)threadIdx.x * V; i < end; i += 256 * V) {
+      float f[V];
+      Vec16<T>::load(base + i, f);
+#pragma unroll
+      for (int j = 0; j < V; ++j) {
+        s += f[j];
+        ss += f[j] * f[j];
+      }
+    }
+  } else {
+    for (int64_t i = begin + threadIdx.x; i < end; i += 256) {
+      const float v = Elem<T>::load(base, i);
+      s += v;
+      ss += v * v;
+    }
   }
   s = wave_sum(s);
   ss = wave_sum(ss);
@@ -67,58 +116,157 @@ __global__ __launch_bounds__(256) void group_norm_stats_kernel(const T* __restri
     partial[bg * splits + split] = make_float2(red[0] + red[1] + red[2] + red[3], red[4] + red[5] + red[6] + red[7]);
 }
 
+// stats[bg] = (mean, 1/sqrt(var + eps)) from the chunk partials; one wave per (sample, group).
+__global__ __launch_bounds__(64) void group_norm_finalize_kernel(const float2* __restrict__ partial,
+                                                                 float2* __restrict__ stats, int splits,
+                                                                 int64_t group_size, float eps) {
+  const int64_t bg = blockIdx.x;
+  float s = 0.0f, ss = 0.0f;
+  for (int i = threadIdx.x; i < splits; i += 64) {
+    const float2 p = partial[bg * splits + i];
+    s += p.x;
+    ss += p.y;
+  }
+  s = wave_sum(s);
+  ss = wave_sum(ss);
+  if (threadIdx.x == 0) {
+    const float n = (float)group_size;
+    const float mean = s / n;
+    const float var = fmaxf(0.0f, ss / n - mean * mean);
+    stats[bg] = make_float2(mean, 1.0f / sqrtf(var + eps));
+  }
+}
+
+// Normalised value of one element in the reference's per-dtype form, with the optional SiLU
+// applied to the narrowed normalised value (the unfused op sequence narrows in between).
 template <typename T>
+__device__ __forceinline__ float gn_value(float v, float mean, float inv, float gm, float bt, int fuse_silu) {
+  float out;
+  if constexpr (sizeof(T) == 2) {
+    // affine_float32_to_half_bits(scale = gamma*inv, shift = beta - mean*gamma*inv)
+    // (tensor.cpp:18768-18781).
+    const float scale = gm * inv;
+    const float shift = bt - mean * gm * inv;
+    out = v * scale + shift;
+  } else {
+    // (x - mean) * inv * gamma + beta (tensor.cpp:18834-18837).
+    out = (v - mean) * inv * gm + bt;
+  }
+  if (fuse_silu) out = apply_unary<T>(MTHIP_UNARY_SILU, Elem<T>::round_trip(out));
+  return out;
+}
+
+template <typename T, bool VECT>
 __global__ __launch_bounds__(256) void group_norm_apply_kernel(const T* __restrict__ x, const T* __restrict__ gamma,
                                                                const T* __restrict__ beta, T* __restrict__ y,
-                                                               const float2* __restrict__ partial, int64_t C,
+                                                               const float2* __restrict__ stats, int64_t C,
                                                                int64_t groups, int64_t inner, int64_t group_size,
-                                                               int64_t chunk, int splits, float eps, int fuse_silu) {
-  __shared__ float stats[2];
+                                                               int64_t chunk, float eps, int fuse_silu) {
   const int64_t bg = blockIdx.y;
   const int split = blockIdx.x;
-  if (threadIdx.x < 64) {
-    float s = 0.0f, ss = 0.0f;
-    for (int i = threadIdx.x; i < splits; i += 64) {
-      const float2 p = partial[bg * splits + i];
-      s += p.x;
-      ss += p.y;
-    }
-    s = wave_sum(s);
-    ss = wave_sum(ss);
-    if (threadIdx.x == 0) {
-      const float n = (float)group_size;
-      const float mean = s / n;
-      const float var = fmaxf(0.0f, ss / n - mean * mean);
-      stats[0] = mean;
-      stats[1] = 1.0f / sqrtf(var + eps);
-    }
-  }
-  __syncthreads();
-  const float mean = stats[0], inv = stats[1];
+  const float2 st = stats[bg];
+  const float mean = st.x, inv = st.y;
   const int64_t g = bg % groups;
   const int64_t gc = C / groups;
   const int64_t begin = (int64_t)split * chunk;
   const int64_t end = min(begin + chunk, group_size);
   const T* xb = x + bg * group_size;
   T* yb = y + bg * group_size;
-  for (int64_t i = begin + threadIdx.x; i < end; i += 256) {
-    const int64_t c = g * gc + i / inner;
-    const float gm = gamma ? Elem<T>::load(gamma, c) : 1.0f;
-    const float bt = beta ? Elem<T>::load(beta, c) : 0.0f;
-    const float v = Elem<T>::load(xb, i);
-    float out;
-    if constexpr (sizeof(T) == 2) {
-      // affine_float32_to_half_bits(scale = gamma*inv, shift = beta - mean*gamma*inv)
-      // (tensor.cpp:18768-18781).
-      const float scale = gm * inv;
-      const float shift = bt - mean * gm * inv;
-      out = v * scale + shift;
-    } else {
-      // (x - mean) * inv * gamma + beta (tensor.cpp:18834-18837).
-      out = (v - mean) * inv * gm + bt;
+  if constexpr (VECT) {
+    // inner % V == 0, so a vector never straddles two channels.
+    constexpr int V = Vec16<T>::N;
+    for (int64_t i = begin + (int64_t)threadIdx.x * V; i < end; i += 256 * V) {
+      const int64_t c = g * gc + i / inner;
+      const float gm = gamma ? Elem<T>::load(gamma, c) : 1.0f;
+      const float bt = beta ? Elem<T>::load(beta, c) : 0.0f;
+      float f[V];
+      Vec16<T>::load(xb + i, f);
+#pragma unroll
+      for (int j = 0; j < V; ++j) f[j] = gn_value<T>(f[j], mean, inv, gm, bt, fuse_silu);
+      Vec16<T>::store(yb + i, f);
     }
-    if (fuse_silu) out = apply_unary<T>(MTHIP_UNARY_SILU, Elem<T>::round_trip(out));
-    Elem<T>::store(yb, i, out);
+  } else {
+    for (int64_t i = begin + threadIdx.x; i < end; i += 256) {
+      const int64_t c = g * gc + i / inner;
+      const float gm = gamma ? Elem<T>::load(gamma, c) : 1.0f;
+      const float bt = beta ? Elem<T>::load(beta, c) : 0.0f;
+      Elem<T>::store(yb, i, gn_value<T>(Elem<T>::load(xb, i), mean, inv, gm, bt, fuse_silu));
+    }
+  }
+}
+
+// Same values written channels-last: y[b][p][0..Cp) with channels C..Cp-1 zero, the layout the
+// implicit-GEMM conv stages its input in.  A workgroup transposes a 64-channel x 64-pixel tile
+// through LDS: reads walk pixels of one channel, writes walk channels of one pixel.
+template <typename T>
+__global__ __launch_bounds__(256) void group_norm_apply_nhwc_kernel(const T* __restrict__ x,
+                                                                    const T* __restrict__ gamma,
+                                                                    const T* __restrict__ beta, T* __restrict__ y,
+                                                                    const float2* __restrict__ stats, int64_t C,
+                                                                    int64_t Cp, int64_t groups, int64_t HW,
+                                                                    int fuse_silu, int vec_io) {
+  constexpr int TP = 64 + 2;  // LDS row pitch (elements)
+  constexpr int V = Vec16<T>::N;
+  __shared__ T tile[64 * TP];
+  const int64_t b = blockIdx.z;
+  const int64_t p0 = (int64_t)blockIdx.x * 64, c0 = (int64_t)blockIdx.y * 64;
+  const int t = threadIdx.x;
+  {
+    const int cl = t >> 2, pl0 = (t & 3) * 16;
+    const int64_t c = c0 + cl;
+    float f[16];
+    if (c < C) {
+      const int64_t gc = C / groups;
+      const float2 st = stats[b * groups + c / gc];
+      const float gm = gamma ? Elem<T>::load(gamma, c) : 1.0f;
+      const float bt = beta ? Elem<T>::load(beta, c) : 0.0f;
+      const T* xr = x + (b * C + c) * HW + p0 + pl0;
+      if (vec_io && p0 + pl0 + 16 <= HW) {
+#pragma unroll
+        for (int j = 0; j < 16; j += V) {
+          float part[V];
+          Vec16<T>::load(xr + j, part);
+#pragma unroll
+          for (int k = 0; k < V; ++k) f[j + k] = part[k];
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < 16; ++j) f[j] = p0 + pl0 + j < HW ? Elem<T>::load(xr, j) : 0.0f;
+      }
+#pragma unroll
+      for (int j = 0; j < 16; ++j) f[j] = gn_value<T>(f[j], st.x, st.y, gm, bt, fuse_silu);
+    } else {
+#pragma unroll
+      for (int j = 0; j < 16; ++j) f[j] = 0.0f;
+    }
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      if constexpr (sizeof(T) == 2)
+        tile[(pl0 + j) * TP + cl] = f2h_fast(f[j]);
+      else
+        tile[(pl0 + j) * TP + cl] = f[j];
+    }
+  }
+  __syncthreads();
+  {
+    const int pl = t >> 2, cl0 = (t & 3) * 16;
+    const int64_t p = p0 + pl;
+    if (p < HW) {
+      T* yr = y + (b * HW + p) * Cp + c0 + cl0;
+      if (vec_io && c0 + cl0 + 16 <= Cp) {
+#pragma unroll
+        for (int j = 0; j < 16; j += V) {
+          T part[V];
+#pragma unroll
+          for (int k = 0; k < V; ++k) part[k] = tile[pl * TP + cl0 + j + k];
+          *reinterpret_cast<uint4*>(yr + j) = *reinterpret_cast<const uint4*>(part);
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < 16; ++j)
+          if (c0 + cl0 + j < Cp) yr[j] = tile[pl * TP + cl0 + j];
+      }
+    }
   }
 }
 
@@ -270,31 +418,59 @@ __global__ __launch_bounds__(256) void softmax_long_kernel(const T* __restrict__
   }
 }
 
+// Stats (chunked partials, then one wave per group), then the apply pass: NCHW in place of x's
+// layout (y_nhwc == false) or channels-last with Cp channels.
 template <typename T>
 int run_group_norm(int device, const void* x, const void* weight, const void* bias, void* y, int64_t B, int64_t C,
-                   int64_t inner, int64_t groups, double eps, int fuse_silu, hipStream_t s) {
+                   int64_t inner, int64_t groups, double eps, int fuse_silu, bool y_nhwc, int64_t Cp, hipStream_t s) {
   const int64_t group_size = (C / groups) * inner;
   const int64_t n_groups = B * groups;
   if (n_groups == 0 || group_size == 0) return MTHIP_OK;
   MTHIP_REQUIRE(n_groups <= 65535, "mthip_group_norm: batch*groups must be <= 65535");
+  constexpr int V = Vec16<T>::N;
+  const bool vect = ((uintptr_t)x % 16 == 0) && ((uintptr_t)y % 16 == 0) && inner % V == 0;
   // Aim for ~4096 workgroups in total, each streaming at least 2048 elements.
   int64_t splits = std::max<int64_t>(1, std::min<int64_t>(ceil_div(4096, n_groups), ceil_div(group_size, 2048)));
   splits = std::min<int64_t>(splits, 1024);
-  const int64_t chunk = ceil_div(group_size, splits);
+  int64_t chunk = ceil_div(group_size, splits);
+  if (vect) chunk = ceil_div(chunk, V) * V;
   splits = ceil_div(group_size, chunk);
-  void* partial = nullptr;
-  if (int rc = mthip_malloc(device, (size_t)(n_groups * splits) * sizeof(float2), &partial)) return rc;
+  void* ws = nullptr;
+  if (int rc = mthip_malloc(device, (size_t)(n_groups * (splits + 1)) * sizeof(float2), &ws)) return rc;
+  float2* partial = static_cast<float2*>(ws);
+  float2* stats = partial + n_groups * splits;
   dim3 grid((unsigned)splits, (unsigned)n_groups);
-  hipLaunchKernelGGL(group_norm_stats_kernel<T>, grid, dim3(256), 0, s, (const T*)x, (float2*)partial, group_size,
-                     chunk, (int)splits);
+  if (vect)
+    hipLaunchKernelGGL((group_norm_stats_kernel<T, true>), grid, dim3(256), 0, s, (const T*)x, partial, group_size,
+                       chunk, (int)splits);
+  else
+    hipLaunchKernelGGL((group_norm_stats_kernel<T, false>), grid, dim3(256), 0, s, (const T*)x, partial, group_size,
+                       chunk, (int)splits);
   int rc = check_launch("group_norm_stats_kernel");
   if (rc == MTHIP_OK) {
-    hipLaunchKernelGGL(group_norm_apply_kernel<T>, grid, dim3(256), 0, s, (const T*)x, (const T*)weight,
-                       (const T*)bias, (T*)y, (const float2*)partial, C, groups, inner, group_size, chunk, (int)splits,
-                       (float)eps, fuse_silu);
+    hipLaunchKernelGGL(group_norm_finalize_kernel, dim3((unsigned)n_groups), dim3(64), 0, s, (const float2*)partial,
+                       stats, (int)splits, group_size, (float)eps);
+    rc = check_launch("group_norm_finalize_kernel");
+  }
+  if (rc == MTHIP_OK) {
+    if (y_nhwc) {
+      dim3 g2((unsigned)ceil_div(inner, 64), (unsigned)ceil_div(Cp, 64), (unsigned)B);
+      // 16-byte row access: pixel rows and channel rows start on 16-byte boundaries.
+      const int vec_io = ((uintptr_t)x % 16 == 0) && ((uintptr_t)y % 16 == 0) && inner % V == 0 && Cp % V == 0;
+      hipLaunchKernelGGL(group_norm_apply_nhwc_kernel<T>, g2, dim3(256), 0, s, (const T*)x, (const T*)weight,
+                         (const T*)bias, (T*)y, (const float2*)stats, C, Cp, groups, inner, fuse_silu, vec_io);
+    } else if (vect) {
+      hipLaunchKernelGGL((group_norm_apply_kernel<T, true>), grid, dim3(256), 0, s, (const T*)x, (const T*)weight,
+                         (const T*)bias, (T*)y, (const float2*)stats, C, groups, inner, group_size, chunk, (float)eps,
+                         fuse_silu);
+    } else {
+      hipLaunchKernelGGL((group_norm_apply_kernel<T, false>), grid, dim3(256), 0, s, (const T*)x, (const T*)weight,
+                         (const T*)bias, (T*)y, (const float2*)stats, C, groups, inner, group_size, chunk, (float)eps,
+                         fuse_silu);
+    }
     rc = check_launch("group_norm_apply_kernel");
   }
-  mthip_free(device, partial);
+  mthip_free(device, ws);
   return rc;
 }
 
@@ -347,8 +523,24 @@ int mthip_group_norm(int device, int dtype, const void* x, const void* weight, c
   hipStream_t s = stream_for(device);
   if (!s) return MTHIP_ERR_HIP;
   if (int rc = use_device(device)) return rc;
-  if (dtype == MTHIP_F16) return run_group_norm<uint16_t>(device, x, weight, bias, y, B, C, inner, groups, eps, fuse_silu, s);
-  return run_group_norm<float>(device, x, weight, bias, y, B, C, inner, groups, eps, fuse_silu, s);
+  if (dtype == MTHIP_F16)
+    return run_group_norm<uint16_t>(device, x, weight, bias, y, B, C, inner, groups, eps, fuse_silu, false, C, s);
+  return run_group_norm<float>(device, x, weight, bias, y, B, C, inner, groups, eps, fuse_silu, false, C, s);
+}
+
+int mthip_group_norm_nhwc(int device, int dtype, const void* x, const void* weight, const void* bias, void* y_nhwc,
+                          int64_t B, int64_t C, int64_t HW, int64_t groups, double eps, int fuse_silu) {
+  MTHIP_REQUIRE(dtype == MTHIP_F16 || dtype == MTHIP_F32, "mthip_group_norm_nhwc: dtype must be F16 or F32");
+  MTHIP_REQUIRE(groups > 0 && C % groups == 0, "mthip_group_norm_nhwc: num_channels must be divisible by num_groups");
+  MTHIP_REQUIRE(B >= 0 && HW >= 0 && B <= 65535, "mthip_group_norm_nhwc: bad extents");
+  hipStream_t s = stream_for(device);
+  if (!s) return MTHIP_ERR_HIP;
+  if (int rc = use_device(device)) return rc;
+  const int64_t vec = dtype == MTHIP_F16 ? 8 : 4;
+  const int64_t Cp = ceil_div(C, vec) * vec;
+  if (dtype == MTHIP_F16)
+    return run_group_norm<uint16_t>(device, x, weight, bias, y_nhwc, B, C, HW, groups, eps, fuse_silu, true, Cp, s);
+  return run_group_norm<float>(device, x, weight, bias, y_nhwc, B, C, HW, groups, eps, fuse_silu, true, Cp, s);
 }
 
 int mthip_layer_norm(int device, int dtype, const void* x, const void* weight, const void* bias, void* y, int64_t rows,

@@ -59,6 +59,14 @@ def group_norm_silu(input, num_groups, weight=None, bias=None, eps=1e-5):
     return _ops.group_norm(input, num_groups, weight, bias, eps, fuse_silu=True)
 
 
+def group_norm_silu_conv2d(input, num_groups, gn_weight, gn_bias, eps, weight, bias=None, stride=1, padding=0,
+                           dilation=1, residual=None):
+    """conv2d(silu(group_norm(input, num_groups, gn_weight, gn_bias, eps)), weight, bias, ...)
+    (+ residual), with the normalised activation handed to the conv channels-last"""
+    return _ops.group_norm_silu_conv2d(input, num_groups, gn_weight, gn_bias, eps, weight, bias, stride, padding,
+                                       dilation, residual)
+
+
 def conv2d_residual(input, weight, bias, residual, stride=1, padding=0, dilation=1, groups=1):
     """conv2d(input, weight, bias, ...) + residual"""
     return _ops.conv2d(input, weight, bias, stride, padding, dilation, groups, residual=residual)

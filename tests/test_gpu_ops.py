@@ -344,7 +344,7 @@ def test_sdpa(dt, Lq, Lk, E):
 
 @pytest.mark.parametrize("L,Lk,E", [(4096, 4096, 40), (4096, 77, 40), (1024, 1024, 80), (256, 256, 160)])
 def test_sdpa_sd_shapes_query_subset(L, Lk, E):
-    """BASELINE configs[2] shapes ([2,8,L,E] fp16).  Every query row is independent, so the
+    """BASELINE.json configs[2] shapes ([2,8,L,E] fp16).  Every query row is independent, so the
     oracle checks a strided subset of rows of the full-size GPU result."""
     g = Gen(L + Lk + E)
     q = g.randn((2, 8, L, E), "float16")
@@ -423,6 +423,27 @@ def test_group_norm(dt, shape, groups):
     assert rel(val(got), val(ref)) <= TOL[dt]
     got = host(F.group_norm_silu(dev(x), groups, dev(w), dev(b), 1e-5))
     assert rel(val(got), val(orc.silu(ref))) <= TOL[dt]
+
+
+@pytest.mark.parametrize("dt", ["float32", "float16"])
+@pytest.mark.parametrize("B,C,H,W,O,G", [(2, 64, 16, 16, 48, 32), (1, 12, 9, 11, 8, 4), (2, 40, 8, 8, 40, 8)])
+def test_group_norm_silu_conv2d_channels_last_handoff(dt, B, C, H, W, O, G):
+    """GN -> SiLU written channels-last and consumed by the conv equals the three-op sequence
+    (channel padding, ragged pixel tiles and the residual epilogue included)."""
+    g = Gen(B * 1000 + C + O)
+    x = g.randn((B, C, H, W), dt)
+    gamma = g.randn((C,), dt)
+    beta = g.randn((C,), dt)
+    w = g.randn((O, C, 3, 3), dt, 1.0 / np.sqrt(9 * C))
+    b = g.randn((O,), dt)
+    r = g.randn((B, O, H, W), dt)
+    h = orc.silu(orc.group_norm(x, G, gamma, beta, 1e-5))
+    ref = orc.binary(orc.conv2d(h, w, b, padding=1), r, "add")
+    got = host(F.group_norm_silu_conv2d(dev(x), G, dev(gamma), dev(beta), 1e-5, dev(w), dev(b), padding=1,
+                                        residual=dev(r)))
+    assert rel(val(got), val(ref)) <= TOL[dt]
+    got = host(F.group_norm_silu_conv2d(dev(x), G, dev(gamma), dev(beta), 1e-5, dev(w), None, stride=2, padding=1))
+    assert rel(val(got), val(orc.conv2d(h, w, None, stride=2, padding=1))) <= TOL[dt]
 
 
 def test_sd_group_norm_scenario_fixture():
