@@ -1,6 +1,6 @@
 """Benchmark of mtorch's SD-UNet hot path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload resnet|linear_gelu] [--no-cpu]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload resnet|linear_gelu|copy_calibration] [--no-cpu]
 
 Default workload (fp16 leg): the SD ResNet sub-block on a 64x64
 latent at batch 2 -- x[2,320,64,64] -> GroupNorm(32, eps 1e-5, affine) -> SiLU ->
@@ -28,6 +28,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 PEAK = {"fp16_mfma_tflops": 2516.6, "fp32_tflops": 157.3, "hbm_gbs": 8000.0}
+CPU_CHANNELS = 128  # output channels of the CPU-baseline conv sample
 
 
 def _cpu_model():
@@ -68,12 +69,31 @@ def resnet_inputs(mt):
     return x, gamma, beta, w, b
 
 
+def _traffic(kernel_key):
+    """HBM bytes per launch of a kernel from the committed rocprofv3 --pmc summaries under
+    profiles/ (FETCH_SIZE and WRITE_SIZE per dispatch, each scaled by the copy-kernel
+    calibration recorded in the same file), or None when no summary is present."""
+    path = os.path.join(ROOT, "profiles", f"traffic_{kernel_key}.md")
+    try:
+        with open(path) as fh:
+            for line in fh:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return float(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
+
+
 def run_resnet(args):
-    import numpy as np
+    """One step = GroupNorm(32)+SiLU written channels-last, then the implicit-GEMM conv with bias
+    and residual, through the C ABI exactly as F.group_norm_silu_conv2d issues it.  HIP events
+    on the library's stream time every step and, inside it, the conv launch."""
+    import ctypes
 
     import mtorch_amd as mt
+    from mtorch_amd import _lib, _ops
+    from mtorch_amd import _tensor as T
 
-    F = mt.nn.functional
     x, gamma, beta, w, b = resnet_inputs(mt)
     # gamma = 1 + 0.1 N(0,1), beta = 0.1 N(0,1): formed on the device in fp32, then cast.
     xd = x.to("cuda").half()
@@ -81,25 +101,38 @@ def run_resnet(args):
     bd = (beta.to("cuda") * 0.1).half()
     wd = w.to("cuda").half()
     bbd = b.to("cuda").half()
+    L = _lib.lib()
+    B, C, H, W, O = 2, 320, 64, 64, 320
+    wp = _ops._conv_packed_weight(wd, 0, O, C, 3, 3)
+    xn = T._DeviceBuffer(B * H * W * C * 2, 0)
+    y = mt.empty(B, O, H, W, dtype=mt.float16, device="cuda")
+    ev = [(mt.cuda.Event(), mt.cuda.Event()) for _ in range(args.steps)]
 
-    def step():
-        h = F.group_norm_silu(xd, 32, gd, bd, 1e-5)
-        return F.conv2d_residual(h, wd, bbd, xd, padding=1)
-
-    h_fixed = F.group_norm_silu(xd, 32, gd, bd, 1e-5)
-
-    def conv_only():
-        return F.conv2d_residual(h_fixed, wd, bbd, xd, padding=1)
+    def step(marks=None):
+        _lib.check(L.mthip_group_norm_nhwc(0, _lib.F16, xd.data_ptr(), gd.data_ptr(), bd.data_ptr(), xn.ptr, B, C,
+                                           H * W, 32, 1e-5, 1))
+        if marks:
+            marks[0].record()
+        _lib.check(L.mthip_conv2d_nhwc(0, _lib.F16, xn.ptr, wp, bbd.data_ptr(), y.data_ptr(), B, C, H, W, O, 3, 3,
+                                       1, 1, 1, 1, 1, 1, xd.data_ptr()))
+        if marks:
+            marks[1].record()
 
     for _ in range(args.warmup):
         step()
     mt.cuda.synchronize()
+    start, end = mt.cuda.Event(), mt.cuda.Event()
     t0 = time.perf_counter()
-    ms_events = _time_events(step, args.steps)
+    start.record()
+    for i in range(args.steps):
+        step(ev[i])
+    end.record()
+    mt.cuda.synchronize()
     wall_ms = (time.perf_counter() - t0) * 1e3 / args.steps
-    conv_ms = _time_events(conv_only, args.steps)
-    flops = 2.0 * 2 * 320 * 64 * 64 * 320 * 9  # 15.10 GFLOP per step (conv)
-    value = flops / (ms_events * 1e-3) / 1e12
+    ms_step = start.elapsed_time(end) / args.steps
+    conv_ms = sum(a.elapsed_time(b_) for a, b_ in ev) / args.steps
+    flops = 2.0 * B * H * W * O * C * 9  # 15.10 GFLOP per step (the conv; GN/SiLU/add are not counted)
+    value = flops / (ms_step * 1e-3) / 1e12
     conv_tflops = flops / (conv_ms * 1e-3) / 1e12
     out = {
         "metric": "SD ResNet sub-block (GN32+SiLU+conv3x3 320->320+residual) fp16 TFLOP/s, batch 2, 64x64",
@@ -108,7 +141,7 @@ def run_resnet(args):
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(ms_events, 4),
+        "ms_per_step": round(ms_step, 4),
         "wall_ms_per_step": round(wall_ms, 4),
         "higher_is_better": True,
         "scaling": "weak",
@@ -118,24 +151,42 @@ def run_resnet(args):
         "config": {"workload": "configs[1] ResNet sub-block fp16: x[2,320,64,64], GN(32), SiLU, conv3x3 320->320, residual",
                    "batch": 2, "channels": 320, "hw": [64, 64]},
         "roofline": {
-            "kernel": "conv2d implicit-GEMM (gemm_kernel MODE_CONV) incl. its staging",
+            "kernel": "gemm_kernel<fp16, 64x64, MODE_CONV, EPI_CONV> (conv3x3 implicit GEMM, bias+residual fused)",
             "bound": "mfma",
             "achieved": round(conv_tflops, 3),
             "peak": PEAK["fp16_mfma_tflops"],
             "unit": "TFLOP/s",
             "frac": round(conv_tflops / PEAK["fp16_mfma_tflops"], 4),
-            "traffic": None,
+            "traffic": _traffic("conv_gemm_resnet_fp16"),
+            "kernel_ms": round(conv_ms, 5),
         },
     }
     if args.cpu:
         out["cpu_baseline"] = cpu_baseline_resnet(x, gamma, beta, w, b)
-    # parity spot check of the measured output against the oracle on a channel subset
     return out
+
+
+def run_copy_calibration(args):
+    """A plain streaming kernel of known size (fp32 negation over 256 MiB: 256 MiB read and
+    256 MiB written per launch) for scaling the FETCH_SIZE / WRITE_SIZE counters."""
+    import mtorch_amd as mt
+    from mtorch_amd import _lib
+
+    n = 64 << 20
+    x = mt.zeros(n, device="cuda")
+    y = mt.empty(n, device="cuda")
+    L = _lib.lib()
+    for _ in range(args.warmup + args.steps):
+        _lib.check(L.mthip_unary(0, 6, _lib.F32, x.data_ptr(), y.data_ptr(), n))
+    mt.cuda.synchronize()
+    return {"metric": "copy calibration", "bytes_read_per_launch": n * 4, "bytes_written_per_launch": n * 4,
+            "launches": args.warmup + args.steps}
 
 
 def cpu_baseline_resnet(x, gamma, beta, w, b):
     """The oracle's restatement of mtorch's Linux fp16 path, one core, on a bounded sample:
-    GroupNorm+SiLU on the full input and the conv for 16 of the 320 output channels."""
+    GroupNorm+SiLU on the full input and the conv for CPU_CHANNELS of the 320 output channels
+    (about 10 s of CPU work); the rate is the sample's conv FLOP over its time."""
     import numpy as np
 
     import oracle
@@ -143,21 +194,21 @@ def cpu_baseline_resnet(x, gamma, beta, w, b):
     xh = oracle.f2h(x.numpy())
     g = oracle.f2h((gamma.numpy().astype(np.float64) * 0.1 + 1.0).astype(np.float32))
     be = oracle.f2h((beta.numpy().astype(np.float64) * 0.1).astype(np.float32))
-    wh = oracle.f2h(w.numpy())[:16]
-    bh = oracle.f2h(b.numpy())[:16]
+    wh = oracle.f2h(w.numpy())[:CPU_CHANNELS]
+    bh = oracle.f2h(b.numpy())[:CPU_CHANNELS]
     os.sched_setaffinity(0, {sorted(os.sched_getaffinity(0))[0]})
     t0 = time.perf_counter()
     h = oracle.silu(oracle.group_norm(xh, 32, g, be, 1e-5))
     y = oracle.conv2d(h, wh, bh, padding=1)
-    oracle.binary(y, xh[:, :16], "add")
+    oracle.binary(y, np.ascontiguousarray(xh[:, :CPU_CHANNELS]), "add")
     dt = time.perf_counter() - t0
-    flops = 2.0 * 2 * 16 * 64 * 64 * 320 * 9
+    flops = 2.0 * 2 * CPU_CHANNELS * 64 * 64 * 320 * 9
     return {
         "value": round(flops / dt / 1e12, 6),
         "unit": "TFLOP/s",
         "cores": 1,
         "kind": "port",
-        "sample": f"fp16 GN32+SiLU on the full [2,320,64,64] input + conv3x3 for 16/320 output channels "
+        "sample": f"fp16 GN32+SiLU on the full [2,320,64,64] input + conv3x3 for {CPU_CHANNELS}/320 output channels "
                   f"+ residual; {dt:.2f} s on 1 core of {_cpu_model()} (nproc {os.cpu_count()})",
         "seconds": round(dt, 3),
     }
@@ -201,7 +252,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", default="resnet", choices=["resnet", "linear_gelu"])
+    ap.add_argument("--workload", default="resnet", choices=["resnet", "linear_gelu", "copy_calibration"])
     ap.add_argument("--no-cpu", dest="cpu", action="store_false")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -213,7 +264,8 @@ def main():
     if not mt.cuda.is_available():
         raise SystemExit("bench.py: no GPU visible to libmthip")
     with mt.no_grad():
-        out = run_resnet(args) if args.workload == "resnet" else run_linear_gelu(args)
+        run = {"resnet": run_resnet, "linear_gelu": run_linear_gelu, "copy_calibration": run_copy_calibration}
+        out = run[args.workload](args)
     out["device"] = mt.cuda.get_device_name(0)
     print(json.dumps(out), flush=True)
 

@@ -74,9 +74,10 @@ int launch_tile(int device, GemmArgs a, int64_t batch, hipStream_t s) {
   const int64_t slots = (int64_t)cu_count(device) * resident_per_cu<T, BM, BN, MODE, EPI, ACT, FAST>();
   int64_t ksplit = 1;
   // Split K only for single-batch problems with fewer tiles than about `split_target` units
-  // per CU, into enough slices to reach that, each slice keeping >= 16 K tiles: every slice
-  // costs an fp32 M x N write and read in the reduction, which only long K amortises (the
-  // 3x3 convs at 1280 channels gain 4x; linears with K = 1280 already lose at 2 slices).
+  // per CU and >= 32 K tiles, into enough slices to reach that, each slice keeping >= 16 K
+  // tiles: every slice costs an fp32 M x N write and read in the reduction, which only long K
+  // amortises (the 3x3 convs gain 5-15% at 320 channels and 1.5-4x at 640-1280; linears with
+  // K <= 1280 are left alone).
   const int64_t target = (int64_t)cu_count(device) * split_target();
   if (batch == 1 && tiles < target && nk >= 32 && splitk_enabled())
     ksplit = std::max<int64_t>(1, std::min<int64_t>(std::min<int64_t>(ceil_div(target, tiles), nk / 16), 16));

@@ -1,12 +1,13 @@
 // group_norm (+ fused SiLU), layer_norm and last-dim softmax: HBM-streaming kernels with
 // wave64 shuffle reductions.
 //
-// group_norm splits every (sample, group) range into chunks so that thousands of workgroups
-// stream at once (an SD group is 40,960 elements but there are only B*32 groups): a stats pass
-// writes per-chunk (sum, sum of squares), and an apply pass folds the chunk partials of its
-// group and normalises its own chunk (its re-read of the input is served mostly by the 256 MB
-// last-level cache).  Statistics follow the reference's one-pass E[x^2] - mean^2 form
-// (tensor.cpp:18765-18767, 18822-18824) with fp32 tree sums.
+// group_norm splits every (sample, group) range into chunks of >= 8192 elements (an SD group is
+// up to 40,960 elements but there are only B*32 groups): a stats pass writes per-chunk (sum,
+// sum of squares), and an apply pass folds the partials of its group(s) with one wave and
+// normalises its own chunk -- NCHW, or channels-last through an LDS transpose for the conv that
+// follows.  Two launches per group_norm; the apply pass's re-read of the input is served mostly
+// by the 256 MB last-level cache.  Statistics follow the reference's one-pass E[x^2] - mean^2
+// form (tensor.cpp:18765-18767, 18822-18824) with fp32 tree sums.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -88,6 +89,7 @@ __global__ __launch_bounds__(256) void group_norm_stats_kernel(const T* __restri
   float s = 0.0f, ss = 0.0f;
   if constexpr (VECT) {
     constexpr int V = Vec16<T>::N;
+#pragma unroll 4
     for (int64_t i = begin + (int64_t)threadIdx.x * V; i < end; i += 256 * V) {
       float f[V];
       Vec16<T>::load(base + i, f);
@@ -116,25 +118,22 @@ __global__ __launch_bounds__(256) void group_norm_stats_kernel(const T* __restri
     partial[bg * splits + split] = make_float2(red[0] + red[1] + red[2] + red[3], red[4] + red[5] + red[6] + red[7]);
 }
 
-// stats[bg] = (mean, 1/sqrt(var + eps)) from the chunk partials; one wave per (sample, group).
-__global__ __launch_bounds__(64) void group_norm_finalize_kernel(const float2* __restrict__ partial,
-                                                                 float2* __restrict__ stats, int splits,
-                                                                 int64_t group_size, float eps) {
-  const int64_t bg = blockIdx.x;
+// (mean, 1/sqrt(var + eps)) of one (sample, group) from its chunk partials, folded by one wave
+// (every lane returns the result).
+__device__ __forceinline__ float2 fold_group_stats(const float2* __restrict__ partial, int64_t bg, int splits,
+                                                   int64_t group_size, float eps, int lane) {
   float s = 0.0f, ss = 0.0f;
-  for (int i = threadIdx.x; i < splits; i += 64) {
+  for (int i = lane; i < splits; i += 64) {
     const float2 p = partial[bg * splits + i];
     s += p.x;
     ss += p.y;
   }
   s = wave_sum(s);
   ss = wave_sum(ss);
-  if (threadIdx.x == 0) {
-    const float n = (float)group_size;
-    const float mean = s / n;
-    const float var = fmaxf(0.0f, ss / n - mean * mean);
-    stats[bg] = make_float2(mean, 1.0f / sqrtf(var + eps));
-  }
+  const float n = (float)group_size;
+  const float mean = s / n;
+  const float var = fmaxf(0.0f, ss / n - mean * mean);
+  return make_float2(mean, 1.0f / sqrtf(var + eps));
 }
 
 // Normalised value of one element in the reference's per-dtype form, with the optional SiLU
@@ -159,13 +158,18 @@ __device__ __forceinline__ float gn_value(float v, float mean, float inv, float 
 template <typename T, bool VECT>
 __global__ __launch_bounds__(256) void group_norm_apply_kernel(const T* __restrict__ x, const T* __restrict__ gamma,
                                                                const T* __restrict__ beta, T* __restrict__ y,
-                                                               const float2* __restrict__ stats, int64_t C,
+                                                               const float2* __restrict__ partial, int64_t C,
                                                                int64_t groups, int64_t inner, int64_t group_size,
-                                                               int64_t chunk, float eps, int fuse_silu) {
+                                                               int64_t chunk, int splits, float eps, int fuse_silu) {
+  __shared__ float2 st_s;
   const int64_t bg = blockIdx.y;
   const int split = blockIdx.x;
-  const float2 st = stats[bg];
-  const float mean = st.x, inv = st.y;
+  if (threadIdx.x < 64) {
+    const float2 st = fold_group_stats(partial, bg, splits, group_size, eps, threadIdx.x);
+    if (threadIdx.x == 0) st_s = st;
+  }
+  __syncthreads();
+  const float mean = st_s.x, inv = st_s.y;
   const int64_t g = bg % groups;
   const int64_t gc = C / groups;
   const int64_t begin = (int64_t)split * chunk;
@@ -202,37 +206,54 @@ template <typename T>
 __global__ __launch_bounds__(256) void group_norm_apply_nhwc_kernel(const T* __restrict__ x,
                                                                     const T* __restrict__ gamma,
                                                                     const T* __restrict__ beta, T* __restrict__ y,
-                                                                    const float2* __restrict__ stats, int64_t C,
+                                                                    const float2* __restrict__ partial, int64_t C,
                                                                     int64_t Cp, int64_t groups, int64_t HW,
-                                                                    int fuse_silu, int vec_io) {
+                                                                    int splits, float eps, int fuse_silu, int vec_io) {
   constexpr int TP = 64 + 2;  // LDS row pitch (elements)
   constexpr int V = Vec16<T>::N;
   __shared__ T tile[64 * TP];
+  __shared__ float2 st_s[64];
   const int64_t b = blockIdx.z;
   const int64_t p0 = (int64_t)blockIdx.x * 64, c0 = (int64_t)blockIdx.y * 64;
   const int t = threadIdx.x;
-  {
-    const int cl = t >> 2, pl0 = (t & 3) * 16;
-    const int64_t c = c0 + cl;
-    float f[16];
-    if (c < C) {
-      const int64_t gc = C / groups;
-      const float2 st = stats[b * groups + c / gc];
-      const float gm = gamma ? Elem<T>::load(gamma, c) : 1.0f;
-      const float bt = beta ? Elem<T>::load(beta, c) : 0.0f;
-      const T* xr = x + (b * C + c) * HW + p0 + pl0;
-      if (vec_io && p0 + pl0 + 16 <= HW) {
+  const int64_t gc = C / groups;
+  const int64_t g_first = c0 / gc;
+  const int cl = t >> 2, pl0 = (t & 3) * 16;
+  const int64_t c = c0 + cl;
+  // The tile's input and affine parameters are requested first; the group statistics are
+  // folded while they arrive.
+  float f[16];
+  float gm = 1.0f, bt = 0.0f;
+  if (c < C) {
+    if (gamma) gm = Elem<T>::load(gamma, c);
+    if (beta) bt = Elem<T>::load(beta, c);
+    const T* xr = x + (b * C + c) * HW + p0 + pl0;
+    if (vec_io && p0 + pl0 + 16 <= HW) {
 #pragma unroll
-        for (int j = 0; j < 16; j += V) {
-          float part[V];
-          Vec16<T>::load(xr + j, part);
+      for (int j = 0; j < 16; j += V) {
+        float part[V];
+        Vec16<T>::load(xr + j, part);
 #pragma unroll
-          for (int k = 0; k < V; ++k) f[j + k] = part[k];
-        }
-      } else {
-#pragma unroll
-        for (int j = 0; j < 16; ++j) f[j] = p0 + pl0 + j < HW ? Elem<T>::load(xr, j) : 0.0f;
+        for (int k = 0; k < V; ++k) f[j + k] = part[k];
       }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 16; ++j) f[j] = p0 + pl0 + j < HW ? Elem<T>::load(xr, j) : 0.0f;
+    }
+  }
+  {
+    // statistics of the (at most 64) groups this tile's channels belong to, one wave each
+    const int64_t c_last = (c0 + 64 < C ? c0 + 64 : C) - 1;
+    const int ng = c0 < C ? (int)(c_last / gc - g_first + 1) : 0;
+    for (int k = t >> 6; k < ng; k += 4) {
+      const float2 st = fold_group_stats(partial, b * groups + g_first + k, splits, gc * HW, eps, t & 63);
+      if ((t & 63) == 0) st_s[k] = st;
+    }
+  }
+  __syncthreads();
+  {
+    if (c < C) {
+      const float2 st = st_s[c / gc - g_first];
 #pragma unroll
       for (int j = 0; j < 16; ++j) f[j] = gn_value<T>(f[j], st.x, st.y, gm, bt, fuse_silu);
     } else {
@@ -418,8 +439,8 @@ __global__ __launch_bounds__(256) void softmax_long_kernel(const T* __restrict__
   }
 }
 
-// Stats (chunked partials, then one wave per group), then the apply pass: NCHW in place of x's
-// layout (y_nhwc == false) or channels-last with Cp channels.
+// Stats (chunked partials), then the apply pass, which folds its group's partials: NCHW as x
+// (y_nhwc == false) or channels-last with Cp channels.
 template <typename T>
 int run_group_norm(int device, const void* x, const void* weight, const void* bias, void* y, int64_t B, int64_t C,
                    int64_t inner, int64_t groups, double eps, int fuse_silu, bool y_nhwc, int64_t Cp, hipStream_t s) {
@@ -429,16 +450,15 @@ int run_group_norm(int device, const void* x, const void* weight, const void* bi
   MTHIP_REQUIRE(n_groups <= 65535, "mthip_group_norm: batch*groups must be <= 65535");
   constexpr int V = Vec16<T>::N;
   const bool vect = ((uintptr_t)x % 16 == 0) && ((uintptr_t)y % 16 == 0) && inner % V == 0;
-  // Aim for ~4096 workgroups in total, each streaming at least 2048 elements.
-  int64_t splits = std::max<int64_t>(1, std::min<int64_t>(ceil_div(4096, n_groups), ceil_div(group_size, 2048)));
-  splits = std::min<int64_t>(splits, 1024);
+  // Stats chunks of >= 8192 elements (16-32 KB per workgroup), at most 64 per group: the apply
+  // kernels fold a group's partials themselves.
+  int64_t splits = std::max<int64_t>(1, std::min<int64_t>(ceil_div(group_size, 8192), 64));
   int64_t chunk = ceil_div(group_size, splits);
   if (vect) chunk = ceil_div(chunk, V) * V;
   splits = ceil_div(group_size, chunk);
   void* ws = nullptr;
-  if (int rc = mthip_malloc(device, (size_t)(n_groups * (splits + 1)) * sizeof(float2), &ws)) return rc;
+  if (int rc = mthip_malloc(device, (size_t)(n_groups * splits) * sizeof(float2), &ws)) return rc;
   float2* partial = static_cast<float2*>(ws);
-  float2* stats = partial + n_groups * splits;
   dim3 grid((unsigned)splits, (unsigned)n_groups);
   if (vect)
     hipLaunchKernelGGL((group_norm_stats_kernel<T, true>), grid, dim3(256), 0, s, (const T*)x, partial, group_size,
@@ -448,25 +468,21 @@ int run_group_norm(int device, const void* x, const void* weight, const void* bi
                        chunk, (int)splits);
   int rc = check_launch("group_norm_stats_kernel");
   if (rc == MTHIP_OK) {
-    hipLaunchKernelGGL(group_norm_finalize_kernel, dim3((unsigned)n_groups), dim3(64), 0, s, (const float2*)partial,
-                       stats, (int)splits, group_size, (float)eps);
-    rc = check_launch("group_norm_finalize_kernel");
-  }
-  if (rc == MTHIP_OK) {
     if (y_nhwc) {
       dim3 g2((unsigned)ceil_div(inner, 64), (unsigned)ceil_div(Cp, 64), (unsigned)B);
       // 16-byte row access: pixel rows and channel rows start on 16-byte boundaries.
       const int vec_io = ((uintptr_t)x % 16 == 0) && ((uintptr_t)y % 16 == 0) && inner % V == 0 && Cp % V == 0;
       hipLaunchKernelGGL(group_norm_apply_nhwc_kernel<T>, g2, dim3(256), 0, s, (const T*)x, (const T*)weight,
-                         (const T*)bias, (T*)y, (const float2*)stats, C, Cp, groups, inner, fuse_silu, vec_io);
+                         (const T*)bias, (T*)y, (const float2*)partial, C, Cp, groups, inner, (int)splits, (float)eps,
+                         fuse_silu, vec_io);
     } else if (vect) {
       hipLaunchKernelGGL((group_norm_apply_kernel<T, true>), grid, dim3(256), 0, s, (const T*)x, (const T*)weight,
-                         (const T*)bias, (T*)y, (const float2*)stats, C, groups, inner, group_size, chunk, (float)eps,
-                         fuse_silu);
+                         (const T*)bias, (T*)y, (const float2*)partial, C, groups, inner, group_size, chunk,
+                         (int)splits, (float)eps, fuse_silu);
     } else {
       hipLaunchKernelGGL((group_norm_apply_kernel<T, false>), grid, dim3(256), 0, s, (const T*)x, (const T*)weight,
-                         (const T*)bias, (T*)y, (const float2*)stats, C, groups, inner, group_size, chunk, (float)eps,
-                         fuse_silu);
+                         (const T*)bias, (T*)y, (const float2*)partial, C, groups, inner, group_size, chunk,
+                         (int)splits, (float)eps, fuse_silu);
     }
     rc = check_launch("group_norm_apply_kernel");
   }
