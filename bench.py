@@ -1,6 +1,6 @@
 """Benchmark of mtorch's SD-UNet hot path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload resnet|linear_gelu|copy_calibration] [--no-cpu]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload resnet|linear_gelu|unet|copy_calibration] [--no-cpu]
 
 Default workload (fp16 leg): the SD ResNet sub-block on a 64x64
 latent at batch 2 -- x[2,320,64,64] -> GroupNorm(32, eps 1e-5, affine) -> SiLU ->
@@ -110,7 +110,7 @@ def run_resnet(args):
 
     def step(marks=None):
         _lib.check(L.mthip_group_norm_nhwc(0, _lib.F16, xd.data_ptr(), gd.data_ptr(), bd.data_ptr(), xn.ptr, B, C,
-                                           H * W, 32, 1e-5, 1))
+                                           H * W, 32, 1e-5, 1, _lib.F16))
         if marks:
             marks[0].record()
         _lib.check(L.mthip_conv2d_nhwc(0, _lib.F16, xn.ptr, wp, bbd.data_ptr(), y.data_ptr(), B, C, H, W, O, 3, 3,
@@ -248,12 +248,60 @@ def run_linear_gelu(args):
     }
 
 
+def run_unet(args):
+    """one SD-1.5-shaped UNet denoising step at batch 2 (latent [2,4,64,64], t = 500,
+    context [2,77,768]; ~860 M parameters N(0, 0.02) in fp16, norms fp32 with upcast), captured
+    once into a HIP graph and replayed; each replay is one full forward."""
+    import mtorch_amd as mt
+    from mtorch_amd import sd_unet
+
+    t0 = time.perf_counter()
+    model = sd_unet.UNet(seed=0, device="cuda")
+    build_s = time.perf_counter() - t0
+    mt.manual_seed(1)
+    latent = mt.randn(2, 4, 64, 64).half().to("cuda")
+    ctx = mt.randn(2, 77, 768).half().to("cuda")
+    t = mt.tensor([500.0, 500.0]).to("cuda")
+    model(latent, t, ctx)  # eager pass: packs the conv weights outside the graph
+    mt.cuda.synchronize()
+    t1 = time.perf_counter()
+    model(latent, t, ctx)
+    mt.cuda.synchronize()
+    eager_ms = (time.perf_counter() - t1) * 1e3
+    g = mt.cuda.CUDAGraph()
+    with mt.cuda.graph(g):
+        model(latent, t, ctx)
+    for _ in range(args.warmup):
+        g.replay()
+    mt.cuda.synchronize()
+    start, end = mt.cuda.Event(), mt.cuda.Event()
+    start.record()
+    for _ in range(args.steps):
+        g.replay()
+    end.record()
+    mt.cuda.synchronize()
+    ms = start.elapsed_time(end) / args.steps
+    flops = sd_unet.unet_flops()
+    tflops = flops / (ms * 1e-3) / 1e12
+    return {
+        "metric": "SD-1.5 UNet step ms, batch 2, 64x64 latent, fp16 (graph-replayed)",
+        "value": round(ms, 3), "unit": "ms", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms, 3), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": "fp16", "data": "synthetic (mtorch generator: weights seed 0, inputs seed 1)",
+        "config": {"workload": "configs[4] SD-1.5 UNet, batch 2, latent [2,4,64,64], context [2,77,768], t=500",
+                   "params": sum(p.numel() for p in model.parameters())},
+        "tflops": round(tflops, 2), "unet_tflop_per_step": round(flops / 1e12, 4),
+        "mfma_frac": round(tflops / PEAK["fp16_mfma_tflops"], 4),
+        "eager_ms_per_step": round(eager_ms, 2), "model_build_s": round(build_s, 1),
+    }
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", default="resnet", choices=["resnet", "linear_gelu", "copy_calibration"])
+    ap.add_argument("--workload", default="resnet", choices=["resnet", "linear_gelu", "unet", "copy_calibration"])
     ap.add_argument("--no-cpu", dest="cpu", action="store_false")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -265,7 +313,8 @@ def main():
     if not mt.cuda.is_available():
         raise SystemExit("bench.py: no GPU visible to libmthip")
     with mt.no_grad():
-        run = {"resnet": run_resnet, "linear_gelu": run_linear_gelu, "copy_calibration": run_copy_calibration}
+        run = {"resnet": run_resnet, "linear_gelu": run_linear_gelu, "unet": run_unet,
+               "copy_calibration": run_copy_calibration}
         out = run[args.workload](args)
     out["device"] = mt.cuda.get_device_name(0)
     print(json.dumps(out), flush=True)

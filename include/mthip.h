@@ -222,15 +222,17 @@ enum { MTHIP_MASK_NONE = 0, MTHIP_MASK_BOOL = 1, MTHIP_MASK_ADD = 2 };
 /* o = softmax(q k^T * scale + mask) v over heads -- mtorch::scaled_dot_product_attention
  * (tensor.cpp:30930-31324; py_scaled_dot_product_attention module.cpp:7407-7459).
  * Layout: q[B,H,Lq,E], k[B,Hk,Lk,E], v[B,Hk,Lk,Ev] addressed by element strides
- * (qs/ks/vs = {batch, head, seq}; the last dim is contiguous); o is contiguous [B,H,Lq,Ev].
+ * (qs/ks/vs = {batch, head, seq}; the last dim is contiguous); o likewise through os (NULL:
+ * contiguous [B,H,Lq,Ev]) -- e.g. {Lq*H*Ev, Ev, H*Ev} writes the heads merged back into a
+ * [B, Lq, H*Ev] token tensor, the layout the output projection reads.
  * Hk divides H (H/Hk query heads share a key head: enable_gqa).  mask: MTHIP_MASK_BOOL
  * (uint8, false -> -inf) or MTHIP_MASK_ADD (mask_dtype F32 or the query dtype, added to the
  * scaled score), read through 4 strides {b, h, q, k} with 0 on broadcast axes.  is_causal
  * masks keys after the query.  scale <= 0 selects 1/sqrt(E).  q/k/v/o share dtype F16
  * (fp16 MFMA, fp32 softmax) or F32.  Fully-masked rows give NaN, as the reference does. */
 int mthip_sdpa(int device, int dtype, const void* q, const int64_t* qs, const void* k,
-               const int64_t* ks, const void* v, const int64_t* vs, void* o, int64_t B, int64_t H,
-               int64_t Hk, int64_t Lq, int64_t Lk, int64_t E, int64_t Ev, int mask_kind,
+               const int64_t* ks, const void* v, const int64_t* vs, void* o, const int64_t* os,
+               int64_t B, int64_t H, int64_t Hk, int64_t Lq, int64_t Lk, int64_t E, int64_t Ev, int mask_kind,
                int mask_dtype, const void* mask, const int64_t* mask_strides, int is_causal,
                double scale);
 
@@ -238,21 +240,25 @@ int mthip_sdpa(int device, int dtype, const void* q, const int64_t* qs, const vo
 
 /* group_norm on contiguous x[B, C, inner] (tensor.cpp:18643-18963; py_group_norm
  * module.cpp:7646-7693); weight/bias [C] or NULL.  fuse_silu != 0 applies silu to the
- * narrowed result (the GroupNorm->SiLU pair of every SD ResBlock) with silu's own rounding. */
+ * narrowed result (the GroupNorm->SiLU pair of every SD ResBlock) with silu's own rounding.
+ * param_dtype is the dtype of weight/bias and of the computation: equal to dtype, or F32 with
+ * F16 data -- the upcast pattern group_norm(x.float(), w32, b32).half() of SD pipelines, run as
+ * the reference's fp32 path (tensor.cpp:18797-18841) narrowed once. */
 int mthip_group_norm(int device, int dtype, const void* x, const void* weight, const void* bias,
                      void* y, int64_t B, int64_t C, int64_t inner, int64_t groups, double eps,
-                     int fuse_silu);
+                     int fuse_silu, int param_dtype);
 /* The same values written channels-last for mthip_conv2d_nhwc: y_nhwc[B][HW][Cp], Cp = C
  * rounded up to 8 (F16) or 4 (F32) channels, the padding channels zero.  x stays NCHW. */
 int mthip_group_norm_nhwc(int device, int dtype, const void* x, const void* weight, const void* bias,
                           void* y_nhwc, int64_t B, int64_t C, int64_t HW, int64_t groups, double eps,
-                          int fuse_silu);
+                          int fuse_silu, int param_dtype);
 
 /* layer_norm over the trailing N elements of contiguous x[rows, N] (tensor.cpp:17386-17708;
  * py_layer_norm module.cpp:7461-7516); weight/bias [N] or NULL.  fp16 uses the two-pass
- * centred variance, fp32 the one-pass form, as the reference does. */
+ * centred variance, fp32 the one-pass form, as the reference does.  param_dtype as for
+ * mthip_group_norm (F32 over F16 data: layer_norm(x.float(), w32, b32).half()). */
 int mthip_layer_norm(int device, int dtype, const void* x, const void* weight, const void* bias,
-                     void* y, int64_t rows, int64_t N, double eps);
+                     void* y, int64_t rows, int64_t N, double eps, int param_dtype);
 
 /* softmax over the last dim of contiguous x[rows, cols] (tensor.cpp:15145-15221,
  * try_softmax_float32_kernel :7508-7741, try_softmax_float16_kernel :7743-7802).

@@ -621,8 +621,9 @@ def group_norm_silu_conv2d(x: Tensor, num_groups: int, gn_weight: Tensor, gn_bia
     the GroupNorm -> SiLU -> conv chain of an SD ResNet block (the reference runs it as three
     ops, tensor.cpp:18643, 16480, 26490).  On the device the normalised activation is written
     once, channels-last, in the layout the implicit-GEMM conv reads (mthip_group_norm_nhwc then
-    mthip_conv2d_nhwc); values equal the unfused sequence's."""
-    _same_dtype("group_norm", [x, gn_weight, gn_bias], "tensors")
+    mthip_conv2d_nhwc); values equal the unfused sequence's.  fp32 GroupNorm parameters over an
+    fp16 input mean the upcast pattern silu(group_norm(x.float(), ...).half())."""
+    pdt = _norm_param_dtype("group_norm", x, gn_weight, gn_bias)
     _same_dtype("conv2d", [x, w, b], "tensors")
     dev = _gpu("group_norm_silu_conv2d", x, gn_weight, gn_bias, w, b, residual)
     if x.dim() != 4:
@@ -638,11 +639,33 @@ def group_norm_silu_conv2d(x: Tensor, num_groups: int, gn_weight: Tensor, gn_bia
         Cp = -(-C // vec) * vec
         xn = T._DeviceBuffer(B * H * W * Cp * x.dtype.itemsize, dev)
         _lib.check(L.mthip_group_norm_nhwc(dev, x.dtype.code, x.contiguous().data_ptr(), _ptr(_contig(gn_weight)),
-                                           _ptr(_contig(gn_bias)), xn.ptr, B, C, H * W, num_groups, float(eps), 1))
+                                           _ptr(_contig(gn_bias)), xn.ptr, B, C, H * W, num_groups, float(eps), 1,
+                                           pdt))
         wp = _conv_packed_weight(w.contiguous(), dev, O, C, KH, KW)
         _lib.check(L.mthip_conv2d_nhwc(dev, x.dtype.code, xn.ptr, wp, _ptr(_contig(b)), out.data_ptr(), B, C, H, W, O,
                                        KH, KW, p["sh"], p["sw"], p["ph"], p["pw"], p["dh"], p["dw"], _ptr(rc)))
         del xn  # stream-ordered free: reused only by later work
+    return out
+
+
+def conv2d_tokens(tok: Tensor, w: Tensor, b: Tensor, H: int, W: int, residual: Tensor = None) -> Tensor:
+    """1x1 conv of a channels-last token tensor tok[B, H*W, C] to NCHW [B, O, H, W] (+ residual):
+    conv2d(tok.reshape(B, H, W, C).permute(0, 3, 1, 2), w, b) without the permute -- the proj_out
+    of an SD transformer block, whose epilogue adds the block's NCHW input."""
+    _same_dtype("conv2d", [tok, w, b], "tensors")
+    dev = _gpu("conv2d", tok, w, b, residual)
+    B, L, C = tok.shape
+    O = w.shape[0]
+    if L != H * W or list(w.shape[1:]) not in ([C, 1, 1], [C]):
+        raise ValueError("conv2d_tokens: token / weight shape mismatch")
+    if C % (8 if tok.dtype is T.float16 else 4):
+        raise ValueError("conv2d_tokens: the channel count must be a whole number of 16-byte chunks")
+    out = _empty([B, O, H, W], tok.dtype, dev)
+    rc = _conv_residual(residual, out)
+    tc = tok.contiguous()
+    wp = _conv_packed_weight(w.contiguous().reshape(O, C, 1, 1), dev, O, C, 1, 1)
+    _lib.check(_L().mthip_conv2d_nhwc(dev, tok.dtype.code, tc.data_ptr(), wp, _ptr(_contig(b)), out.data_ptr(), B, C, H,
+                                      W, O, 1, 1, 1, 1, 0, 0, 1, 1, _ptr(rc)))
     return out
 
 
@@ -784,13 +807,25 @@ def scaled_dot_product_attention(query: Tensor, key: Tensor, value: Tensor, attn
         mptr = m2.data_ptr()
     sc = -1.0 if scale is None else float(scale)
     _lib.check(_L().mthip_sdpa(dev, query.dtype.code, q2.data_ptr(), _lib.int64_array(qs), k2.data_ptr(),
-                               _lib.int64_array(ks), v2.data_ptr(), _lib.int64_array(vs), out.data_ptr(), B, H, Hk, Lq,
-                               Lk, E, Ev, mask_kind, mask_dt, mptr, _lib.int64_array(ms) if ms else None,
+                               _lib.int64_array(ks), v2.data_ptr(), _lib.int64_array(vs), out.data_ptr(), None, B, H,
+                               Hk, Lq, Lk, E, Ev, mask_kind, mask_dt, mptr, _lib.int64_array(ms) if ms else None,
                                1 if is_causal else 0, sc))
     return out
 
 
 # ------------------------------------------------------------------------------ normalisation
+
+
+def _norm_param_dtype(op: str, x: Tensor, weight: Tensor, bias: Tensor) -> int:
+    """dtype code of a norm's parameters: x's dtype, or float32 over a float16 input -- the
+    upcast pattern norm(x.float(), w32, b32).half(), which the fused device paths run as one
+    kernel.  (The public F.group_norm / F.layer_norm keep the reference's same-dtype rule.)"""
+    dts = {t.dtype for t in (weight, bias) if t is not None}
+    if not dts or dts == {x.dtype}:
+        return x.dtype.code
+    if dts == {T.float32} and x.dtype is T.float16:
+        return T.float32.code
+    raise ValueError(f"expected {op} input and parameters to have the same dtype")
 
 
 def _group_norm_check(x: Tensor, num_groups: int, weight: Tensor, bias: Tensor):
@@ -816,9 +851,14 @@ def _group_norm_check(x: Tensor, num_groups: int, weight: Tensor, bias: Tensor):
 
 
 def group_norm(x: Tensor, num_groups: int, weight: Tensor = None, bias: Tensor = None, eps=1e-5,
-               fuse_silu=False) -> Tensor:
-    """mtorch::group_norm (tensor.cpp:18643-18963), binding py_group_norm (module.cpp:7646-7693)."""
-    _same_dtype("group_norm", [x, weight, bias], "tensors")
+               fuse_silu=False, allow_upcast=False) -> Tensor:
+    """mtorch::group_norm (tensor.cpp:18643-18963), binding py_group_norm (module.cpp:7646-7693).
+    allow_upcast: float32 parameters over a float16 input run group_norm(x.float(), w, b).half()."""
+    if allow_upcast:
+        pdt = _norm_param_dtype("group_norm", x, weight, bias)
+    else:
+        _same_dtype("group_norm", [x, weight, bias], "tensors")
+        pdt = x.dtype.code
     dev = _gpu("group_norm", x, weight, bias)
     inner = _group_norm_check(x, num_groups, weight, bias)
     B, C = x.shape[0], x.shape[1]
@@ -826,16 +866,23 @@ def group_norm(x: Tensor, num_groups: int, weight: Tensor = None, bias: Tensor =
     out = _empty(x.shape, x.dtype, dev)
     if out.numel():
         _lib.check(_L().mthip_group_norm(dev, x.dtype.code, xc.data_ptr(), _ptr(_contig(weight)), _ptr(_contig(bias)),
-                                         out.data_ptr(), B, C, inner, num_groups, float(eps), 1 if fuse_silu else 0))
+                                         out.data_ptr(), B, C, inner, num_groups, float(eps), 1 if fuse_silu else 0,
+                                         pdt))
     return out
 
 
-def layer_norm(x: Tensor, normalized_shape, weight: Tensor = None, bias: Tensor = None, eps=1e-5) -> Tensor:
-    """mtorch::layer_norm (tensor.cpp:17386-17708), binding py_layer_norm (module.cpp:7461-7516)."""
+def layer_norm(x: Tensor, normalized_shape, weight: Tensor = None, bias: Tensor = None, eps=1e-5,
+               allow_upcast=False) -> Tensor:
+    """mtorch::layer_norm (tensor.cpp:17386-17708), binding py_layer_norm (module.cpp:7461-7516).
+    allow_upcast: float32 parameters over a float16 input run layer_norm(x.float(), w, b).half()."""
     if isinstance(normalized_shape, int):
         normalized_shape = [normalized_shape]
     normalized_shape = [int(s) for s in normalized_shape]
-    _same_dtype("layer_norm", [x, weight, bias], "tensors")
+    if allow_upcast:
+        pdt = _norm_param_dtype("layer_norm", x, weight, bias)
+    else:
+        _same_dtype("layer_norm", [x, weight, bias], "tensors")
+        pdt = x.dtype.code
     dev = _gpu("layer_norm", x, weight, bias)
     if not normalized_shape:
         raise ValueError("layer_norm normalized_shape must not be empty")
@@ -856,7 +903,7 @@ def layer_norm(x: Tensor, normalized_shape, weight: Tensor = None, bias: Tensor 
     out = _empty(x.shape, x.dtype, dev)
     if out.numel():
         _lib.check(_L().mthip_layer_norm(dev, x.dtype.code, xc.data_ptr(), _ptr(_contig(weight)),
-                                         _ptr(_contig(bias)), out.data_ptr(), rows, N, float(eps)))
+                                         _ptr(_contig(bias)), out.data_ptr(), rows, N, float(eps), pdt))
     return out
 
 

@@ -34,7 +34,7 @@ struct FlashArgs {
   const void* k;
   const void* v;
   void* o;
-  int64_t qs[3], ks[3], vs[3];  // element strides: batch, head, sequence (last dim contiguous)
+  int64_t qs[3], ks[3], vs[3], os[3];  // element strides: batch, head, sequence (last dim contiguous)
   int64_t H, Hk, Lq, Lk, E, Ev;
   int mask_kind, mask_dtype;
   const void* mask;
@@ -270,7 +270,7 @@ __global__ __launch_bounds__(64 * WAVES) void flash_fwd_f16_kernel(const FlashAr
   }
 
   if (!qok) return;
-  uint16_t* O = reinterpret_cast<uint16_t*>(a.o) + (bh * a.Lq + q) * a.Ev;
+  uint16_t* O = reinterpret_cast<uint16_t*>(a.o) + b * a.os[0] + head * a.os[1] + q * a.os[2];
   const float inv_l = 1.0f / l_run;
   const bool zero_l = l_run == 0.0f;  // fully masked row: 0/0 = NaN like the reference
 #pragma unroll
@@ -337,7 +337,7 @@ __global__ __launch_bounds__(256) void attention_rowwise_kernel(const FlashArgs 
       o[j] = o[j] * alpha + (d < a.Ev ? p * Elem<T>::load(V, key * a.vs[2] + d) : 0.0f);
     }
   }
-  T* O = reinterpret_cast<T*>(a.o) + (bh * a.Lq + q) * a.Ev;
+  T* O = reinterpret_cast<T*>(a.o) + b * a.os[0] + head * a.os[1] + q * a.os[2];
 #pragma unroll
   for (int j = 0; j < VPL; ++j) {
     const int64_t d = lane + 64 * j;
@@ -376,7 +376,8 @@ bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 using namespace mthip;
 
 extern "C" int mthip_sdpa(int device, int dtype, const void* q, const int64_t* qs, const void* k, const int64_t* ks,
-                          const void* v, const int64_t* vs, void* o, int64_t B, int64_t H, int64_t Hk, int64_t Lq,
+                          const void* v, const int64_t* vs, void* o, const int64_t* os, int64_t B, int64_t H,
+                          int64_t Hk, int64_t Lq,
                           int64_t Lk, int64_t E, int64_t Ev, int mask_kind, int mask_dtype, const void* mask,
                           const int64_t* mask_strides, int is_causal, double scale) {
   MTHIP_REQUIRE(dtype == MTHIP_F16 || dtype == MTHIP_F32, "mthip_sdpa: dtype must be F16 or F32");
@@ -402,6 +403,13 @@ extern "C" int mthip_sdpa(int device, int dtype, const void* q, const int64_t* q
     a.qs[i] = qs[i];
     a.ks[i] = ks[i];
     a.vs[i] = vs[i];
+  }
+  if (os) {
+    for (int i = 0; i < 3; ++i) a.os[i] = os[i];
+  } else {  // contiguous [B, H, Lq, Ev]
+    a.os[2] = Ev;
+    a.os[1] = Lq * Ev;
+    a.os[0] = H * Lq * Ev;
   }
   a.H = H;
   a.Hk = Hk;

@@ -138,10 +138,13 @@ __device__ __forceinline__ float2 fold_group_stats(const float2* __restrict__ pa
 
 // Normalised value of one element in the reference's per-dtype form, with the optional SiLU
 // applied to the narrowed normalised value (the unfused op sequence narrows in between).
-template <typename T>
+// P is the parameter (and computation) dtype: fp16 parameters take the fp16 path's form; fp32
+// parameters over fp16 data are the "upcast" pattern group_norm(x.float(), w32, b32).half(),
+// i.e. the fp32 path's form narrowed once.
+template <typename T, typename P>
 __device__ __forceinline__ float gn_value(float v, float mean, float inv, float gm, float bt, int fuse_silu) {
   float out;
-  if constexpr (sizeof(T) == 2) {
+  if constexpr (sizeof(P) == 2) {
     // affine_float32_to_half_bits(scale = gamma*inv, shift = beta - mean*gamma*inv)
     // (tensor.cpp:18768-18781).
     const float scale = gm * inv;
@@ -155,9 +158,9 @@ __device__ __forceinline__ float gn_value(float v, float mean, float inv, float 
   return out;
 }
 
-template <typename T, bool VECT>
-__global__ __launch_bounds__(256) void group_norm_apply_kernel(const T* __restrict__ x, const T* __restrict__ gamma,
-                                                               const T* __restrict__ beta, T* __restrict__ y,
+template <typename T, typename P, bool VECT>
+__global__ __launch_bounds__(256) void group_norm_apply_kernel(const T* __restrict__ x, const P* __restrict__ gamma,
+                                                               const P* __restrict__ beta, T* __restrict__ y,
                                                                const float2* __restrict__ partial, int64_t C,
                                                                int64_t groups, int64_t inner, int64_t group_size,
                                                                int64_t chunk, int splits, float eps, int fuse_silu) {
@@ -181,20 +184,20 @@ __global__ __launch_bounds__(256) void group_norm_apply_kernel(const T* __restri
     constexpr int V = Vec16<T>::N;
     for (int64_t i = begin + (int64_t)threadIdx.x * V; i < end; i += 256 * V) {
       const int64_t c = g * gc + i / inner;
-      const float gm = gamma ? Elem<T>::load(gamma, c) : 1.0f;
-      const float bt = beta ? Elem<T>::load(beta, c) : 0.0f;
+      const float gm = gamma ? Elem<P>::load(gamma, c) : 1.0f;
+      const float bt = beta ? Elem<P>::load(beta, c) : 0.0f;
       float f[V];
       Vec16<T>::load(xb + i, f);
 #pragma unroll
-      for (int j = 0; j < V; ++j) f[j] = gn_value<T>(f[j], mean, inv, gm, bt, fuse_silu);
+      for (int j = 0; j < V; ++j) f[j] = gn_value<T, P>(f[j], mean, inv, gm, bt, fuse_silu);
       Vec16<T>::store(yb + i, f);
     }
   } else {
     for (int64_t i = begin + threadIdx.x; i < end; i += 256) {
       const int64_t c = g * gc + i / inner;
-      const float gm = gamma ? Elem<T>::load(gamma, c) : 1.0f;
-      const float bt = beta ? Elem<T>::load(beta, c) : 0.0f;
-      Elem<T>::store(yb, i, gn_value<T>(Elem<T>::load(xb, i), mean, inv, gm, bt, fuse_silu));
+      const float gm = gamma ? Elem<P>::load(gamma, c) : 1.0f;
+      const float bt = beta ? Elem<P>::load(beta, c) : 0.0f;
+      Elem<T>::store(yb, i, gn_value<T, P>(Elem<T>::load(xb, i), mean, inv, gm, bt, fuse_silu));
     }
   }
 }
@@ -202,10 +205,10 @@ __global__ __launch_bounds__(256) void group_norm_apply_kernel(const T* __restri
 // Same values written channels-last: y[b][p][0..Cp) with channels C..Cp-1 zero, the layout the
 // implicit-GEMM conv stages its input in.  A workgroup transposes a 64-channel x 64-pixel tile
 // through LDS: reads walk pixels of one channel, writes walk channels of one pixel.
-template <typename T>
+template <typename T, typename P>
 __global__ __launch_bounds__(256) void group_norm_apply_nhwc_kernel(const T* __restrict__ x,
-                                                                    const T* __restrict__ gamma,
-                                                                    const T* __restrict__ beta, T* __restrict__ y,
+                                                                    const P* __restrict__ gamma,
+                                                                    const P* __restrict__ beta, T* __restrict__ y,
                                                                     const float2* __restrict__ partial, int64_t C,
                                                                     int64_t Cp, int64_t groups, int64_t HW,
                                                                     int splits, float eps, int fuse_silu, int vec_io) {
@@ -225,8 +228,8 @@ __global__ __launch_bounds__(256) void group_norm_apply_nhwc_kernel(const T* __r
   float f[16];
   float gm = 1.0f, bt = 0.0f;
   if (c < C) {
-    if (gamma) gm = Elem<T>::load(gamma, c);
-    if (beta) bt = Elem<T>::load(beta, c);
+    if (gamma) gm = Elem<P>::load(gamma, c);
+    if (beta) bt = Elem<P>::load(beta, c);
     const T* xr = x + (b * C + c) * HW + p0 + pl0;
     if (vec_io && p0 + pl0 + 16 <= HW) {
 #pragma unroll
@@ -255,7 +258,7 @@ __global__ __launch_bounds__(256) void group_norm_apply_nhwc_kernel(const T* __r
     if (c < C) {
       const float2 st = st_s[c / gc - g_first];
 #pragma unroll
-      for (int j = 0; j < 16; ++j) f[j] = gn_value<T>(f[j], st.x, st.y, gm, bt, fuse_silu);
+      for (int j = 0; j < 16; ++j) f[j] = gn_value<T, P>(f[j], st.x, st.y, gm, bt, fuse_silu);
     } else {
 #pragma unroll
       for (int j = 0; j < 16; ++j) f[j] = 0.0f;
@@ -293,9 +296,11 @@ __global__ __launch_bounds__(256) void group_norm_apply_nhwc_kernel(const T* __r
 
 // ------------------------------------------------------------------------------ layer_norm
 // One wave per row; the row lives in registers (up to 64*MAXV elements).
-template <typename T, int MAXV>
-__global__ __launch_bounds__(256) void layer_norm_kernel(const T* __restrict__ x, const T* __restrict__ w,
-                                                         const T* __restrict__ b, T* __restrict__ y, int64_t rows,
+// P: parameter / computation dtype, as for group_norm (fp32 over fp16 data = the upcast pattern
+// layer_norm(x.float(), w32, b32).half()).
+template <typename T, typename P, int MAXV>
+__global__ __launch_bounds__(256) void layer_norm_kernel(const T* __restrict__ x, const P* __restrict__ w,
+                                                         const P* __restrict__ b, T* __restrict__ y, int64_t rows,
                                                          int64_t N, float eps) {
   const int lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -312,7 +317,7 @@ __global__ __launch_bounds__(256) void layer_norm_kernel(const T* __restrict__ x
   const float n = (float)N;
   const float mean = wave_sum(s) / n;
   float var;
-  if constexpr (sizeof(T) == 2) {
+  if constexpr (sizeof(P) == 2) {
     // fp16: two-pass centred variance (tensor.cpp:17531-17545).
     float css = 0.0f;
 #pragma unroll
@@ -336,17 +341,17 @@ __global__ __launch_bounds__(256) void layer_norm_kernel(const T* __restrict__ x
     const int64_t i = lane + (int64_t)j * 64;
     if (i < N) {
       float o = (v[j] - mean) * inv;
-      if (w) o = o * Elem<T>::load(w, i);
-      if (b) o = o + Elem<T>::load(b, i);
+      if (w) o = o * Elem<P>::load(w, i);
+      if (b) o = o + Elem<P>::load(b, i);
       Elem<T>::store(yr, i, o);
     }
   }
 }
 
 // Rows too long for registers: one workgroup per row, three passes over the row.
-template <typename T>
-__global__ __launch_bounds__(256) void layer_norm_long_kernel(const T* __restrict__ x, const T* __restrict__ w,
-                                                              const T* __restrict__ b, T* __restrict__ y, int64_t N,
+template <typename T, typename P>
+__global__ __launch_bounds__(256) void layer_norm_long_kernel(const T* __restrict__ x, const P* __restrict__ w,
+                                                              const P* __restrict__ b, T* __restrict__ y, int64_t N,
                                                               float eps) {
   __shared__ float red[4];
   const int64_t row = blockIdx.x;
@@ -356,7 +361,7 @@ __global__ __launch_bounds__(256) void layer_norm_long_kernel(const T* __restric
   const float n = (float)N;
   const float mean = block_sum256(s, red) / n;
   float var;
-  if constexpr (sizeof(T) == 2) {
+  if constexpr (sizeof(P) == 2) {
     float css = 0.0f;
     for (int64_t i = threadIdx.x; i < N; i += 256) {
       const float c = Elem<T>::load(xr, i) - mean;
@@ -375,8 +380,8 @@ __global__ __launch_bounds__(256) void layer_norm_long_kernel(const T* __restric
   T* yr = y + row * N;
   for (int64_t i = threadIdx.x; i < N; i += 256) {
     float o = (Elem<T>::load(xr, i) - mean) * inv;
-    if (w) o = o * Elem<T>::load(w, i);
-    if (b) o = o + Elem<T>::load(b, i);
+    if (w) o = o * Elem<P>::load(w, i);
+    if (b) o = o + Elem<P>::load(b, i);
     Elem<T>::store(yr, i, o);
   }
 }
@@ -441,7 +446,7 @@ __global__ __launch_bounds__(256) void softmax_long_kernel(const T* __restrict__
 
 // Stats (chunked partials), then the apply pass, which folds its group's partials: NCHW as x
 // (y_nhwc == false) or channels-last with Cp channels.
-template <typename T>
+template <typename T, typename P>
 int run_group_norm(int device, const void* x, const void* weight, const void* bias, void* y, int64_t B, int64_t C,
                    int64_t inner, int64_t groups, double eps, int fuse_silu, bool y_nhwc, int64_t Cp, hipStream_t s) {
   const int64_t group_size = (C / groups) * inner;
@@ -472,16 +477,16 @@ int run_group_norm(int device, const void* x, const void* weight, const void* bi
       dim3 g2((unsigned)ceil_div(inner, 64), (unsigned)ceil_div(Cp, 64), (unsigned)B);
       // 16-byte row access: pixel rows and channel rows start on 16-byte boundaries.
       const int vec_io = ((uintptr_t)x % 16 == 0) && ((uintptr_t)y % 16 == 0) && inner % V == 0 && Cp % V == 0;
-      hipLaunchKernelGGL(group_norm_apply_nhwc_kernel<T>, g2, dim3(256), 0, s, (const T*)x, (const T*)weight,
-                         (const T*)bias, (T*)y, (const float2*)partial, C, Cp, groups, inner, (int)splits, (float)eps,
+      hipLaunchKernelGGL((group_norm_apply_nhwc_kernel<T, P>), g2, dim3(256), 0, s, (const T*)x, (const P*)weight,
+                         (const P*)bias, (T*)y, (const float2*)partial, C, Cp, groups, inner, (int)splits, (float)eps,
                          fuse_silu, vec_io);
     } else if (vect) {
-      hipLaunchKernelGGL((group_norm_apply_kernel<T, true>), grid, dim3(256), 0, s, (const T*)x, (const T*)weight,
-                         (const T*)bias, (T*)y, (const float2*)partial, C, groups, inner, group_size, chunk,
+      hipLaunchKernelGGL((group_norm_apply_kernel<T, P, true>), grid, dim3(256), 0, s, (const T*)x, (const P*)weight,
+                         (const P*)bias, (T*)y, (const float2*)partial, C, groups, inner, group_size, chunk,
                          (int)splits, (float)eps, fuse_silu);
     } else {
-      hipLaunchKernelGGL((group_norm_apply_kernel<T, false>), grid, dim3(256), 0, s, (const T*)x, (const T*)weight,
-                         (const T*)bias, (T*)y, (const float2*)partial, C, groups, inner, group_size, chunk,
+      hipLaunchKernelGGL((group_norm_apply_kernel<T, P, false>), grid, dim3(256), 0, s, (const T*)x, (const P*)weight,
+                         (const P*)bias, (T*)y, (const float2*)partial, C, groups, inner, group_size, chunk,
                          (int)splits, (float)eps, fuse_silu);
     }
     rc = check_launch("group_norm_apply_kernel");
@@ -490,22 +495,26 @@ int run_group_norm(int device, const void* x, const void* weight, const void* bi
   return rc;
 }
 
-template <typename T>
+template <typename T, typename P>
 int run_layer_norm(const void* x, const void* w, const void* b, void* y, int64_t rows, int64_t N, double eps,
                    hipStream_t s) {
   if (rows == 0 || N == 0) return MTHIP_OK;
   const unsigned grid4 = (unsigned)ceil_div(rows, 4);
   const float e = (float)eps;
+  const T* xp = (const T*)x;
+  const P* wp = (const P*)w;
+  const P* bp = (const P*)b;
+  T* yp = (T*)y;
   if (N <= 64 * 4)
-    hipLaunchKernelGGL((layer_norm_kernel<T, 4>), dim3(grid4), dim3(256), 0, s, (const T*)x, (const T*)w, (const T*)b, (T*)y, rows, N, e);
+    hipLaunchKernelGGL((layer_norm_kernel<T, P, 4>), dim3(grid4), dim3(256), 0, s, xp, wp, bp, yp, rows, N, e);
   else if (N <= 64 * 12)
-    hipLaunchKernelGGL((layer_norm_kernel<T, 12>), dim3(grid4), dim3(256), 0, s, (const T*)x, (const T*)w, (const T*)b, (T*)y, rows, N, e);
+    hipLaunchKernelGGL((layer_norm_kernel<T, P, 12>), dim3(grid4), dim3(256), 0, s, xp, wp, bp, yp, rows, N, e);
   else if (N <= 64 * 20)
-    hipLaunchKernelGGL((layer_norm_kernel<T, 20>), dim3(grid4), dim3(256), 0, s, (const T*)x, (const T*)w, (const T*)b, (T*)y, rows, N, e);
+    hipLaunchKernelGGL((layer_norm_kernel<T, P, 20>), dim3(grid4), dim3(256), 0, s, xp, wp, bp, yp, rows, N, e);
   else if (N <= 64 * 32)
-    hipLaunchKernelGGL((layer_norm_kernel<T, 32>), dim3(grid4), dim3(256), 0, s, (const T*)x, (const T*)w, (const T*)b, (T*)y, rows, N, e);
+    hipLaunchKernelGGL((layer_norm_kernel<T, P, 32>), dim3(grid4), dim3(256), 0, s, xp, wp, bp, yp, rows, N, e);
   else
-    hipLaunchKernelGGL(layer_norm_long_kernel<T>, dim3((unsigned)rows), dim3(256), 0, s, (const T*)x, (const T*)w, (const T*)b, (T*)y, N, e);
+    hipLaunchKernelGGL((layer_norm_long_kernel<T, P>), dim3((unsigned)rows), dim3(256), 0, s, xp, wp, bp, yp, N, e);
   return check_launch("layer_norm_kernel");
 }
 
@@ -531,22 +540,31 @@ using namespace mthip;
 
 extern "C" {
 
+// Data / parameter dtype pairs: (F16, F16), (F32, F32) and (F16, F32) -- the last one is the
+// upcast pattern norm(x.float(), w32, b32).half().
+static bool norm_dtypes_ok(int dtype, int param_dtype) {
+  return (dtype == MTHIP_F16 || dtype == MTHIP_F32) && (param_dtype == dtype || (dtype == MTHIP_F16 && param_dtype == MTHIP_F32));
+}
+
 int mthip_group_norm(int device, int dtype, const void* x, const void* weight, const void* bias, void* y, int64_t B,
-                     int64_t C, int64_t inner, int64_t groups, double eps, int fuse_silu) {
-  MTHIP_REQUIRE(dtype == MTHIP_F16 || dtype == MTHIP_F32, "mthip_group_norm: dtype must be F16 or F32");
+                     int64_t C, int64_t inner, int64_t groups, double eps, int fuse_silu, int param_dtype) {
+  MTHIP_REQUIRE(norm_dtypes_ok(dtype, param_dtype), "mthip_group_norm: unsupported dtype / param_dtype pair");
   MTHIP_REQUIRE(groups > 0 && C % groups == 0, "mthip_group_norm: num_channels must be divisible by num_groups");
   MTHIP_REQUIRE(B >= 0 && inner >= 0, "mthip_group_norm: negative extent");
   hipStream_t s = stream_for(device);
   if (!s) return MTHIP_ERR_HIP;
   if (int rc = use_device(device)) return rc;
-  if (dtype == MTHIP_F16)
-    return run_group_norm<uint16_t>(device, x, weight, bias, y, B, C, inner, groups, eps, fuse_silu, false, C, s);
-  return run_group_norm<float>(device, x, weight, bias, y, B, C, inner, groups, eps, fuse_silu, false, C, s);
+  if (dtype == MTHIP_F32)
+    return run_group_norm<float, float>(device, x, weight, bias, y, B, C, inner, groups, eps, fuse_silu, false, C, s);
+  if (param_dtype == MTHIP_F32)
+    return run_group_norm<uint16_t, float>(device, x, weight, bias, y, B, C, inner, groups, eps, fuse_silu, false, C, s);
+  return run_group_norm<uint16_t, uint16_t>(device, x, weight, bias, y, B, C, inner, groups, eps, fuse_silu, false, C, s);
 }
 
 int mthip_group_norm_nhwc(int device, int dtype, const void* x, const void* weight, const void* bias, void* y_nhwc,
-                          int64_t B, int64_t C, int64_t HW, int64_t groups, double eps, int fuse_silu) {
-  MTHIP_REQUIRE(dtype == MTHIP_F16 || dtype == MTHIP_F32, "mthip_group_norm_nhwc: dtype must be F16 or F32");
+                          int64_t B, int64_t C, int64_t HW, int64_t groups, double eps, int fuse_silu,
+                          int param_dtype) {
+  MTHIP_REQUIRE(norm_dtypes_ok(dtype, param_dtype), "mthip_group_norm_nhwc: unsupported dtype / param_dtype pair");
   MTHIP_REQUIRE(groups > 0 && C % groups == 0, "mthip_group_norm_nhwc: num_channels must be divisible by num_groups");
   MTHIP_REQUIRE(B >= 0 && HW >= 0 && B <= 65535, "mthip_group_norm_nhwc: bad extents");
   hipStream_t s = stream_for(device);
@@ -554,21 +572,25 @@ int mthip_group_norm_nhwc(int device, int dtype, const void* x, const void* weig
   if (int rc = use_device(device)) return rc;
   const int64_t vec = dtype == MTHIP_F16 ? 8 : 4;
   const int64_t Cp = ceil_div(C, vec) * vec;
-  if (dtype == MTHIP_F16)
-    return run_group_norm<uint16_t>(device, x, weight, bias, y_nhwc, B, C, HW, groups, eps, fuse_silu, true, Cp, s);
-  return run_group_norm<float>(device, x, weight, bias, y_nhwc, B, C, HW, groups, eps, fuse_silu, true, Cp, s);
+  if (dtype == MTHIP_F32)
+    return run_group_norm<float, float>(device, x, weight, bias, y_nhwc, B, C, HW, groups, eps, fuse_silu, true, Cp, s);
+  if (param_dtype == MTHIP_F32)
+    return run_group_norm<uint16_t, float>(device, x, weight, bias, y_nhwc, B, C, HW, groups, eps, fuse_silu, true, Cp, s);
+  return run_group_norm<uint16_t, uint16_t>(device, x, weight, bias, y_nhwc, B, C, HW, groups, eps, fuse_silu, true, Cp,
+                                            s);
 }
 
 int mthip_layer_norm(int device, int dtype, const void* x, const void* weight, const void* bias, void* y, int64_t rows,
-                     int64_t N, double eps) {
-  MTHIP_REQUIRE(dtype == MTHIP_F16 || dtype == MTHIP_F32, "mthip_layer_norm: dtype must be F16 or F32");
+                     int64_t N, double eps, int param_dtype) {
+  MTHIP_REQUIRE(norm_dtypes_ok(dtype, param_dtype), "mthip_layer_norm: unsupported dtype / param_dtype pair");
   MTHIP_REQUIRE(rows >= 0 && N >= 0, "mthip_layer_norm: negative extent");
   MTHIP_REQUIRE(rows <= 0x7fffffffLL * 4, "mthip_layer_norm: too many rows");
   hipStream_t s = stream_for(device);
   if (!s) return MTHIP_ERR_HIP;
   if (int rc = use_device(device)) return rc;
-  if (dtype == MTHIP_F16) return run_layer_norm<uint16_t>(x, weight, bias, y, rows, N, eps, s);
-  return run_layer_norm<float>(x, weight, bias, y, rows, N, eps, s);
+  if (dtype == MTHIP_F32) return run_layer_norm<float, float>(x, weight, bias, y, rows, N, eps, s);
+  if (param_dtype == MTHIP_F32) return run_layer_norm<uint16_t, float>(x, weight, bias, y, rows, N, eps, s);
+  return run_layer_norm<uint16_t, uint16_t>(x, weight, bias, y, rows, N, eps, s);
 }
 
 int mthip_softmax_lastdim(int device, int dtype, const void* x, void* y, int64_t rows, int64_t cols, int divide) {
