@@ -174,6 +174,16 @@ int mthip_linear(int device, int dtype, const void* x, int64_t lda, const void* 
  * narrowed as narrow(beta*c_in) before alpha*product is added, as addmm does
  * (tensor.cpp:25253-25258, 25320-25334).  Serves matmul (tensor.cpp:24896-25064),
  * batched_matmul (:24822-24894), bmm (:25066) and addmm (:25184-25366). */
+/* The SD feed-forward's GEGLU input projection in one GEMM: for h = x . W^T + b with
+ * W = [W_value; W_gate] ([2N, K]), y[M, N] = h[:, :N] * gelu(h[:, N:]) -- the reference's
+ * linear (tensor.cpp:31401) -> chunk(2, -1) (:12519) -> gelu (:17207) -> mul (:18965)
+ * sequence, each intermediate narrowed as it narrows them.  w/b must be given with their rows
+ * interleaved in 32-row blocks: rows [64q, 64q+32) = W_value[32q, 32q+32) and rows
+ * [64q+32, 64q+64) = W_gate[32q, 32q+32) (b likewise; N a multiple of 32); b may be NULL.
+ * x, w 16-byte aligned, K a multiple of 8 (F16) / 4 (F32) elements. */
+int mthip_linear_geglu(int device, int dtype, const void* x, int64_t lda, const void* w, const void* b,
+                       void* y, int64_t ldy, int64_t M, int64_t N, int64_t K);
+
 int mthip_gemm(int device, int dtype, int64_t batch, int64_t M, int64_t N, int64_t K,
                const void* a, int64_t lda, int64_t stride_a,
                const void* b, int64_t ldb, int64_t stride_b, int b_trans,

@@ -55,6 +55,8 @@ _SIGNATURES = {
     "mthip_geglu": (_int, [_int, _int, _c_void_p, _c_void_p, _i64, _i64]),
     "mthip_linear": (_int, [_int, _int, _c_void_p, _i64, _c_void_p, _i64, _c_void_p, _c_void_p, _i64,
                             _i64, _i64, _i64, _int, _c_void_p, _i64]),
+    "mthip_linear_geglu": (_int, [_int, _int, _c_void_p, _i64, _c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i64,
+                                  _i64]),
     "mthip_gemm": (_int, [_int, _int, _i64, _i64, _i64, _i64, _c_void_p, _i64, _i64, _c_void_p, _i64, _i64,
                           _int, _c_void_p, _i64, _i64, _dbl, _dbl, _c_void_p, _i64, _i64, _i64]),
     "mthip_conv2d": (_int, [_int, _int, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i64, _i64,

@@ -376,6 +376,52 @@ def linear(x: Tensor, w: Tensor, b: Tensor = None, act: int = ACT_NONE, residual
     return out
 
 
+def linear_geglu(x: Tensor, w: Tensor, b: Tensor = None) -> Tensor:
+    """a * gelu(gate) with (a, gate) = linear(x, w, b).chunk(2, dim=-1): the GEGLU projection of
+    the SD feed-forward as one GEMM whose epilogue pairs each value column with its gate
+    (mthip_linear_geglu); the weight/bias row interleave it needs is built once per weight
+    version and kept on the weight's storage.  Shapes the fused kernel does not take run as
+    linear then geglu."""
+    _same_dtype("linear", [x, w, b])
+    dev = _gpu("linear", x, w, b)
+    if w.dim() != 2 or x.dim() < 1 or w.shape[1] != x.shape[-1]:
+        raise ValueError("linear input and weight shapes cannot be multiplied")
+    K, N2 = x.shape[-1], w.shape[0]
+    vec = 8 if x.dtype is T.float16 else 4
+    rv = _rows_view(x)
+    if N2 % 64 or K % vec or (b is not None and list(b.shape) != [N2]) or rv is None or rv[1] % vec \
+            or x.data_ptr() % 16 or not w.is_contiguous() or w.data_ptr() % 16:
+        return geglu(linear(x, w, b))
+    _float_dtype("linear", x.dtype)
+    M, lda = rv
+    N = N2 // 2
+    wp, bp = _geglu_packed(w, b)
+    out = _empty(list(x.shape[:-1]) + [N], x.dtype, dev)
+    if out.numel():
+        _lib.check(_L().mthip_linear_geglu(dev, x.dtype.code, x.data_ptr(), lda, wp.data_ptr(), _ptr(bp), out.data_ptr(),
+                                           N, M, N, K))
+    return out
+
+
+def _geglu_packed(w: Tensor, b: Tensor):
+    """w/b with rows interleaved in 32-row blocks (value block q, then gate block q), cached on
+    w's storage and rebuilt after an in-place write to w or b."""
+    st = w._storage
+    N2, K = w.shape
+    key = ("geglu", w._offset, N2, K, id(b._storage) if b is not None else None, b._offset if b is not None else 0)
+    ver = (st.version, b._storage.version if b is not None else 0)
+    if st.packs is None:
+        st.packs = {}
+    hit = st.packs.get(key)
+    if hit is not None and hit[0] == ver:
+        return hit[1], hit[2]
+    q = N2 // 64
+    wp = w.reshape(2, q, 32, K).permute(1, 0, 2, 3).contiguous().reshape(N2, K)
+    bp = b.reshape(2, q, 32).permute(1, 0, 2).contiguous().reshape(N2) if b is not None else None
+    st.packs[key] = (ver, wp, bp)
+    return wp, bp
+
+
 def _gemm(a: Tensor, b: Tensor, out: Tensor, batch, M, N, K, sa, sb, alpha=1.0, beta=0.0, c_in=None,
           c_rs=0, c_cs=0, c_bs=0):
     """out[batch,M,N] = alpha*a.b (+beta*c_in); a/b are [batch?, M, K] / [batch?, K, N] views."""
@@ -825,7 +871,7 @@ def _norm_param_dtype(op: str, x: Tensor, weight: Tensor, bias: Tensor) -> int:
         return x.dtype.code
     if dts == {T.float32} and x.dtype is T.float16:
         return T.float32.code
-    raise ValueError(f"expected {op} input and parameters to have the same dtype")
+    raise RuntimeError(f"expected {op} tensors to have the same dtype")
 
 
 def _group_norm_check(x: Tensor, num_groups: int, weight: Tensor, bias: Tensor):

@@ -9,9 +9,14 @@
 #include "common.h"
 
 namespace mthip {
+// These run inside kernels built with contraction on (the GEMM epilogues): every body turns
+// it off so each multiply and add rounds separately, as the reference's x86-64 build (no FMA)
+// evaluates them.
+
 // fp32 GELU exactly as the reference's Linux fp32 path: truncated series for |x| <= 1,
 // else Abramowitz-Stegun 7.1.26 erf (tensor.cpp:17132-17154, 17265-17273).
 __device__ __forceinline__ float gelu_ref_f32(float x) {
+#pragma clang fp contract(off)
   if (fabsf(x) <= 1.0f) {
     const float inv_sqrt_two_pi = 0.39894228040143267794f;
     const float x2 = x * x;
@@ -31,15 +36,18 @@ __device__ __forceinline__ float gelu_ref_f32(float x) {
 // fp16 GELU: the reference evaluates 0.5*x*(1+erf(x/sqrt 2)) in double (tensor.cpp:17103-17113,
 // 17225-17235); doubles are cheap next to the HBM traffic of this op.
 __device__ __forceinline__ float gelu_ref_f16(float xf) {
+#pragma clang fp contract(off)
   const double x = (double)xf;
   return (float)(0.5 * x * (1.0 + erf(x * 0.70710678118654752440)));
 }
 
 __device__ __forceinline__ float gelu_tanh_f32(float x) {
+#pragma clang fp contract(off)
   return 0.5f * x * (1.0f + tanhf(0.79788456080286535588f * (x + 0.044715f * x * x * x)));
 }
 
 __device__ __forceinline__ float gelu_tanh_f16(float xf) {
+#pragma clang fp contract(off)
   const double x = (double)xf;
   return (float)(0.5 * x * (1.0 + tanh(0.79788456080286535588 * (x + 0.044715 * x * x * x))));
 }
@@ -49,6 +57,7 @@ __device__ __forceinline__ float apply_unary(int op, float x);
 
 template <>
 __device__ __forceinline__ float apply_unary<float>(int op, float x) {
+#pragma clang fp contract(off)
   switch (op) {
     case MTHIP_UNARY_SILU: return x / (1.0f + expf(-x));
     case MTHIP_UNARY_GELU: return gelu_ref_f32(x);
@@ -64,6 +73,7 @@ __device__ __forceinline__ float apply_unary<float>(int op, float x) {
 
 template <>
 __device__ __forceinline__ float apply_unary<uint16_t>(int op, float x) {
+#pragma clang fp contract(off)
   switch (op) {
     case MTHIP_UNARY_SILU: return x / (1.0f + expf(-x));
     case MTHIP_UNARY_GELU: return gelu_ref_f16(x);

@@ -49,11 +49,11 @@ int cu_count(int device) {
 }
 
 // Resident workgroups per CU of one kernel instance (registers and LDS decide it).
-template <typename T, int BM, int BN, int MODE, int EPI, int ACT, bool FAST>
+template <typename T, int BM, int BN, int MODE, int EPI, int ACT, bool FAST, int WGM = 2>
 int resident_per_cu() {
   static const int v = [] {
     int n = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, gemm_kernel<T, BM, BN, 2, MODE, EPI, ACT, FAST>, 256, 0) !=
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, gemm_kernel<T, BM, BN, WGM, MODE, EPI, ACT, FAST>, 256, 0) !=
             hipSuccess ||
         n < 1)
       n = 1;
@@ -64,14 +64,14 @@ int resident_per_cu() {
 
 // Sizes the persistent grid, splits K when the output tiles cannot fill the chip, launches the
 // GEMM (and the slice reduction).
-template <typename T, int BM, int BN, int MODE, int EPI, int ACT, bool FAST>
+template <typename T, int BM, int BN, int MODE, int EPI, int ACT, bool FAST, int WGM = 2>
 int launch_tile(int device, GemmArgs a, int64_t batch, hipStream_t s) {
   constexpr int BK = Mfma<T>::BK;
   a.tiles_m = ceil_div(a.M, BM);
   a.tiles_n = ceil_div(a.N, BN);
   const int64_t nk = std::max<int64_t>(ceil_div(a.K, BK), 1);
   const int64_t tiles = a.tiles_m * a.tiles_n * batch;
-  const int64_t slots = (int64_t)cu_count(device) * resident_per_cu<T, BM, BN, MODE, EPI, ACT, FAST>();
+  const int64_t slots = (int64_t)cu_count(device) * resident_per_cu<T, BM, BN, MODE, EPI, ACT, FAST, WGM>();
   int64_t ksplit = 1;
   // Split K only for single-batch problems with fewer tiles than about `split_target` units
   // per CU and >= 32 K tiles, into enough slices to reach that, each slice keeping >= 16 K
@@ -79,7 +79,7 @@ int launch_tile(int device, GemmArgs a, int64_t batch, hipStream_t s) {
   // amortises (the 3x3 convs gain 5-15% at 320 channels and 1.5-4x at 640-1280; linears with
   // K <= 1280 are left alone).
   const int64_t target = (int64_t)cu_count(device) * split_target();
-  if (batch == 1 && tiles < target && nk >= 32 && splitk_enabled())
+  if (batch == 1 && tiles < target && nk >= 32 && splitk_enabled() && EPI != EPI_GEGLU)
     ksplit = std::max<int64_t>(1, std::min<int64_t>(std::min<int64_t>(ceil_div(target, tiles), nk / 16), 16));
   a.kt_per_split = ceil_div(nk, ksplit);
   a.ksplit = ceil_div(nk, a.kt_per_split);  // no empty slice
@@ -106,8 +106,9 @@ int launch_tile(int device, GemmArgs a, int64_t batch, hipStream_t s) {
     if (int rc = mthip_malloc(device, (size_t)(a.ksplit * a.M * a.ld_partial) * sizeof(float), &ws)) return rc;
     a.partial = static_cast<float*>(ws);
   }
-  hipLaunchKernelGGL((gemm_kernel<T, BM, BN, 2, MODE, EPI, ACT, FAST>), dim3((unsigned)g), dim3(256), 0, s, a);
+  hipLaunchKernelGGL((gemm_kernel<T, BM, BN, WGM, MODE, EPI, ACT, FAST>), dim3((unsigned)g), dim3(256), 0, s, a);
   int rc = check_launch("gemm_kernel");
+  if constexpr (EPI == EPI_GEGLU) return rc;
   if (rc == MTHIP_OK && a.ksplit > 1) {
     const int64_t work = a.M * ceil_div(a.N, 4);
     const unsigned rg = (unsigned)std::min<int64_t>(ceil_div(work, 256), 8192);
@@ -184,6 +185,34 @@ int pad_operand(int device, hipStream_t s, const void* src, int64_t batches, int
 }
 
 constexpr int64_t kMaxBufferBytes = (int64_t(1) << 31) - 1;
+
+// fp16 gelu of every half value, as mtorch's fp16 path computes it (tensor.cpp:17225-17235):
+// a GEGLU gate is always an fp16 value, so the fused epilogue looks its gelu up instead of
+// evaluating a double-precision erf per element.  Filled once per device.
+__device__ uint16_t g_gelu_f16_table[65536];
+
+__global__ void gelu_f16_table_kernel(uint16_t* tab) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < 65536) tab[i] = f2h_fast(gelu_ref_f16(h2f_exact((uint16_t)i)));
+}
+
+const uint16_t* gelu_f16_table(int device, hipStream_t s) {
+  static const uint16_t* ptr[64] = {nullptr};
+  if (device < 0 || device >= 64) return nullptr;
+  if (!ptr[device]) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(g_gelu_f16_table)) != hipSuccess) return nullptr;
+    hipLaunchKernelGGL(gelu_f16_table_kernel, dim3(256), dim3(256), 0, s, static_cast<uint16_t*>(p));
+    if (hipGetLastError() != hipSuccess) return nullptr;
+    // Under stream capture the fill is only recorded (it runs with each replay, ahead of the
+    // GEMM that reads the table), so the table counts as ready only after an eager fill.
+    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(s, &st) != hipSuccess) return nullptr;
+    if (st != hipStreamCaptureStatusNone) return static_cast<const uint16_t*>(p);
+    ptr[device] = static_cast<const uint16_t*>(p);
+  }
+  return ptr[device];
+}
 
 }  // namespace
 
@@ -263,6 +292,42 @@ int mthip_linear(int device, int dtype, const void* x, int64_t lda, const void* 
   mthip_free(device, xp);  // stream-ordered: reused only by later work
   mthip_free(device, wp);
   return rc;
+}
+
+int mthip_linear_geglu(int device, int dtype, const void* x, int64_t lda, const void* w, const void* b, void* y,
+                       int64_t ldy, int64_t M, int64_t N, int64_t K) {
+  MTHIP_REQUIRE(dtype == MTHIP_F16 || dtype == MTHIP_F32, "mthip_linear_geglu: dtype must be F16 or F32");
+  MTHIP_REQUIRE(M >= 0 && N >= 0 && K >= 0 && N % 32 == 0, "mthip_linear_geglu: N must be a multiple of 32");
+  MTHIP_REQUIRE(lda >= K && ldy >= N, "mthip_linear_geglu: leading dimension smaller than the row");
+  const int vec = dtype == MTHIP_F16 ? 8 : 4;
+  MTHIP_REQUIRE(aligned16(x) && aligned16(w) && lda % vec == 0 && K % vec == 0,
+                "mthip_linear_geglu: operands must be 16-byte aligned with K a multiple of 16 bytes");
+  if (M == 0 || N == 0) return MTHIP_OK;
+  hipStream_t s = stream_for(device);
+  if (!s) return MTHIP_ERR_HIP;
+  if (int rc = use_device(device)) return rc;
+  const int64_t es = dtype == MTHIP_F16 ? 2 : 4;
+  GemmArgs a{};
+  a.M = M;
+  a.N = 2 * N;  // interleaved value/gate columns
+  a.K = K;
+  a.a = x;
+  a.lda = lda;
+  a.b = w;
+  a.ldb = K;
+  a.c = y;
+  a.ldc = ldy;
+  a.bias = b;
+  a.a_bytes = ((M - 1) * lda + K) * es;
+  a.b_bytes = (2 * N * K) * es;
+  MTHIP_REQUIRE(a.a_bytes <= kMaxBufferBytes && a.b_bytes <= kMaxBufferBytes,
+                "mthip_linear_geglu: operands above 2 GiB are not supported");
+  if (dtype == MTHIP_F16) {
+    a.gelu_tab = gelu_f16_table(device, s);
+    if (!a.gelu_tab) return fail(MTHIP_ERR_HIP, "mthip_linear_geglu: gelu table setup failed");
+    return launch_tile<uint16_t, 128, 64, MODE_NT, EPI_GEGLU, MTHIP_ACT_NONE, false, 4>(device, a, 1, s);
+  }
+  return launch_tile<float, 128, 64, MODE_NT, EPI_GEGLU, MTHIP_ACT_NONE, false, 4>(device, a, 1, s);
 }
 
 int mthip_gemm(int device, int dtype, int64_t batch, int64_t M, int64_t N, int64_t K, const void* a_ptr, int64_t lda,

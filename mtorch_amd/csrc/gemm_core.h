@@ -45,7 +45,7 @@ typedef float floatx16 __attribute__((ext_vector_type(16)));
 typedef _Float16 halfx8 __attribute__((ext_vector_type(8)));
 
 enum { MODE_NT = 0, MODE_NN = 1, MODE_CONV = 2 };
-enum { EPI_LINEAR = 0, EPI_GEMM = 1, EPI_CONV = 2 };
+enum { EPI_LINEAR = 0, EPI_GEMM = 1, EPI_CONV = 2, EPI_GEGLU = 3 };
 
 template <typename T>
 struct Mfma;
@@ -107,6 +107,8 @@ struct GemmArgs {
   // Divisors of the index arithmetic (units, pixels and N stay below 2^31).
   FastDiv div_tiles_n, div_tiles_m, div_ksplit, div_ohw, div_ow;
   int xcd_remap;  // 1: number units XCD-contiguously (see decode_unit)
+  // EPI_GEGLU: gelu of every fp16 value (65536 entries, mtorch's fp16 gelu bit for bit)
+  const uint16_t* gelu_tab;
 };
 
 // Stores the first nv (1..4) of 4 consecutive outputs, narrowed once each; one 8-byte (fp16)
@@ -432,6 +434,46 @@ __global__ __launch_bounds__(256) void gemm_kernel(const GemmArgs args) {
   const int lane_col = 4 * (lane >> 5);
   auto finish_unit = [&](const GemmUnit& un) {
     const int M = (int)args.M;
+    if constexpr (EPI == EPI_GEGLU) {
+      // B rows come interleaved in 32-row blocks (values, then the matching gates), and each
+      // wave owns 64 columns = fragment 0 (values) + fragment 1 (gates) of 32 output columns:
+      // out[row][col] = value * gelu(gate), each factor narrowed as the unfused
+      // linear -> chunk -> gelu -> mul sequence narrows it.
+      static_assert(FN == 2 && WGN == 1 && BN == 64, "GEGLU epilogue pairs two 32-column fragments");
+      const T* bias = reinterpret_cast<const T*>(args.bias);
+      T* Cp = reinterpret_cast<T*>(args.c);
+      const int Nout = (int)args.N / 2;
+#pragma unroll
+      for (int i = 0; i < FM; ++i) {
+        const int row = (int)un.m0 + wm * WM + i * 32 + (lane & 31);
+        if (row < M) {
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            const int pc = (int)un.n0 + 8 * g + lane_col;  // permuted column of the value
+            const int col0 = (int)un.n0 / 2 + 8 * g + lane_col;
+            if (col0 < Nout) {
+              float v[4];
+#pragma unroll
+              for (int t = 0; t < 4; ++t) {
+                float val = acc[i][0][4 * g + t], gate = acc[i][1][4 * g + t];
+                if (bias) {
+                  val += Elem<T>::load(bias, pc + t);
+                  gate += Elem<T>::load(bias, pc + 32 + t);
+                }
+                if constexpr (sizeof(T) == 2) {
+                  const float gl = h2f_bits(args.gelu_tab[f2h_fast(gate)]);
+                  v[t] = h2f_bits(f2h_fast(val)) * gl;
+                } else {
+                  v[t] = val * gelu_ref_f32(gate);
+                }
+              }
+              store_cols<T>(Cp + (int64_t)row * args.ldc + col0, v, Nout - col0 < 4 ? Nout - col0 : 4);
+            }
+          }
+        }
+      }
+      return;
+    }
 #pragma unroll
     for (int i = 0; i < FM; ++i) {
       const int row = (int)un.m0 + wm * WM + i * 32 + (lane & 31);

@@ -72,6 +72,11 @@ def conv2d_residual(input, weight, bias, residual, stride=1, padding=0, dilation
     return _ops.conv2d(input, weight, bias, stride, padding, dilation, groups, residual=residual)
 
 
+def linear_geglu(input, weight, bias=None):
+    """a * gelu(gate) with (a, gate) = linear(input, weight, bias).chunk(2, dim=-1)"""
+    return _ops.linear_geglu(input, weight, bias)
+
+
 def geglu(input):
     """a * gelu(gate) with (a, gate) = input.chunk(2, dim=-1)"""
     return _ops.geglu(input)

@@ -140,11 +140,14 @@ class ResBlock(nn.Module):
         self.conv2 = _Conv(init, cout, cout, 3)
         self.shortcut = _Conv(init, cin, cout, 1) if cin != cout else None
 
-    def forward(self, x: Tensor, temb_silu: Tensor) -> Tensor:
+    def forward(self, x: Tensor, temb_silu: Tensor, t: Tensor | None = None) -> Tensor:
+        """t: this block's time projection linear(temb_silu) when the caller computed it already
+        (the UNet runs every block's projection as one GEMM)."""
         n1, n2 = self.norm1, self.norm2
         h = F.group_norm_silu_conv2d(x, n1.groups, n1.weight, n1.bias, n1.eps, self.conv1.weight, self.conv1.bias,
                                      padding=1)
-        t = F.linear(temb_silu, self.time_emb_proj.weight, self.time_emb_proj.bias)
+        if t is None:
+            t = F.linear(temb_silu, self.time_emb_proj.weight, self.time_emb_proj.bias)
         h = h + t.unsqueeze(-1).unsqueeze(-1)
         res = F.conv2d(x, self.shortcut.weight, self.shortcut.bias) if self.shortcut is not None else x
         return F.group_norm_silu_conv2d(h, n2.groups, n2.weight, n2.bias, n2.eps, self.conv2.weight, self.conv2.bias,
@@ -163,14 +166,17 @@ class Attention(nn.Module):
             self.to_kv = _Linear(init, ctx, 2 * C, bias=False)  # to_k, to_v stacked
         self.to_out = _Linear(init, C, C)
 
-    def forward(self, h: Tensor, residual: Tensor, context: Tensor | None = None) -> Tensor:
+    def forward(self, h: Tensor, residual: Tensor, context: Tensor | None = None, kv: Tensor | None = None) -> Tensor:
+        """kv: this block's context projection linear(context, to_kv) when the caller computed
+        it already (the UNet projects the context for every cross-attention in one GEMM)."""
         C = h.shape[-1]
         if self.self_attn:
             qkv = F.linear(h, self.to_qkv.weight)
             q, k, v = qkv[..., :C], qkv[..., C:2 * C], qkv[..., 2 * C:]
         else:
             q = F.linear(h, self.to_q.weight)
-            kv = F.linear(context, self.to_kv.weight)
+            if kv is None:
+                kv = F.linear(context, self.to_kv.weight)
             k, v = kv[..., :C], kv[..., C:]
         o = _attention_tokens(q, k, v, self.heads)
         return F.linear_residual(o, self.to_out.weight, self.to_out.bias, residual)
@@ -193,13 +199,13 @@ class SpatialTransformer(nn.Module):
         self.ff_out = _Linear(init, 4 * C, C)
         self.proj_out = _Conv(init, C, C, 1)
 
-    def forward(self, x: Tensor, context: Tensor) -> Tensor:
+    def forward(self, x: Tensor, context: Tensor, kv: Tensor | None = None) -> Tensor:
         B, C, H, W = x.shape
         tok = _tokens_nhwc(x, self.norm)
         tok = F.linear(tok, self.proj_in.weight.view(C, C), self.proj_in.bias)
         tok = self.attn1(_layer_norm(tok, self.norm1), tok)
-        tok = self.attn2(_layer_norm(tok, self.norm2), tok, context)
-        ff = F.geglu(F.linear(_layer_norm(tok, self.norm3), self.ff_in.weight, self.ff_in.bias))
+        tok = self.attn2(_layer_norm(tok, self.norm2), tok, context, kv)
+        ff = F.linear_geglu(_layer_norm(tok, self.norm3), self.ff_in.weight, self.ff_in.bias)
         tok = F.linear_residual(ff, self.ff_out.weight, self.ff_out.bias, tok)
         return _ops.conv2d_tokens(tok, self.proj_out.weight, self.proj_out.bias, H, W, residual=x)
 
@@ -284,12 +290,52 @@ class UNet(nn.Module):
         self.norm_out = _GN(init, ch[0], 1e-5)
         self.conv_out = _Conv(init, ch[0], 4, 3)
         self.freqs = timestep_frequencies(ch[0], device)
+        object.__setattr__(self, "_stack_cache", {})
+
+    def _stacked(self, name: str, linears) -> tuple:
+        """Weights (and biases) of several linears that read the same input, concatenated along
+        the output dimension so they run as one GEMM; rebuilt whenever one of the parameters
+        was written in place (storage version), like the packed conv weights."""
+        import mtorch_amd as mt
+
+        params = [p for lin in linears for p in (lin.weight, lin.bias) if p is not None]
+        key = tuple((id(p._storage), p._storage.version) for p in params)
+        hit = self._stack_cache.get(name)
+        if hit is None or hit[0] != key:
+            w = mt.cat([lin.weight for lin in linears], dim=0)
+            b = mt.cat([lin.bias for lin in linears], dim=0) if linears[0].bias is not None else None
+            offs = np.cumsum([0] + [lin.weight.shape[0] for lin in linears]).tolist()
+            hit = (key, w, b, offs)
+            self._stack_cache[name] = hit
+        return hit[1], hit[2], hit[3]
+
+    def _blocks(self):
+        for blocks in list(self.down) + [self.mid] + list(self.up):
+            yield from blocks
 
     def forward(self, latent: Tensor, timesteps: Tensor, context: Tensor) -> Tensor:
+        import mtorch_amd as mt
+
         emb = timestep_embedding(timesteps, self.freqs).half()
         emb = F.linear_silu(emb, self.time1.weight, self.time1.bias)
         emb = F.linear(emb, self.time2.weight, self.time2.bias)
         temb_silu = F.silu(emb)  # every ResBlock's time projection reads silu(emb)
+        # all ResBlock time projections as one GEMM, all cross-attention K/V projections as another
+        res_blocks = [b for b in self._blocks() if isinstance(b, ResBlock)]
+        tw, tb, toff = self._stacked("time", [b.time_emb_proj for b in res_blocks])
+        t_all = F.linear(temb_silu, tw, tb)
+        t_of = {id(b): t_all[:, toff[i]:toff[i + 1]] for i, b in enumerate(res_blocks)}
+        xf_blocks = [b for b in self._blocks() if isinstance(b, SpatialTransformer)]
+        kw, _, koff = self._stacked("kv", [b.attn2.to_kv for b in xf_blocks])
+        kv_all = F.linear(context, kw)
+        kv_of = {id(b): kv_all[..., koff[i]:koff[i + 1]] for i, b in enumerate(xf_blocks)}
+
+        def res(blk, x):
+            return blk(x, temb_silu, t_of[id(blk)])
+
+        def xf(blk, x):
+            return blk(x, context, kv_of[id(blk)])
+
         h = F.conv2d(latent, self.conv_in.weight, self.conv_in.bias, padding=1)
         skips = [h]
         for blocks in self.down:
@@ -297,28 +343,26 @@ class UNet(nn.Module):
             i = 0
             while i < len(items):
                 if isinstance(items[i], ResBlock):
-                    h = items[i](h, temb_silu)
+                    h = res(items[i], h)
                     if i + 1 < len(items) and isinstance(items[i + 1], SpatialTransformer):
                         i += 1
-                        h = items[i](h, context)
+                        h = xf(items[i], h)
                 else:  # Downsample
                     h = items[i](h)
                 skips.append(h)
                 i += 1
-        h = self.mid[0](h, temb_silu)
-        h = self.mid[1](h, context)
-        h = self.mid[2](h, temb_silu)
-        import mtorch_amd as mt
-
+        h = res(self.mid[0], h)
+        h = xf(self.mid[1], h)
+        h = res(self.mid[2], h)
         for blocks in self.up:
             items = list(blocks)
             i = 0
             while i < len(items):
                 if isinstance(items[i], ResBlock):
-                    h = items[i](mt.cat([h, skips.pop()], dim=1), temb_silu)
+                    h = res(items[i], mt.cat([h, skips.pop()], dim=1))
                     if i + 1 < len(items) and isinstance(items[i + 1], SpatialTransformer):
                         i += 1
-                        h = items[i](h, context)
+                        h = xf(items[i], h)
                 else:  # Upsample
                     h = items[i](h)
                 i += 1

@@ -139,6 +139,49 @@ def test_activations(dt):
         assert rel(val(got), val(ref)) <= (2e-6 if dt == "float32" else 1e-3), name
 
 
+@pytest.mark.parametrize("dt", ["float32", "float16"])
+@pytest.mark.parametrize("M,N,K,bias", [(77, 64, 40, True), (300, 320, 96, True), (128, 128, 64, False), (8192, 2560, 320, True)])
+def test_linear_geglu_fused(dt, M, N, K, bias):
+    """The GEGLU epilogue (value/gate pairing over interleaved weight rows, gelu table lookup)
+    equals linear -> geglu bit for bit, and the oracle's linear -> chunk -> gelu -> mul within
+    tolerance."""
+    g = Gen(M + N + K)
+    x = g.randn((M, K), dt)
+    w = g.randn((2 * N, K), dt, 1.0 / np.sqrt(K))
+    b = g.randn((2 * N,), dt) if bias else None
+    xd, wd, bd = dev(x), dev(w), (dev(b) if bias else None)
+    fused = host(F.linear_geglu(xd, wd, bd))
+    unfused = host(F.geglu(F.linear(xd, wd, bd)))
+    assert np.array_equal(fused, unfused)
+    if M * N <= 300 * 320:
+        lin = orc.linear(x, w, b)
+        ref = orc.binary(np.ascontiguousarray(lin[:, :N]), orc.gelu(np.ascontiguousarray(lin[:, N:])), "mul")
+        assert rel(val(fused), val(ref)) <= TOL[dt]
+
+
+def test_norm_upcast_pattern():
+    """fp32 norm parameters over fp16 data: norm(x.float(), w32, b32).half() in one kernel."""
+    from mtorch_amd import _ops
+
+    g = Gen(81)
+    x = g.randn((2, 64, 8, 8), "float16")
+    w = g.randn((64,), "float32")
+    b = g.randn((64,), "float32")
+    got = host(_ops.group_norm(dev(x), 8, dev(w), dev(b), 1e-5, allow_upcast=True))
+    ref = orc.f2h(orc.group_norm(orc.h2f(x), 8, w, b, 1e-5))
+    assert got.dtype == np.uint16 and rel(val(got), val(ref)) <= 2e-3
+    got = host(_ops.group_norm(dev(x), 8, dev(w), dev(b), 1e-5, fuse_silu=True, allow_upcast=True))
+    assert rel(val(got), val(orc.silu(ref))) <= 2e-3
+    t = g.randn((3, 77, 320), "float16")
+    lw = g.randn((320,), "float32")
+    lb = g.randn((320,), "float32")
+    got = host(_ops.layer_norm(dev(t), [320], dev(lw), dev(lb), 1e-5, allow_upcast=True))
+    ref = orc.f2h(orc.layer_norm(orc.h2f(t), 320, lw, lb, 1e-5))
+    assert rel(val(got), val(ref)) <= 2e-3
+    with pytest.raises(RuntimeError, match="same dtype"):
+        F.layer_norm(dev(t), [320], dev(lw), dev(lb))  # the public op keeps the same-dtype rule
+
+
 def test_geglu_matches_chunk_gelu_mul():
     g = Gen(13)
     x = g.randn((2, 17, 64), "float16", 2.0)
