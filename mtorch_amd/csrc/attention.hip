@@ -175,6 +175,7 @@ __global__ __launch_bounds__(64 * WAVES) void flash_fwd_f16_kernel(const FlashAr
     for (int r = 0; r < 16; ++r) acc[i][r] = 0.0f;
   float m_run = -INFINITY, l_run = 0.0f;
   const float sl2 = a.scale * kLog2e;
+  const float inv_scale = 1.0f / a.scale;
   const bool qok = q < a.Lq;
   const int mask_kind = MASK >= 0 ? MASK : a.mask_kind;
   // This lane's mask row (query q of head `head`), addressed per key by one 32-bit multiply.
@@ -199,8 +200,10 @@ __global__ __launch_bounds__(64 * WAVES) void flash_fwd_f16_kernel(const FlashAr
     __syncthreads();
     if (kv0 + BKV < Lk) fetch(kv0 + BKV);  // next tile's loads overlap this tile's math
 
+    // Raw scores (unscaled; an additive mask enters divided by the scale) and their max.
     float s[2][16];
     float mx = -INFINITY;
+    const bool checked = kv0 + BKV > Lk || a.causal || mask_kind != MTHIP_MASK_NONE;
 #pragma unroll
     for (int sb = 0; sb < 2; ++sb) {
       floatx16 t;
@@ -211,43 +214,57 @@ __global__ __launch_bounds__(64 * WAVES) void flash_fwd_f16_kernel(const FlashAr
         const halfx8 kf = *reinterpret_cast<const halfx8*>(&Ks[(sb * 32 + col) * KP + st * 16 + hh * 8]);
         t = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[st], t, 0, 0, 0);
       }
+      if (!checked) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int key = kv0 + sb * 32 + 8 * (r >> 2) + 4 * hh + (r & 3);
-        float v = t[r] * sl2;
-        if (key >= Lk) {
-          v = -INFINITY;
-        } else {
-          if (a.causal && key > q) v = -INFINITY;
-          if (mask_kind == MTHIP_MASK_BOOL) {
-            if (qok && !mrow_b[key * mk]) v = -INFINITY;
-          } else if (mask_kind == MTHIP_MASK_ADD && qok) {
-            v += (mrow_h ? h2f_bits(mrow_h[key * mk]) : mrow_f[key * mk]) * kLog2e;
-          }
+        for (int r = 0; r < 16; ++r) {
+          s[sb][r] = t[r];
+          mx = fmaxf(mx, t[r]);
         }
-        s[sb][r] = v;
-        mx = fmaxf(mx, v);
+      } else {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int key = kv0 + sb * 32 + 8 * (r >> 2) + 4 * hh + (r & 3);
+          float v = t[r];
+          if (key >= Lk) {
+            v = -INFINITY;
+          } else {
+            if (a.causal && key > q) v = -INFINITY;
+            if (mask_kind == MTHIP_MASK_BOOL) {
+              if (qok && !mrow_b[key * mk]) v = -INFINITY;
+            } else if (mask_kind == MTHIP_MASK_ADD && qok) {
+              v += (mrow_h ? h2f_bits(mrow_h[key * mk]) : mrow_f[key * mk]) * inv_scale;
+            }
+          }
+          s[sb][r] = v;
+          mx = fmaxf(mx, v);
+        }
       }
     }
     mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    const float m_new = fmaxf(m_run, mx);
-    const float m_use = m_new == -INFINITY ? 0.0f : m_new;
-    const float alpha = exp2f(m_run - m_use);
+    // Lazy rescaling: the running max (log2 units) moves only when a score exceeds it by more
+    // than 8, so P <= 2^8 (exact in fp16 and in the fp32 sums) and most tiles skip the
+    // accumulator rescale.  O = acc / l is unchanged by the choice of reference max.
+    const float m_cand = fmaxf(m_run, mx * sl2);
+    if (m_cand > m_run + 8.0f) {
+      const float alpha = __builtin_amdgcn_exp2f(m_run - m_cand);  // 0 when m_run = -inf
+      l_run *= alpha;
+#pragma unroll
+      for (int i = 0; i < DVB; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[i][r] *= alpha;
+      m_run = m_cand;
+    }
+    const float m_use = m_run == -INFINITY ? 0.0f : m_run;
     float psum = 0.0f;
 #pragma unroll
     for (int sb = 0; sb < 2; ++sb)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        s[sb][r] = exp2f(s[sb][r] - m_use);
+        s[sb][r] = __builtin_amdgcn_exp2f(fmaf(s[sb][r], sl2, -m_use));
         psum += s[sb][r];
       }
     psum += __shfl_xor(psum, 32, 64);
-    l_run = l_run * alpha + psum;
-    m_run = m_new;
-#pragma unroll
-    for (int i = 0; i < DVB; ++i)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][r] *= alpha;
+    l_run += psum;
 
     // O^T += V^T . P^T, four 16-key steps.
 #pragma unroll
