@@ -21,11 +21,11 @@ TileKind pick_tile(int MODE, int64_t M, int64_t N, int64_t batch) {
   }
   (void)M;
   (void)batch;
-  // Measured on the SD-UNet shapes: implicit-GEMM convs with >= 512 output pixels (16x16 and
-  // up at batch 2) run 5-20% faster on 128x128 tiles (64x64 waves: half the LDS reads per
-  // MFMA); the 8x8 convs and every linear (K = 320..1280, thin N) prefer 64x64, whose four
-  // resident workgroups per CU hide the short K loops' load latency.
-  if (MODE == MODE_CONV && N >= 512) return T128x128;
+  // 64x64 everywhere: in isolation 128x128 tiles ran some large convs 5-20% faster, but inside
+  // the UNet step (bias/residual epilogues, split-K interplay) they were 13% slower in total;
+  // the four resident 64x64 workgroups per CU also hide the short K loops of the linears.
+  (void)MODE;
+  (void)N;
   return T64x64;
 }
 
