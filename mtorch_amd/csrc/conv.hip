@@ -127,6 +127,7 @@ int run_conv_gemm_nhwc(int device, int dtype, const void* xp, const void* wp, co
   a.OH = OH;
   a.OW = OW;
   a.KW = KW;
+  a.KH_ = KH;
   a.sh = sh;
   a.sw = sw;
   a.ph = ph;

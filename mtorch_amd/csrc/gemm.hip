@@ -220,14 +220,16 @@ const uint16_t* gelu_f16_table(int device, hipStream_t s) {
 
 }  // namespace
 
-// Shared with conv.hip.
+// Shared with conv.hip.  The fast im2col (tap bitmasks) needs Cp % BK == 0 and <= 32 taps.
 int launch_conv_gemm(int device, int dtype, const GemmArgs& a, hipStream_t s) {
   // With the padded channel count a multiple of BK, no K tile straddles two filter taps.
   if (dtype == MTHIP_F16) {
-    if (a.Cp % Mfma<uint16_t>::BK == 0) return launch_gemm_fast<uint16_t, MODE_CONV, EPI_CONV, true>(device, a, 1, s);
+    if (a.Cp % Mfma<uint16_t>::BK == 0 && a.KH_ * a.KW <= 32)
+      return launch_gemm_fast<uint16_t, MODE_CONV, EPI_CONV, true>(device, a, 1, s);
     return launch_gemm_fast<uint16_t, MODE_CONV, EPI_CONV, false>(device, a, 1, s);
   }
-  if (a.Cp % Mfma<float>::BK == 0) return launch_gemm_fast<float, MODE_CONV, EPI_CONV, true>(device, a, 1, s);
+  if (a.Cp % Mfma<float>::BK == 0 && a.KH_ * a.KW <= 32)
+    return launch_gemm_fast<float, MODE_CONV, EPI_CONV, true>(device, a, 1, s);
   return launch_gemm_fast<float, MODE_CONV, EPI_CONV, false>(device, a, 1, s);
 }
 

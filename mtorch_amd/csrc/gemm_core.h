@@ -21,8 +21,11 @@
 //
 // K advances in BK-wide tiles through two LDS buffers fed by two register stages; one barrier
 // per step suffices.  Loads are range-checked buffer loads from precomputed per-thread
-// offsets; the implicit im2col of the conv mode derives the (ky, kx, channel) of a tile once
-// per tile (uniform across the workgroup) when the padded channel count is a multiple of BK.
+// offsets.  The implicit im2col of the conv mode, when the padded channel count is a multiple
+// of BK (a tile never straddles two filter taps) and the filter has <= 32 taps, keeps per
+// output pixel the offset of tap (0, 0) and a bitmask of the taps inside the image (both set
+// once per unit) and steps the tile's (tap, ky, kx, channel) with counters, so a chunk costs a
+// bit test and one add per tile.
 //
 // When the output tiles alone cannot fill the chip and K is long (the 1280-channel convs at
 // 8x8 and 16x16), K is split into slices whose fp32 partial tiles go to a workspace;
@@ -56,10 +59,13 @@ struct Mfma<uint16_t> {
   static constexpr int VEC = 8;  // elements per 16-byte global chunk
   static constexpr int PAD = 8;  // LDS row padding (elements) against bank conflicts
   static constexpr int BK = 64;
-  // acc += rowfrag(p) x colfrag(q): p supplies the MFMA's A (output rows i), q its B (cols j).
-  static __device__ __forceinline__ floatx16 fma(const uint16_t* p, const uint16_t* q, int kk, int lane, floatx16 acc) {
-    const halfx8 a = *reinterpret_cast<const halfx8*>(p + kk + (lane >> 5) * 8);
-    const halfx8 b = *reinterpret_cast<const halfx8*>(q + kk + (lane >> 5) * 8);
+  typedef halfx8 Frag;
+  // This lane's operand fragment of a 32-row LDS block at k offset kk.
+  static __device__ __forceinline__ Frag load(const uint16_t* p, int kk, int lane) {
+    return *reinterpret_cast<const halfx8*>(p + kk + (lane >> 5) * 8);
+  }
+  // acc += a x b, a supplying the MFMA's A (output rows), b its B (output cols).
+  static __device__ __forceinline__ floatx16 mma(const Frag& a, const Frag& b, floatx16 acc) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, acc, 0, 0, 0);
   }
 };
@@ -70,8 +76,10 @@ struct Mfma<float> {
   static constexpr int VEC = 4;
   static constexpr int PAD = 4;
   static constexpr int BK = 32;
-  static __device__ __forceinline__ floatx16 fma(const float* p, const float* q, int kk, int lane, floatx16 acc) {
-    return __builtin_amdgcn_mfma_f32_32x32x2f32(p[kk + (lane >> 5)], q[kk + (lane >> 5)], acc, 0, 0, 0);
+  typedef float Frag;
+  static __device__ __forceinline__ Frag load(const float* p, int kk, int lane) { return p[kk + (lane >> 5)]; }
+  static __device__ __forceinline__ floatx16 mma(const Frag& a, const Frag& b, floatx16 acc) {
+    return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, acc, 0, 0, 0);
   }
 };
 
@@ -94,6 +102,7 @@ struct GemmArgs {
   int64_t c_in_rs, c_in_cs, stride_c_in;
   // MODE_CONV: B[n = output pixel, k = (ky, kx, c)] gathered from x_nhwc[img, iy, ix, Cp]
   int64_t H, W, Cp, OH, OW, KW, sh, sw, ph, pw, dh, dw;
+  int64_t KH_;  // filter height (CONV_FAST tap masks)
   // Extent (bytes) of the A and B buffers as seen from one batch's base; buffer loads beyond
   // it return zeros.  Must stay below 2^31.
   int64_t a_bytes, b_bytes;
@@ -275,6 +284,12 @@ __global__ __launch_bounds__(256) void gemm_kernel(const GemmArgs args) {
   uint32_t a_off[A_CH];
   uint32_t b_off[MODE == MODE_NN ? 1 : B_CH];
   int conv_iy[MODE == MODE_CONV ? B_CH : 1], conv_ix[MODE == MODE_CONV ? B_CH : 1];
+  // CONV_FAST: per chunk the element offset of tap (0, 0) at this thread's channel (negative
+  // in the padding) and the bitmask of the filter taps that land inside the image; per tile the
+  // (tap, ky, kx, channel) of the loader cursor, stepped by counters instead of divided out.
+  int c_base[MODE == MODE_CONV ? B_CH : 1];
+  uint32_t c_mask[MODE == MODE_CONV ? B_CH : 1];
+  int l_tap = 0, l_ky = 0, l_kx = 0, l_ch = 0;
   uint32_t l_u = blockIdx.x;  // loader cursor: unit, K tile within the unit
   int64_t l_k = 0;
   GemmUnit lun{};
@@ -314,6 +329,27 @@ __global__ __launch_bounds__(256) void gemm_kernel(const GemmArgs args) {
         // element offset of x_nhwc[img, iy0, ix0, kc] (iy0/ix0 may lie in the padding; only
         // in-bounds taps are ever turned into a real offset)
         b_off[i] = (img * (uint32_t)args.H * (uint32_t)args.W) * (uint32_t)args.Cp + (uint32_t)kc;
+        if constexpr (CONV_FAST) {
+          const int H = (int)args.H, W = (int)args.W, KW = (int)args.KW, KH = (int)args.KH_;
+          const int iy0 = conv_iy[i], ix0 = conv_ix[i];
+          c_base[i] = ok ? (int)b_off[i] + (iy0 * W + ix0) * (int)args.Cp : 0;
+          uint32_t m = 0;
+          for (int ky = 0; ky < KH; ++ky) {
+            const int iy = iy0 + ky * (int)args.dh;
+            for (int kx = 0; kx < KW; ++kx) {
+              const int ix = ix0 + kx * (int)args.dw;
+              if (ok && iy >= 0 && iy < H && ix >= 0 && ix < W) m |= 1u << (ky * KW + kx);
+            }
+          }
+          c_mask[i] = m;
+        }
+      }
+      if constexpr (CONV_FAST) {
+        const int k0 = (int)(lun.kt0 * BK), Cp = (int)args.Cp, KW = (int)args.KW;
+        l_tap = k0 / Cp;
+        l_ch = k0 - l_tap * Cp;
+        l_ky = l_tap / KW;
+        l_kx = l_tap - l_ky * KW;
       }
     }
   };
@@ -333,42 +369,60 @@ __global__ __launch_bounds__(256) void gemm_kernel(const GemmArgs args) {
   auto load_next = [&](uint4(&ra)[A_CH], uint4(&rb)[NRB]) {
     const bool live = l_u < args.units;
     const int64_t k0 = (lun.kt0 + l_k) * BK;
-    const bool kin = live && k0 + kc < args.K;  // K % VEC == 0: a chunk is entirely in or out
     const uint32_t kb = (uint32_t)(k0 * ES);
+    if constexpr (MODE == MODE_CONV && CONV_FAST) {
+      // K = taps * Cp is a whole number of tiles: every chunk of a live tile is in range.  Rows
+      // past M carry a_off = kOOB, and kOOB + kb (< 2^32) is still beyond the buffer.
 #pragma unroll
-    for (int i = 0; i < A_CH; ++i) ra[i] = bload(a_rsrc, (kin && a_off[i] != kOOB) ? a_off[i] + kb : kOOB);
-    if constexpr (MODE == MODE_NT) {
-#pragma unroll
-      for (int i = 0; i < B_CH; ++i) rb[i] = bload(b_rsrc, (kin && b_off[i] != kOOB) ? b_off[i] + kb : kOOB);
-    } else if constexpr (MODE == MODE_NN) {
-#pragma unroll
-      for (int i = 0; i < B_CH_NN; ++i) {
-        const int c = tid + i * 256;
-        const int64_t k = k0 + c / NB_CH_ROW, n = l_n0 + (c % NB_CH_ROW) * VEC;
-        const bool ok = live && k < args.K && n < args.N;  // N % VEC == 0: chunks are whole
-        rb[i] = bload(b_rsrc, ok ? (uint32_t)((k * args.ldb + n) * ES) : kOOB);
-      }
-    } else {
-      // Implicit im2col: k = (ky*KW + kx)*Cp + ch.  With Cp % BK == 0 a tile never straddles
-      // two taps, so (ky, kx, ch0) are uniform across the workgroup for the whole tile.
-      const int W = (int)args.W, H = (int)args.H, Cp = (int)args.Cp, KW = (int)args.KW;
-      int tap, ch;
-      if constexpr (CONV_FAST) {
-        tap = (int)k0 / Cp;
-        ch = (int)k0 - tap * Cp;  // + kc, already folded into b_off
-      } else {
-        const int k = (int)k0 + kc;
-        tap = k / Cp;
-        ch = k - tap * Cp - kc;
-      }
-      const int ky = tap / KW, kx = tap - (tap / KW) * KW;
-      const int dy = ky * (int)args.dh, dx = kx * (int)args.dw;
+      for (int i = 0; i < A_CH; ++i) ra[i] = bload(a_rsrc, a_off[i] + kb);
+      const int tap_off = (l_ky * (int)args.dh * (int)args.W + l_kx * (int)args.dw) * (int)args.Cp + l_ch;
 #pragma unroll
       for (int i = 0; i < B_CH; ++i) {
-        const int iy = conv_iy[i] + dy, ix = conv_ix[i] + dx;
-        const bool ok = kin && iy >= 0 && iy < H && ix >= 0 && ix < W;
-        const uint32_t off = (b_off[i] + (uint32_t)((iy * W + ix) * Cp + ch)) * (uint32_t)ES;
-        rb[i] = bload(b_rsrc, ok ? off : kOOB);
+        const bool ok = live && ((c_mask[i] >> l_tap) & 1u);
+        rb[i] = bload(b_rsrc, ok ? (uint32_t)(c_base[i] + tap_off) * (uint32_t)ES : kOOB);
+      }
+      if (live) {
+        l_ch += BK;
+        if (l_ch == (int)args.Cp) {
+          l_ch = 0;
+          ++l_tap;
+          if (++l_kx == (int)args.KW) {
+            l_kx = 0;
+            ++l_ky;
+          }
+        }
+      }
+    } else {
+      const bool kin = live && k0 + kc < args.K;  // K % VEC == 0: a chunk is entirely in or out
+#pragma unroll
+      for (int i = 0; i < A_CH; ++i) ra[i] = bload(a_rsrc, kin ? a_off[i] + kb : kOOB);
+      if constexpr (MODE == MODE_NT) {
+#pragma unroll
+        for (int i = 0; i < B_CH; ++i) rb[i] = bload(b_rsrc, kin ? b_off[i] + kb : kOOB);
+      } else if constexpr (MODE == MODE_NN) {
+#pragma unroll
+        for (int i = 0; i < B_CH_NN; ++i) {
+          const int c = tid + i * 256;
+          const int64_t k = k0 + c / NB_CH_ROW, n = l_n0 + (c % NB_CH_ROW) * VEC;
+          const bool ok = live && k < args.K && n < args.N;  // N % VEC == 0: chunks are whole
+          rb[i] = bload(b_rsrc, ok ? (uint32_t)((k * args.ldb + n) * ES) : kOOB);
+        }
+      } else {
+        // Implicit im2col, generic: k = (ky*KW + kx)*Cp + ch decoded per chunk (a tile may
+        // straddle taps when Cp is not a multiple of BK).
+        const int W = (int)args.W, H = (int)args.H, Cp = (int)args.Cp, KW = (int)args.KW;
+        const int k = (int)k0 + kc;
+        const int tap = k / Cp;
+        const int ch = k - tap * Cp - kc;
+        const int ky = tap / KW, kx = tap - (tap / KW) * KW;
+        const int dy = ky * (int)args.dh, dx = kx * (int)args.dw;
+#pragma unroll
+        for (int i = 0; i < B_CH; ++i) {
+          const int iy = conv_iy[i] + dy, ix = conv_ix[i] + dx;
+          const bool ok = kin && iy >= 0 && iy < H && ix >= 0 && ix < W;
+          const uint32_t off = (b_off[i] + (uint32_t)((iy * W + ix) * Cp + ch)) * (uint32_t)ES;
+          rb[i] = bload(b_rsrc, ok ? off : kOOB);
+        }
       }
     }
     // advance (uniform across the workgroup)
@@ -415,17 +469,29 @@ __global__ __launch_bounds__(256) void gemm_kernel(const GemmArgs args) {
   };
   zero_acc();
 
+  // All of a K tile's fragments are read from LDS first and the MFMAs issued back to back
+  // after one wait: reading each step's fragments right before its MFMA (into the same
+  // registers) exposes the LDS latency once per MFMA instead of once per tile.
+  constexpr int KS = BK / Mfma<T>::KI;
   auto compute = [&](int buf) {
     const T* a_base = &As[buf][(wm * WM + (lane & 31)) * LDK];
     const T* b_base = &Bs[buf][(wn * WN + (lane & 31)) * LDK];
+    typename Mfma<T>::Frag af[KS][FM], bf[KS][FN];
 #pragma unroll
-    for (int kk = 0; kk < BK; kk += Mfma<T>::KI) {
+    for (int kk = 0; kk < KS; ++kk) {
+#pragma unroll
+      for (int i = 0; i < FM; ++i) af[kk][i] = Mfma<T>::load(a_base + i * 32 * LDK, kk * Mfma<T>::KI, lane);
+#pragma unroll
+      for (int j = 0; j < FN; ++j) bf[kk][j] = Mfma<T>::load(b_base + j * 32 * LDK, kk * Mfma<T>::KI, lane);
+    }
+    // keep the scheduler from sinking each read back next to its MFMA
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int kk = 0; kk < KS; ++kk)
 #pragma unroll
       for (int i = 0; i < FM; ++i)
 #pragma unroll
-        for (int j = 0; j < FN; ++j)
-          acc[i][j] = Mfma<T>::fma(b_base + j * 32 * LDK, a_base + i * 32 * LDK, kk, lane, acc[i][j]);
-    }
+        for (int j = 0; j < FN; ++j) acc[i][j] = Mfma<T>::mma(bf[kk][j], af[kk][i], acc[i][j]);
   };
 
   // ---- epilogue of the compute cursor's unit.  Fragment (i, j), register r of lane l holds
