@@ -5,6 +5,7 @@
 #include <cstdlib>
 
 #include "gemm_core.h"
+#include "gemm_dtl.h"
 
 namespace mthip {
 namespace {
@@ -52,13 +53,25 @@ int cu_count(int device) {
   return cached[device];
 }
 
+// The kernel instance behind a tile choice: DS > 0 selects the direct-to-LDS fp16 kernel
+// with DS stages, DS == 0 the register-staged kernel.
+template <typename T, int BM, int BN, int MODE, int EPI, int ACT, bool FAST, int WGM, int DS>
+constexpr auto gemm_kernel_ptr() {
+  if constexpr (DS > 0) {
+    static_assert(sizeof(T) == 2 && (MODE == MODE_NT || (MODE == MODE_CONV && FAST)), "direct-to-LDS: fp16, k-contiguous");
+    return &gemm_dtl_kernel<BM, BN, WGM, MODE, EPI, ACT, DS>;
+  } else {
+    return &gemm_kernel<T, BM, BN, WGM, MODE, EPI, ACT, FAST>;
+  }
+}
+
 // Resident workgroups per CU of one kernel instance (registers and LDS decide it).
-template <typename T, int BM, int BN, int MODE, int EPI, int ACT, bool FAST, int WGM = 2>
+template <typename T, int BM, int BN, int MODE, int EPI, int ACT, bool FAST, int WGM, int DS>
 int resident_per_cu() {
   static const int v = [] {
     int n = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, gemm_kernel<T, BM, BN, WGM, MODE, EPI, ACT, FAST>, 256, 0) !=
-            hipSuccess ||
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, gemm_kernel_ptr<T, BM, BN, MODE, EPI, ACT, FAST, WGM, DS>(),
+                                                     256, 0) != hipSuccess ||
         n < 1)
       n = 1;
     return n;
@@ -68,14 +81,14 @@ int resident_per_cu() {
 
 // Sizes the persistent grid, splits K when the output tiles cannot fill the chip, launches the
 // GEMM (and the slice reduction).
-template <typename T, int BM, int BN, int MODE, int EPI, int ACT, bool FAST, int WGM = 2>
+template <typename T, int BM, int BN, int MODE, int EPI, int ACT, bool FAST, int WGM = 2, int DS = 0>
 int launch_tile(int device, GemmArgs a, int64_t batch, hipStream_t s) {
   constexpr int BK = Mfma<T>::BK;
   a.tiles_m = ceil_div(a.M, BM);
   a.tiles_n = ceil_div(a.N, BN);
   const int64_t nk = std::max<int64_t>(ceil_div(a.K, BK), 1);
   const int64_t tiles = a.tiles_m * a.tiles_n * batch;
-  const int64_t slots = (int64_t)cu_count(device) * resident_per_cu<T, BM, BN, MODE, EPI, ACT, FAST, WGM>();
+  const int64_t slots = (int64_t)cu_count(device) * resident_per_cu<T, BM, BN, MODE, EPI, ACT, FAST, WGM, DS>();
   int64_t ksplit = 1;
   // Split K only for single-batch problems with fewer tiles than about `split_target` units
   // per CU and >= 32 K tiles, into enough slices to reach that, each slice keeping >= 16 K
@@ -110,7 +123,7 @@ int launch_tile(int device, GemmArgs a, int64_t batch, hipStream_t s) {
     if (int rc = mthip_malloc(device, (size_t)(a.ksplit * a.M * a.ld_partial) * sizeof(float), &ws)) return rc;
     a.partial = static_cast<float*>(ws);
   }
-  hipLaunchKernelGGL((gemm_kernel<T, BM, BN, WGM, MODE, EPI, ACT, FAST>), dim3((unsigned)g), dim3(256), 0, s, a);
+  hipLaunchKernelGGL((gemm_kernel_ptr<T, BM, BN, MODE, EPI, ACT, FAST, WGM, DS>()), dim3((unsigned)g), dim3(256), 0, s, a);
   int rc = check_launch("gemm_kernel");
   if constexpr (EPI == EPI_GEGLU) return rc;
   if (rc == MTHIP_OK && a.ksplit > 1) {
@@ -123,8 +136,45 @@ int launch_tile(int device, GemmArgs a, int64_t batch, hipStream_t s) {
   return rc;
 }
 
+// Direct-to-LDS tile shapes (fp16, k-contiguous operands): MTHIP_GEMM_DTL=0 turns the kernel
+// off, MTHIP_GEMM_DTL_TILE=0..5 forces one of
+//   0: 64x64 (2x2 waves of 32x32), 3 stages     1: 64x64, 4 stages
+//   2: 128x64 (2x2 waves of 64x32), 3 stages    3: 64x128 (2x2 waves of 32x64), 3 stages
+//   4: 128x128 (2x2 waves of 64x64), 3 stages   5: 128x128, 2 stages
+bool dtl_enabled() { return env_flag("MTHIP_GEMM_DTL", 1) != 0; }
+int dtl_tile() { return env_flag("MTHIP_GEMM_DTL_TILE", 0); }
+
+template <int MODE, int EPI, int ACT>
+int launch_dtl(int device, const GemmArgs& a, int64_t batch, hipStream_t s) {
+  using T = uint16_t;
+  constexpr bool F = MODE == MODE_CONV;
+  if constexpr (EPI == EPI_GEGLU) {
+    return launch_tile<T, 128, 64, MODE, EPI, ACT, F, 4, 3>(device, a, batch, s);
+  } else if constexpr (ACT != MTHIP_ACT_NONE) {
+    return launch_tile<T, 64, 64, MODE, EPI, ACT, F, 2, 3>(device, a, batch, s);
+  } else {
+    switch (dtl_tile()) {
+      case 1:
+        return launch_tile<T, 64, 64, MODE, EPI, ACT, F, 2, 4>(device, a, batch, s);
+      case 2:
+        return launch_tile<T, 128, 64, MODE, EPI, ACT, F, 2, 3>(device, a, batch, s);
+      case 3:
+        return launch_tile<T, 64, 128, MODE, EPI, ACT, F, 2, 3>(device, a, batch, s);
+      case 4:
+        return launch_tile<T, 128, 128, MODE, EPI, ACT, F, 2, 3>(device, a, batch, s);
+      case 5:
+        return launch_tile<T, 128, 128, MODE, EPI, ACT, F, 2, 2>(device, a, batch, s);
+      default:
+        return launch_tile<T, 64, 64, MODE, EPI, ACT, F, 2, 3>(device, a, batch, s);
+    }
+  }
+}
+
 template <typename T, int MODE, int EPI, int ACT, bool FAST>
 int launch_gemm_tiles(int device, const GemmArgs& a, int64_t batch, hipStream_t s) {
+  if constexpr (sizeof(T) == 2 && (MODE == MODE_NT || (MODE == MODE_CONV && FAST))) {
+    if (dtl_enabled()) return launch_dtl<MODE, EPI, ACT>(device, a, batch, s);
+  }
   switch (pick_tile(MODE, a.M, a.N, batch)) {
     case T128x128:
       return launch_tile<T, 128, 128, MODE, EPI, ACT, FAST>(device, a, batch, s);
@@ -331,6 +381,7 @@ int mthip_linear_geglu(int device, int dtype, const void* x, int64_t lda, const 
   if (dtype == MTHIP_F16) {
     a.gelu_tab = gelu_f16_table(device, s);
     if (!a.gelu_tab) return fail(MTHIP_ERR_HIP, "mthip_linear_geglu: gelu table setup failed");
+    if (dtl_enabled()) return launch_dtl<MODE_NT, EPI_GEGLU, MTHIP_ACT_NONE>(device, a, 1, s);
     return launch_tile<uint16_t, 128, 64, MODE_NT, EPI_GEGLU, MTHIP_ACT_NONE, false, 4>(device, a, 1, s);
   }
   return launch_tile<float, 128, 64, MODE_NT, EPI_GEGLU, MTHIP_ACT_NONE, false, 4>(device, a, 1, s);

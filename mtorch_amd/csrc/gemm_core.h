@@ -247,6 +247,84 @@ __device__ __forceinline__ GemmUnit decode_unit(const GemmArgs& args, uint32_t u
   return un;
 }
 
+// Epilogue of one unit.  Fragment (i, j), register r of lane l holds
+//   C[row][col], row = m0 + wm*WM + i*32 + l%32,
+//   col = n0 + wn*WN + j*32 + 8*(r/4) + 4*(l/32) + r%4     (4 consecutive cols per r/4),
+// with (wm, wn) the wave's position in the workgroup's WGM x (4/WGM) grid of wave tiles.
+template <typename T, int BM, int BN, int WGM, int EPI, int ACT, int FM, int FN>
+__device__ __forceinline__ void gemm_finish_unit(const GemmArgs& args, const GemmUnit& un, floatx16 (&acc)[FM][FN],
+                                                 int lane, int wm, int wn) {
+  constexpr int WGN = 4 / WGM;
+  constexpr int WM = BM / WGM, WN = BN / WGN;
+  static_assert(FM == WM / 32 && FN == WN / 32, "fragment grid");
+  const int lane_col = 4 * (lane >> 5);
+  const int M = (int)args.M;
+  if constexpr (EPI == EPI_GEGLU) {
+    // B rows come interleaved in 32-row blocks (values, then the matching gates), and each
+    // wave owns 64 columns = fragment 0 (values) + fragment 1 (gates) of 32 output columns:
+    // out[row][col] = value * gelu(gate), each factor narrowed as the unfused
+    // linear -> chunk -> gelu -> mul sequence narrows it.
+    static_assert(FN == 2 && WGN == 1 && BN == 64, "GEGLU epilogue pairs two 32-column fragments");
+    const T* bias = reinterpret_cast<const T*>(args.bias);
+    T* Cp = reinterpret_cast<T*>(args.c);
+    const int Nout = (int)args.N / 2;
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+      const int row = (int)un.m0 + wm * WM + i * 32 + (lane & 31);
+      if (row < M) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int pc = (int)un.n0 + 8 * g + lane_col;  // permuted column of the value
+          const int col0 = (int)un.n0 / 2 + 8 * g + lane_col;
+          if (col0 < Nout) {
+            float v[4];
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+              float val = acc[i][0][4 * g + t], gate = acc[i][1][4 * g + t];
+              if (bias) {
+                val += Elem<T>::load(bias, pc + t);
+                gate += Elem<T>::load(bias, pc + 32 + t);
+              }
+              if constexpr (sizeof(T) == 2) {
+                const float gl = h2f_bits(args.gelu_tab[f2h_fast(gate)]);
+                v[t] = h2f_bits(f2h_fast(val)) * gl;
+              } else {
+                v[t] = val * gelu_ref_f32(gate);
+              }
+            }
+            store_cols<T>(Cp + (int64_t)row * args.ldc + col0, v, Nout - col0 < 4 ? Nout - col0 : 4);
+          }
+        }
+      }
+    }
+    return;
+  }
+#pragma unroll
+  for (int i = 0; i < FM; ++i) {
+    const int row = (int)un.m0 + wm * WM + i * 32 + (lane & 31);
+    const bool row_ok = row < M;
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int col0 = (int)un.n0 + wn * WN + j * 32 + 8 * g + lane_col;
+        float v[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) v[t] = acc[i][j][4 * g + t];
+        if (row_ok) {
+          if (args.ksplit > 1) {
+            if (col0 < (int)args.N)
+              *reinterpret_cast<float4*>(args.partial + (un.split * args.M + row) * args.ld_partial + col0) =
+                  make_float4(v[0], v[1], v[2], v[3]);
+          } else {
+            emit4<T, EPI, ACT>(args, un.bz, row, col0, v);
+          }
+        }
+      }
+    }
+  }
+}
+
 template <typename T, int BM, int BN, int WGM, int MODE, int EPI, int ACT, bool CONV_FAST>
 __global__ __launch_bounds__(256) void gemm_kernel(const GemmArgs args) {
   constexpr int BK = Mfma<T>::BK;
@@ -494,76 +572,8 @@ __global__ __launch_bounds__(256) void gemm_kernel(const GemmArgs args) {
         for (int j = 0; j < FN; ++j) acc[i][j] = Mfma<T>::mma(bf[kk][j], af[kk][i], acc[i][j]);
   };
 
-  // ---- epilogue of the compute cursor's unit.  Fragment (i, j), register r of lane l holds
-  //      C[row][col] with row = m0 + wm*WM + i*32 + l%32,
-  //      col = n0 + wn*WN + j*32 + 8*(r/4) + 4*(l/32) + r%4     (4 consecutive cols per r/4).
-  const int lane_col = 4 * (lane >> 5);
   auto finish_unit = [&](const GemmUnit& un) {
-    const int M = (int)args.M;
-    if constexpr (EPI == EPI_GEGLU) {
-      // B rows come interleaved in 32-row blocks (values, then the matching gates), and each
-      // wave owns 64 columns = fragment 0 (values) + fragment 1 (gates) of 32 output columns:
-      // out[row][col] = value * gelu(gate), each factor narrowed as the unfused
-      // linear -> chunk -> gelu -> mul sequence narrows it.
-      static_assert(FN == 2 && WGN == 1 && BN == 64, "GEGLU epilogue pairs two 32-column fragments");
-      const T* bias = reinterpret_cast<const T*>(args.bias);
-      T* Cp = reinterpret_cast<T*>(args.c);
-      const int Nout = (int)args.N / 2;
-#pragma unroll
-      for (int i = 0; i < FM; ++i) {
-        const int row = (int)un.m0 + wm * WM + i * 32 + (lane & 31);
-        if (row < M) {
-#pragma unroll
-          for (int g = 0; g < 4; ++g) {
-            const int pc = (int)un.n0 + 8 * g + lane_col;  // permuted column of the value
-            const int col0 = (int)un.n0 / 2 + 8 * g + lane_col;
-            if (col0 < Nout) {
-              float v[4];
-#pragma unroll
-              for (int t = 0; t < 4; ++t) {
-                float val = acc[i][0][4 * g + t], gate = acc[i][1][4 * g + t];
-                if (bias) {
-                  val += Elem<T>::load(bias, pc + t);
-                  gate += Elem<T>::load(bias, pc + 32 + t);
-                }
-                if constexpr (sizeof(T) == 2) {
-                  const float gl = h2f_bits(args.gelu_tab[f2h_fast(gate)]);
-                  v[t] = h2f_bits(f2h_fast(val)) * gl;
-                } else {
-                  v[t] = val * gelu_ref_f32(gate);
-                }
-              }
-              store_cols<T>(Cp + (int64_t)row * args.ldc + col0, v, Nout - col0 < 4 ? Nout - col0 : 4);
-            }
-          }
-        }
-      }
-      return;
-    }
-#pragma unroll
-    for (int i = 0; i < FM; ++i) {
-      const int row = (int)un.m0 + wm * WM + i * 32 + (lane & 31);
-      const bool row_ok = row < M;
-#pragma unroll
-      for (int j = 0; j < FN; ++j) {
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const int col0 = (int)un.n0 + wn * WN + j * 32 + 8 * g + lane_col;
-          float v[4];
-#pragma unroll
-          for (int t = 0; t < 4; ++t) v[t] = acc[i][j][4 * g + t];
-          if (row_ok) {
-            if (args.ksplit > 1) {
-              if (col0 < (int)args.N)
-                *reinterpret_cast<float4*>(args.partial + (un.split * args.M + row) * args.ld_partial + col0) =
-                    make_float4(v[0], v[1], v[2], v[3]);
-            } else {
-              emit4<T, EPI, ACT>(args, un.bz, row, col0, v);
-            }
-          }
-        }
-      }
-    }
+    gemm_finish_unit<T, BM, BN, WGM, EPI, ACT>(args, un, acc, lane, wm, wn);
   };
 
   // compute cursor

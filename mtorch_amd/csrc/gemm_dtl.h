@@ -1,0 +1,297 @@
+// fp16 MFMA GEMM with direct-to-LDS operand loads (gfx950), for the k-contiguous operand
+// sources: x.W^T (MODE_NT) and the implicit im2col of an NHWC activation whose padded channel
+// count is a multiple of the K tile (MODE_CONV, at most 32 filter taps).  Same work
+// decomposition, unit order, split-K and epilogues as gemm_kernel in gemm_core.h; what differs
+// is how K tiles reach LDS.
+//
+// Operands go global -> LDS with buffer_load_dwordx4 ... lds: each instruction moves 64 x 16 B,
+// lane l's 16 bytes landing at LDS base + 16*l, so a wave instruction fills 8 consecutive
+// 128-byte tile rows (one K tile = 64 halves per row).  No registers stage the data and no
+// ds_write is issued; the K position is the instruction's scalar offset, so stepping K costs no
+// vector instructions for A and for linear B.  LDS rows are unpadded with the 16-byte chunk c
+// of row r stored at chunk c ^ ((r >> 1) & 7): LDS serves 256 bytes per clock (64 banks), and
+// the 16 lanes of one ds_read_b128 pass -- rows r..r+15 of one fragment column -- then cover
+// all 64 banks.  The swizzle is applied on the global side: lane l of an instruction fetches
+// the logical chunk that belongs at its fixed LDS slot.
+//
+// K tiles rotate through S stages (S-1 tiles in flight while one is multiplied); each stage is a
+// separate LDS array selected by a compile-time stage number, so every LDS address is a
+// register plus an immediate.  Per step: wait until this wave's loads of the step have landed
+// (an explicit vmcnt wait: see dma16 for why the compiler's own is kept out), barrier
+// (everyone's have, and everyone has finished reading the stage about to be refilled), issue
+// the loads S-1 steps ahead, multiply.
+#pragma once
+
+#include <type_traits>
+
+#include "gemm_core.h"
+
+namespace mthip {
+
+template <int N>
+using ic = std::integral_constant<int, N>;
+
+// s_waitcnt immediate that waits for vmcnt <= n only (expcnt and lgkmcnt left at their maxima).
+constexpr int vmcnt_only(int n) { return (n & 0xF) | (0x7 << 4) | (0xF << 8) | ((n >> 4) << 14); }
+
+// LDS byte address of a __shared__ array.
+__device__ __forceinline__ uint32_t lds_addr(uint8_t* p) {
+  return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)p;
+}
+
+// One 64 x 16-byte direct-to-LDS load: lane l's 16 bytes from buffer offset voff + soff land at
+// LDS byte address lds + 16*l.  The LDS address reaches the instruction through readfirstlane,
+// which the compiler cannot see through: the load then carries no alias scope, and the
+// compiler's wait insertion does not tie later LDS reads to it (it cannot tell the stage arrays
+// apart across the unrolled loop and would wait for loads of the next stage too).  Ordering is
+// the kernel's own: every stage is read only after an explicit vmcnt wait and a barrier.
+__device__ __forceinline__ void dma16(const __amdgpu_buffer_rsrc_t& r, uint32_t lds, uint32_t voff, uint32_t soff) {
+  const uint32_t a = __builtin_amdgcn_readfirstlane(lds);
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)(uintptr_t)a, 16, voff, soff, 0,
+                                           0);
+}
+
+template <int BM, int BN, int WGM, int MODE, int EPI, int ACT, int S>
+__global__ __launch_bounds__(256) void gemm_dtl_kernel(const GemmArgs args) {
+  using T = uint16_t;
+  constexpr int BK = 64;  // halves per K tile: 128-byte LDS rows
+  constexpr int WGN = 4 / WGM;
+  constexpr int WM = BM / WGM, WN = BN / WGN;
+  constexpr int FM = WM / 32, FN = WN / 32;
+  constexpr int AI = BM / 32, BI = BN / 32;  // 8-row DMA instructions per wave per K tile
+  constexpr int L = AI + BI;                 // loads per wave per K tile
+  static_assert(MODE == MODE_NT || MODE == MODE_CONV, "k-contiguous operands only");
+  static_assert(S >= 2 && S <= 4, "2..4 stages");
+  static_assert(FM >= 1 && FN >= 1 && WM % 32 == 0 && WN % 32 == 0, "wave tile must be a multiple of 32");
+  static_assert((S - 2) * L <= 63, "vmcnt range");
+
+  __shared__ __align__(16) uint8_t sa0[BM * 128], sa1[BM * 128], sa2[S > 2 ? BM * 128 : 16], sa3[S > 3 ? BM * 128 : 16];
+  __shared__ __align__(16) uint8_t sb0[BN * 128], sb1[BN * 128], sb2[S > 2 ? BN * 128 : 16], sb3[S > 3 ? BN * 128 : 16];
+  auto SA = [&](auto st) -> uint8_t* {
+    constexpr int s = decltype(st)::value;
+    if constexpr (s == 0) return sa0;
+    else if constexpr (s == 1) return sa1;
+    else if constexpr (s == 2) return sa2;
+    else return sa3;
+  };
+  auto SB = [&](auto st) -> uint8_t* {
+    constexpr int s = decltype(st)::value;
+    if constexpr (s == 0) return sb0;
+    else if constexpr (s == 1) return sb1;
+    else if constexpr (s == 2) return sb2;
+    else return sb3;
+  };
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: LDS targets are scalar
+  const int wm = wave % WGM, wn = wave / WGM;
+  const uint32_t G = gridDim.x;
+  const uint32_t nk_total = (uint32_t)ceil_div(args.K, BK);
+  constexpr uint32_t kOOB = 0x80000000u;  // beyond every buffer: the range check returns zeros
+
+  // Tile row and logical chunk of this lane in DMA instruction i of an operand issuing I
+  // instructions per wave: rows (wave*I + i)*8 .. +8, lane l at row +l/8, LDS chunk l%8.
+  auto dma_row = [&](int I, int i) { return (wave * I + i) * 8 + (lane >> 3); };
+  auto dma_chunk = [&](int row) { return (lane & 7) ^ ((row >> 1) & 7); };
+
+  // ---- loader state (the unit whose tiles are being fetched) -------------------------------
+  __amdgpu_buffer_rsrc_t a_rsrc, b_rsrc;
+  uint32_t a_off[AI], b_off[BI];
+  int a_kc[AI], b_kc[BI];  // element k offset of the lane's chunk (K tails)
+  int c_base[MODE == MODE_CONV ? BI : 1];
+  uint32_t c_mask[MODE == MODE_CONV ? BI : 1];
+  int l_tap = 0, l_ky = 0, l_kx = 0, l_ch = 0;
+  uint32_t l_u = blockIdx.x;
+  int64_t l_k = 0;
+  GemmUnit lun{};
+
+  auto set_loader = [&]() {
+    lun = decode_unit<BM, BN>(args, l_u, nk_total);
+    a_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(reinterpret_cast<const T*>(args.a) + lun.bz * args.stride_a), (short)0, (int)args.a_bytes, 0x00020000);
+    b_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(reinterpret_cast<const T*>(args.b) + (MODE == MODE_CONV ? 0 : lun.bz * args.stride_b)), (short)0,
+        (int)args.b_bytes, 0x00020000);
+#pragma unroll
+    for (int i = 0; i < AI; ++i) {
+      const int r = dma_row(AI, i), c = dma_chunk(r);
+      const int64_t row = lun.m0 + r;
+      a_kc[i] = c * 8;
+      a_off[i] = row < args.M ? ((uint32_t)row * (uint32_t)args.lda + (uint32_t)(c * 8)) * 2u : kOOB;
+    }
+    if constexpr (MODE == MODE_NT) {
+#pragma unroll
+      for (int i = 0; i < BI; ++i) {
+        const int r = dma_row(BI, i), c = dma_chunk(r);
+        const int64_t row = lun.n0 + r;
+        b_kc[i] = c * 8;
+        b_off[i] = row < args.N ? ((uint32_t)row * (uint32_t)args.ldb + (uint32_t)(c * 8)) * 2u : kOOB;
+      }
+    } else {
+      const int H = (int)args.H, W = (int)args.W, KW = (int)args.KW, KH = (int)args.KH_, Cp = (int)args.Cp;
+      const int dh = (int)args.dh, dw = (int)args.dw;
+#pragma unroll
+      for (int i = 0; i < BI; ++i) {
+        const int r = dma_row(BI, i), c = dma_chunk(r);
+        b_kc[i] = c * 8;
+        const int64_t p = lun.n0 + r;
+        const bool ok = p < args.N;
+        const uint32_t pp = ok ? (uint32_t)p : 0u;
+        const uint32_t img = args.div_ohw.div(pp), pix = pp - img * args.div_ohw.d;
+        const uint32_t oyu = args.div_ow.div(pix);
+        const int iy0 = (int)oyu * (int)args.sh - (int)args.ph;
+        const int ix0 = (int)(pix - oyu * args.div_ow.d) * (int)args.sw - (int)args.pw;
+        // element offset of x_nhwc[img, iy0, ix0, 8c] (negative in the padding; only taps that
+        // land inside the image are turned into an address)
+        c_base[i] = ok ? (((int)img * H + iy0) * W + ix0) * Cp + c * 8 : 0;
+        uint32_t cols = 0;
+        for (int kx = 0; kx < KW; ++kx) {
+          const int ix = ix0 + kx * dw;
+          cols |= (ix >= 0 && ix < W ? 1u : 0u) << kx;
+        }
+        uint32_t m = 0;
+        for (int ky = 0; ky < KH; ++ky) {
+          const int iy = iy0 + ky * dh;
+          m |= (iy >= 0 && iy < H ? cols : 0u) << (ky * KW);
+        }
+        c_mask[i] = ok ? m : 0u;
+      }
+      const int k0 = (int)(lun.kt0 * BK);
+      l_tap = k0 / Cp;
+      l_ch = k0 - l_tap * Cp;
+      l_ky = l_tap / KW;
+      l_kx = l_tap - l_ky * KW;
+    }
+  };
+  if (l_u < args.units) set_loader();
+
+  // Issues the loader cursor's K tile into stage st and advances the cursor.  Past the last unit
+  // every offset is kOOB: the stage receives zeros that are never read, and every step keeps
+  // issuing exactly L loads per wave, which the vmcnt accounting relies on.
+  auto issue = [&](auto st) {
+    const uint32_t sa = lds_addr(SA(st)), sb = lds_addr(SB(st));
+    const bool live = l_u < args.units;
+    const int64_t k0 = (lun.kt0 + l_k) * BK;
+    const uint32_t kb = live ? (uint32_t)(k0 * 2) : 0u;
+    if constexpr (MODE == MODE_NT) {
+      // a chunk past K would read the next row's data: only the last tile of an unaligned K
+      // needs the per-lane test
+      const bool whole = live && k0 + BK <= args.K;
+      const int kleft = (int)(args.K - k0);
+#pragma unroll
+      for (int i = 0; i < AI; ++i)
+        dma16(a_rsrc, sa + (wave * AI + i) * 1024, whole || (live && a_kc[i] < kleft) ? a_off[i] : kOOB, kb);
+#pragma unroll
+      for (int i = 0; i < BI; ++i)
+        dma16(b_rsrc, sb + (wave * BI + i) * 1024, whole || (live && b_kc[i] < kleft) ? b_off[i] : kOOB, kb);
+    } else {
+      // K = taps * Cp is a whole number of tiles and a tile never straddles two taps.
+#pragma unroll
+      for (int i = 0; i < AI; ++i) dma16(a_rsrc, sa + (wave * AI + i) * 1024, live ? a_off[i] : kOOB, kb);
+      const int tap_el = (l_ky * (int)args.dh * (int)args.W + l_kx * (int)args.dw) * (int)args.Cp;
+      const uint32_t chb = (uint32_t)l_ch * 2u;
+#pragma unroll
+      for (int i = 0; i < BI; ++i) {
+        const bool in = live && ((c_mask[i] >> l_tap) & 1u);
+        dma16(b_rsrc, sb + (wave * BI + i) * 1024, in ? (uint32_t)(c_base[i] + tap_el) * 2u : kOOB, chb);
+      }
+      if (live) {
+        l_ch += BK;
+        if (l_ch == (int)args.Cp) {
+          l_ch = 0;
+          ++l_tap;
+          if (++l_kx == (int)args.KW) {
+            l_kx = 0;
+            ++l_ky;
+          }
+        }
+      }
+    }
+    if (live && ++l_k == lun.nkt) {
+      l_k = 0;
+      l_u += G;
+      if (l_u < args.units) set_loader();
+    }
+  };
+
+  floatx16 acc[FM][FN];
+  auto zero_acc = [&]() {
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+  };
+  zero_acc();
+
+  // Fragment reads: lane l reads row (l%32) of each 32-row block at logical chunk 2*kk + l/32.
+  // The blocks start at multiples of 32 rows, so the swizzle term is ((l%32) >> 1) & 7 for all.
+  int a_rd[4], b_rd[4];
+  {
+    const int sw = ((lane & 31) >> 1) & 7, hi = lane >> 5;
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      a_rd[kk] = (wm * WM + (lane & 31)) * 128 + (((2 * kk + hi) ^ sw) << 4);
+      b_rd[kk] = (wn * WN + (lane & 31)) * 128 + (((2 * kk + hi) ^ sw) << 4);
+    }
+  }
+  auto compute = [&](auto st) {
+    const uint8_t* sa = SA(st);
+    const uint8_t* sb = SB(st);
+    halfx8 af[4][FM], bf[4][FN];
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+#pragma unroll
+      for (int i = 0; i < FM; ++i) af[kk][i] = *reinterpret_cast<const halfx8*>(sa + a_rd[kk] + i * 32 * 128);
+#pragma unroll
+      for (int j = 0; j < FN; ++j) bf[kk][j] = *reinterpret_cast<const halfx8*>(sb + b_rd[kk] + j * 32 * 128);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(bf[kk][j], af[kk][i], acc[i][j], 0, 0, 0);
+  };
+
+  uint32_t c_u = blockIdx.x;
+  int64_t c_k = 0;
+  if (c_u >= args.units) return;  // (the launcher sizes the grid to at most `units`)
+  GemmUnit cun = decode_unit<BM, BN>(args, c_u, nk_total);
+
+  auto step = [&](auto st) -> bool {
+    constexpr int s = decltype(st)::value;
+    __builtin_amdgcn_s_waitcnt(vmcnt_only((S - 2) * L));
+    __builtin_amdgcn_s_barrier();
+    issue(ic<(s + S - 1) % S>{});
+    compute(st);
+    if (++c_k == cun.nkt) {
+      gemm_finish_unit<T, BM, BN, WGM, EPI, ACT>(args, cun, acc, lane, wm, wn);
+      zero_acc();
+      c_k = 0;
+      c_u += G;
+      if (c_u >= args.units) return false;
+      cun = decode_unit<BM, BN>(args, c_u, nk_total);
+    }
+    return true;
+  };
+
+  issue(ic<0>{});
+  if constexpr (S > 2) issue(ic<1>{});
+  if constexpr (S > 3) issue(ic<2>{});
+  while (true) {
+    if (!step(ic<0>{})) break;
+    if (!step(ic<1>{})) break;
+    if constexpr (S > 2)
+      if (!step(ic<2>{})) break;
+    if constexpr (S > 3)
+      if (!step(ic<3>{})) break;
+  }
+  // DMA writes still in flight target this workgroup's LDS: let them land before it is released.
+  __builtin_amdgcn_s_waitcnt(0);
+}
+
+}  // namespace mthip
