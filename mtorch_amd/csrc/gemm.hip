@@ -90,14 +90,34 @@ int launch_tile(int device, GemmArgs a, int64_t batch, hipStream_t s) {
   const int64_t tiles = a.tiles_m * a.tiles_n * batch;
   const int64_t slots = (int64_t)cu_count(device) * resident_per_cu<T, BM, BN, MODE, EPI, ACT, FAST, WGM, DS>();
   int64_t ksplit = 1;
-  // Split K only for single-batch problems with fewer tiles than about `split_target` units
-  // per CU and >= 32 K tiles, into enough slices to reach that, each slice keeping >= 16 K
-  // tiles: every slice costs an fp32 M x N write and read in the reduction, which only long K
-  // amortises (the 3x3 convs gain 5-15% at 320 channels and 1.5-4x at 640-1280; linears with
-  // K <= 1280 are left alone).
-  const int64_t target = (int64_t)cu_count(device) * split_target();
-  if (batch == 1 && tiles < target && nk >= 32 && splitk_enabled() && EPI != EPI_GEGLU)
-    ksplit = std::max<int64_t>(1, std::min<int64_t>(std::min<int64_t>(ceil_div(target, tiles), nk / 16), 16));
+  if (batch == 1 && nk >= 16 && splitk_enabled() && EPI != EPI_GEGLU) {
+    if (DS > 0) {
+      // Pick the slice count with the shortest modelled makespan: the persistent grid runs
+      // ceil(units / slots) rounds of ceil(nk / ksplit) K tiles, and every extra slice adds an
+      // fp32 M x N write here plus its read in the reduction kernel.  (640 tiles on 768 slots
+      // gain nothing from 2 slices -- 2 rounds of half the K -- and would pay the reduction.)
+      constexpr double kStepUs = 0.6, kReduceFixedUs = 3.0, kReduceBytesPerUs = 3.0e6;
+      double best = 0.0;
+      const int64_t max_split = std::min<int64_t>(16, nk / 8);
+      for (int64_t ks = 1; ks <= max_split; ++ks) {
+        const int64_t rounds = ceil_div(tiles * ks, slots);
+        double t = (double)(rounds * ceil_div(nk, ks)) * kStepUs;
+        if (ks > 1) t += kReduceFixedUs + (double)((ks + 1) * a.M * a.N * 4) / kReduceBytesPerUs;
+        if (ks == 1 || t < best) {
+          best = t;
+          ksplit = ks;
+        }
+      }
+      if (const char* force = std::getenv("MTHIP_GEMM_KSPLIT")) ksplit = std::max(1, std::min(16, std::atoi(force)));
+    } else {
+      // Register-staged kernel: split single-batch problems with fewer tiles than about
+      // `split_target` units per CU and >= 32 K tiles into enough slices to reach that, each
+      // slice keeping >= 16 K tiles.
+      const int64_t target = (int64_t)cu_count(device) * split_target();
+      if (tiles < target && nk >= 32)
+        ksplit = std::max<int64_t>(1, std::min<int64_t>(std::min<int64_t>(ceil_div(target, tiles), nk / 16), 16));
+    }
+  }
   a.kt_per_split = ceil_div(nk, ksplit);
   a.ksplit = ceil_div(nk, a.kt_per_split);  // no empty slice
   a.units = tiles * a.ksplit;

@@ -1,8 +1,8 @@
 // group_norm (+ fused SiLU), layer_norm and last-dim softmax: HBM-streaming kernels with
 // wave64 shuffle reductions.
 //
-// group_norm splits every (sample, group) range into chunks of >= 8192 elements (an SD group is
-// up to 40,960 elements but there are only B*32 groups): a stats pass writes per-chunk (sum,
+// group_norm splits every (sample, group) range into chunks of >= 2048 elements (an SD group is
+// up to 122,880 elements but there are only B*32 groups): a stats pass writes per-chunk (sum,
 // sum of squares), and an apply pass folds the partials of its group(s) with one wave and
 // normalises its own chunk -- NCHW, or channels-last through an LDS transpose for the conv that
 // follows.  Two launches per group_norm; the apply pass's re-read of the input is served mostly
@@ -294,6 +294,117 @@ __global__ __launch_bounds__(256) void group_norm_apply_nhwc_kernel(const T* __r
   }
 }
 
+// fp16 SiLU of every half value, as the fused path computes it (SiLU of the narrowed
+// normalised value, narrowed again): the apply kernel looks the activation up by the fp16 bits
+// instead of evaluating expf and an IEEE divide per element.  Filled once per device.
+__device__ uint16_t g_silu_f16_table[65536];
+
+__global__ void silu_f16_table_kernel(uint16_t* tab) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < 65536) tab[i] = f2h_fast(apply_unary<uint16_t>(MTHIP_UNARY_SILU, h2f_bits((uint16_t)i)));
+}
+
+const uint16_t* silu_f16_table(int device, hipStream_t s) {
+  static const uint16_t* ptr[64] = {nullptr};
+  if (device < 0 || device >= 64) return nullptr;
+  if (!ptr[device]) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(g_silu_f16_table)) != hipSuccess) return nullptr;
+    hipLaunchKernelGGL(silu_f16_table_kernel, dim3(256), dim3(256), 0, s, static_cast<uint16_t*>(p));
+    if (hipGetLastError() != hipSuccess) return nullptr;
+    // Under stream capture the fill is only recorded (it runs with each replay, ahead of the
+    // kernel that reads the table), so the table counts as ready only after an eager fill.
+    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(s, &st) != hipSuccess) return nullptr;
+    if (st != hipStreamCaptureStatusNone) return static_cast<const uint16_t*>(p);
+    ptr[device] = static_cast<const uint16_t*>(p);
+  }
+  return ptr[device];
+}
+
+// fp16 channels-last apply for 16-byte aligned rows (HW % 8 == 0, Cp % 8 == 0): a 64-channel x
+// 64-pixel tile, thread t holding channels (2*(t%32), +1) of 8 consecutive pixels.  Both input
+// rows are read with 16-byte loads, each normalised pixel pair is written to LDS as one 32-bit
+// word of the pixel's channel row, and each output pixel row leaves as 16-byte stores of
+// 16-byte LDS reads: 4 LDS instructions per thread where an element-wise transpose needs 32.
+// The fused SiLU is a lookup of the narrowed normalised value (silu_f16_table).
+template <typename P>
+__global__ __launch_bounds__(256) void group_norm_apply_nhwc_f16_kernel(
+    const uint16_t* __restrict__ x, const P* __restrict__ gamma, const P* __restrict__ beta, uint16_t* __restrict__ y,
+    const float2* __restrict__ partial, int64_t C, int64_t Cp, int64_t groups, int64_t HW, int splits, float eps,
+    const uint16_t* __restrict__ silu_tab) {
+  constexpr int PW = 36;  // LDS words per pixel row: 64 channels + 8 pad (16-byte aligned rows)
+  __shared__ uint32_t tile[64 * PW];
+  __shared__ float2 st_s[64];
+  const int64_t b = blockIdx.z;
+  const int64_t p0 = (int64_t)blockIdx.x * 64, c0 = (int64_t)blockIdx.y * 64;
+  const int t = threadIdx.x;
+  const int cp = t & 31, po = t >> 5;  // channel pair, pixel octet
+  const int64_t ca = c0 + 2 * cp;
+  const int64_t pix = p0 + po * 8;
+  const int64_t gc = C / groups;
+  const int64_t g_first = c0 / gc;
+  float fa[8], fb[8];
+  float ga = 1.0f, ba = 0.0f, gb = 1.0f, bb = 0.0f;
+  auto load_row = [&](int64_t c, float (&f)[8]) {
+    if (c < C && pix < HW) {
+      // HW % 8 == 0: an octet is either whole or past the end
+      Vec16<uint16_t>::load(x + (b * C + c) * HW + pix, f);
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) f[j] = 0.0f;
+    }
+  };
+  load_row(ca, fa);
+  load_row(ca + 1, fb);
+  if (ca < C) {
+    if (gamma) ga = Elem<P>::load(gamma, ca);
+    if (beta) ba = Elem<P>::load(beta, ca);
+  }
+  if (ca + 1 < C) {
+    if (gamma) gb = Elem<P>::load(gamma, ca + 1);
+    if (beta) bb = Elem<P>::load(beta, ca + 1);
+  }
+  {
+    // statistics of the (at most 64) groups this tile's channels belong to, one wave each
+    const int64_t c_last = (c0 + 64 < C ? c0 + 64 : C) - 1;
+    const int ng = c0 < C ? (int)(c_last / gc - g_first + 1) : 0;
+    for (int k = t >> 6; k < ng; k += 4) {
+      const float2 st = fold_group_stats(partial, b * groups + g_first + k, splits, gc * HW, eps, t & 63);
+      if ((t & 63) == 0) st_s[k] = st;
+    }
+  }
+  __syncthreads();
+  {
+    const float2 sa = ca < C ? st_s[ca / gc - g_first] : make_float2(0.0f, 0.0f);
+    const float2 sb = ca + 1 < C ? st_s[(ca + 1) / gc - g_first] : make_float2(0.0f, 0.0f);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      uint32_t ha = ca < C ? f2h_fast(gn_value<uint16_t, P>(fa[j], sa.x, sa.y, ga, ba, 0)) : 0u;
+      uint32_t hb = ca + 1 < C ? f2h_fast(gn_value<uint16_t, P>(fb[j], sb.x, sb.y, gb, bb, 0)) : 0u;
+      if (silu_tab) {
+        // padding channels stay 0 (SiLU(0) = 0 anyway)
+        ha = silu_tab[ha];
+        hb = silu_tab[hb];
+      }
+      tile[(po * 8 + j) * PW + cp] = ha | (hb << 16);
+    }
+  }
+  __syncthreads();
+  {
+    const int pl = t >> 2, q = (t & 3) * 8;  // pixel row, word offset (16 channels)
+    const int64_t p = p0 + pl;
+    const int64_t cq = c0 + 2 * q;
+    if (p < HW) {
+      uint16_t* yr = y + (b * HW + p) * Cp + cq;
+      const uint4 lo = *reinterpret_cast<const uint4*>(&tile[pl * PW + q]);
+      const uint4 hi = *reinterpret_cast<const uint4*>(&tile[pl * PW + q + 4]);
+      if (cq + 8 <= Cp) *reinterpret_cast<uint4*>(yr) = lo;
+      if (cq + 16 <= Cp) *reinterpret_cast<uint4*>(yr + 8) = hi;
+    }
+  }
+}
+
 // ------------------------------------------------------------------------------ layer_norm
 // One wave per row; the row lives in registers (up to 64*MAXV elements).
 // P: parameter / computation dtype, as for group_norm (fp32 over fp16 data = the upcast pattern
@@ -535,9 +646,10 @@ int run_group_norm(int device, const void* x, const void* weight, const void* bi
   MTHIP_REQUIRE(n_groups <= 65535, "mthip_group_norm: batch*groups must be <= 65535");
   constexpr int V = Vec16<T>::N;
   const bool vect = ((uintptr_t)x % 16 == 0) && ((uintptr_t)y % 16 == 0) && inner % V == 0;
-  // Stats chunks of >= 8192 elements (16-32 KB per workgroup), at most 64 per group: the apply
-  // kernels fold a group's partials themselves.
-  int64_t splits = std::max<int64_t>(1, std::min<int64_t>(ceil_div(group_size, 8192), 64));
+  // Stats chunks of >= 2048 elements (4-8 KB per workgroup; the SD tensors give >= 4
+  // workgroups per CU, all loads in flight at once), at most 64 per group: the apply kernels
+  // fold a group's partials themselves.
+  int64_t splits = std::max<int64_t>(1, std::min<int64_t>(ceil_div(group_size, 2048), 64));
   int64_t chunk = ceil_div(group_size, splits);
   if (vect) chunk = ceil_div(chunk, V) * V;
   splits = ceil_div(group_size, chunk);
@@ -552,14 +664,27 @@ int run_group_norm(int device, const void* x, const void* weight, const void* bi
     hipLaunchKernelGGL((group_norm_stats_kernel<T, false>), grid, dim3(256), 0, s, (const T*)x, partial, group_size,
                        chunk, (int)splits);
   int rc = check_launch("group_norm_stats_kernel");
+  // The fp16 channels-last apply looks the fused SiLU up in a table (built on first use).
+  const bool nhwc_f16 = y_nhwc && sizeof(T) == 2 && ((uintptr_t)x % 16 == 0) && ((uintptr_t)y % 16 == 0) &&
+                        inner % V == 0 && Cp % V == 0;
+  const uint16_t* silu_tab = nullptr;
+  if (rc == MTHIP_OK && nhwc_f16 && fuse_silu) {
+    silu_tab = silu_f16_table(device, s);
+    if (!silu_tab) rc = fail(MTHIP_ERR_HIP, "mthip_group_norm: silu table setup failed");
+  }
   if (rc == MTHIP_OK) {
     if (y_nhwc) {
       dim3 g2((unsigned)ceil_div(inner, 64), (unsigned)ceil_div(Cp, 64), (unsigned)B);
       // 16-byte row access: pixel rows and channel rows start on 16-byte boundaries.
       const int vec_io = ((uintptr_t)x % 16 == 0) && ((uintptr_t)y % 16 == 0) && inner % V == 0 && Cp % V == 0;
-      hipLaunchKernelGGL((group_norm_apply_nhwc_kernel<T, P>), g2, dim3(256), 0, s, (const T*)x, (const P*)weight,
-                         (const P*)bias, (T*)y, (const float2*)partial, C, Cp, groups, inner, (int)splits, (float)eps,
-                         fuse_silu, vec_io);
+      if (nhwc_f16)
+        hipLaunchKernelGGL((group_norm_apply_nhwc_f16_kernel<P>), g2, dim3(256), 0, s, (const uint16_t*)x,
+                           (const P*)weight, (const P*)bias, (uint16_t*)y, (const float2*)partial, C, Cp, groups,
+                           inner, (int)splits, (float)eps, silu_tab);
+      else
+        hipLaunchKernelGGL((group_norm_apply_nhwc_kernel<T, P>), g2, dim3(256), 0, s, (const T*)x, (const P*)weight,
+                           (const P*)bias, (T*)y, (const float2*)partial, C, Cp, groups, inner, (int)splits,
+                           (float)eps, fuse_silu, vec_io);
     } else if (vect) {
       hipLaunchKernelGGL((group_norm_apply_kernel<T, P, true>), grid, dim3(256), 0, s, (const T*)x, (const P*)weight,
                          (const P*)bias, (T*)y, (const float2*)partial, C, groups, inner, group_size, chunk,
