@@ -162,7 +162,22 @@ int launch_tile(int device, GemmArgs a, int64_t batch, hipStream_t s) {
 //   2: 128x64 (2x2 waves of 64x32), 3 stages    3: 64x128 (2x2 waves of 32x64), 3 stages
 //   4: 128x128 (2x2 waves of 64x64), 3 stages   5: 128x128, 2 stages
 bool dtl_enabled() { return env_flag("MTHIP_GEMM_DTL", 1) != 0; }
-int dtl_tile() { return env_flag("MTHIP_GEMM_DTL_TILE", 0); }
+
+// Default shape per problem, from sweeps of the SD-1.5 GEMMs and convs (fp16, batch 2):
+// convs over more than 128 output pixels with a multiple of 128 output channels take 128x64
+// (5-18% over 64x64 at 640 and 1280 channels; at 320 channels the third 128-row tile is half
+// empty and 64x64 is 9% faster), the 8x8 convs (long K, split) 64x64 with 4 stages; linears take
+// 64x64 (3 stages) up to K = 1280, 4 stages beyond, 64x128 when M*N is large, 128x128 with 2
+// stages for the big square problems.
+int dtl_tile_for(int MODE, int64_t M, int64_t N, int64_t K) {
+  const int forced = env_flag("MTHIP_GEMM_DTL_TILE", -1);
+  if (forced >= 0) return forced;
+  if (MODE == MODE_CONV) return N <= 128 ? 1 : M % 128 == 0 ? 2 : 0;
+  if (M >= 4096 && N >= 4096 && K >= 2048) return 5;
+  if (K >= 2048) return 1;
+  if (M * N >= (int64_t)2048 * 1920 && K >= 640) return 3;
+  return 0;
+}
 
 template <int MODE, int EPI, int ACT>
 int launch_dtl(int device, const GemmArgs& a, int64_t batch, hipStream_t s) {
@@ -173,7 +188,7 @@ int launch_dtl(int device, const GemmArgs& a, int64_t batch, hipStream_t s) {
   } else if constexpr (ACT != MTHIP_ACT_NONE) {
     return launch_tile<T, 64, 64, MODE, EPI, ACT, F, 2, 3>(device, a, batch, s);
   } else {
-    switch (dtl_tile()) {
+    switch (dtl_tile_for(MODE, a.M, a.N, a.K)) {
       case 1:
         return launch_tile<T, 64, 64, MODE, EPI, ACT, F, 2, 4>(device, a, batch, s);
       case 2:

@@ -94,53 +94,74 @@ __global__ __launch_bounds__(256) void gemm_dtl_kernel(const GemmArgs args) {
   auto dma_row = [&](int I, int i) { return (wave * I + i) * 8 + (lane >> 3); };
   auto dma_chunk = [&](int row) { return (lane & 7) ^ ((row >> 1) & 7); };
 
-  // ---- loader state (the unit whose tiles are being fetched) -------------------------------
+  // ---- loader state (the unit whose tiles are being fetched).  All extents, offsets and
+  //      counters are 32-bit: the launcher keeps units, rows and columns below 2^31 and both
+  //      operands below 2 GiB.
+  const int M = (int)args.M, N = (int)args.N, K = (int)args.K;
+  const uint32_t units = (uint32_t)args.units;
+  const bool k_tail = (K % BK) != 0;
   __amdgpu_buffer_rsrc_t a_rsrc, b_rsrc;
   uint32_t a_off[AI], b_off[BI];
   int a_kc[AI], b_kc[BI];  // element k offset of the lane's chunk (K tails)
   int c_base[MODE == MODE_CONV ? BI : 1];
   uint32_t c_mask[MODE == MODE_CONV ? BI : 1];
-  int l_tap = 0, l_ky = 0, l_kx = 0, l_ch = 0;
+  // conv: the loader tile's tap (bit index into c_mask), its kx, channel offset within the tap,
+  // and the tap's element offset (ky*dh*W + kx*dw)*Cp relative to tap (0, 0)
+  int l_tap = 0, l_kx = 0, l_ch = 0, l_tap_el = 0;
   uint32_t l_u = blockIdx.x;
-  int64_t l_k = 0;
-  GemmUnit lun{};
+  int l_k = 0, l_nkt = 1;
+  uint32_t l_kb = 0;  // byte offset of the loader's K tile along a row
+  int l_kleft = 0;    // K - k0 of the loader's K tile
 
+  // A unit's tile origin, K range and batch.  A loader past the last unit gets out-of-range
+  // offsets and a K range it never leaves, so the step path needs no liveness tests.  The
+  // body is straight-line (the dead case is selects over the last unit's values): with an early
+  // return the compiler merges differing stores through a selected address and the loader
+  // state ends up in scratch memory.
   auto set_loader = [&]() {
-    lun = decode_unit<BM, BN>(args, l_u, nk_total);
+    const bool dead = l_u >= units;
+    const GemmUnit un = decode_unit<BM, BN>(args, dead ? units - 1 : l_u, nk_total);
+    const int m0 = (int)un.m0, n0 = (int)un.n0, kt0 = (int)un.kt0;
+    l_nkt = dead ? 0x7fffffff : (int)un.nkt;
+    l_kb = (uint32_t)kt0 * (BK * 2);
+    l_kleft = dead ? 0 : K - kt0 * BK;
     a_rsrc = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)(reinterpret_cast<const T*>(args.a) + lun.bz * args.stride_a), (short)0, (int)args.a_bytes, 0x00020000);
+        (void*)(reinterpret_cast<const T*>(args.a) + un.bz * args.stride_a), (short)0, (int)args.a_bytes, 0x00020000);
     b_rsrc = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)(reinterpret_cast<const T*>(args.b) + (MODE == MODE_CONV ? 0 : lun.bz * args.stride_b)), (short)0,
+        (void*)(reinterpret_cast<const T*>(args.b) + (MODE == MODE_CONV ? 0 : un.bz * args.stride_b)), (short)0,
         (int)args.b_bytes, 0x00020000);
+    const uint32_t lda = (uint32_t)args.lda;
 #pragma unroll
     for (int i = 0; i < AI; ++i) {
       const int r = dma_row(AI, i), c = dma_chunk(r);
-      const int64_t row = lun.m0 + r;
+      const int row = m0 + r;
       a_kc[i] = c * 8;
-      a_off[i] = row < args.M ? ((uint32_t)row * (uint32_t)args.lda + (uint32_t)(c * 8)) * 2u : kOOB;
+      a_off[i] = row < M && !dead ? ((uint32_t)row * lda + (uint32_t)(c * 8)) * 2u : kOOB;
     }
     if constexpr (MODE == MODE_NT) {
+      const uint32_t ldb = (uint32_t)args.ldb;
 #pragma unroll
       for (int i = 0; i < BI; ++i) {
         const int r = dma_row(BI, i), c = dma_chunk(r);
-        const int64_t row = lun.n0 + r;
+        const int row = n0 + r;
         b_kc[i] = c * 8;
-        b_off[i] = row < args.N ? ((uint32_t)row * (uint32_t)args.ldb + (uint32_t)(c * 8)) * 2u : kOOB;
+        b_off[i] = row < N && !dead ? ((uint32_t)row * ldb + (uint32_t)(c * 8)) * 2u : kOOB;
       }
     } else {
       const int H = (int)args.H, W = (int)args.W, KW = (int)args.KW, KH = (int)args.KH_, Cp = (int)args.Cp;
-      const int dh = (int)args.dh, dw = (int)args.dw;
+      const int dh = (int)args.dh, dw = (int)args.dw, sh = (int)args.sh, sw = (int)args.sw;
+      const int ph = (int)args.ph, pw = (int)args.pw;
 #pragma unroll
       for (int i = 0; i < BI; ++i) {
         const int r = dma_row(BI, i), c = dma_chunk(r);
         b_kc[i] = c * 8;
-        const int64_t p = lun.n0 + r;
-        const bool ok = p < args.N;
+        const int p = n0 + r;
+        const bool ok = p < N;
         const uint32_t pp = ok ? (uint32_t)p : 0u;
         const uint32_t img = args.div_ohw.div(pp), pix = pp - img * args.div_ohw.d;
         const uint32_t oyu = args.div_ow.div(pix);
-        const int iy0 = (int)oyu * (int)args.sh - (int)args.ph;
-        const int ix0 = (int)(pix - oyu * args.div_ow.d) * (int)args.sw - (int)args.pw;
+        const int iy0 = (int)oyu * sh - ph;
+        const int ix0 = (int)(pix - oyu * args.div_ow.d) * sw - pw;
         // element offset of x_nhwc[img, iy0, ix0, 8c] (negative in the padding; only taps that
         // land inside the image are turned into an address)
         c_base[i] = ok ? (((int)img * H + iy0) * W + ix0) * Cp + c * 8 : 0;
@@ -154,63 +175,67 @@ __global__ __launch_bounds__(256) void gemm_dtl_kernel(const GemmArgs args) {
           const int iy = iy0 + ky * dh;
           m |= (iy >= 0 && iy < H ? cols : 0u) << (ky * KW);
         }
-        c_mask[i] = ok ? m : 0u;
+        c_mask[i] = ok && !dead ? m : 0u;
       }
-      const int k0 = (int)(lun.kt0 * BK);
+      const int k0 = kt0 * BK;
       l_tap = k0 / Cp;
       l_ch = k0 - l_tap * Cp;
-      l_ky = l_tap / KW;
-      l_kx = l_tap - l_ky * KW;
+      const int ky = l_tap / KW;
+      l_kx = l_tap - ky * KW;
+      l_tap_el = (ky * dh * W + l_kx * dw) * Cp;
     }
   };
-  if (l_u < args.units) set_loader();
+  set_loader();
 
-  // Issues the loader cursor's K tile into stage st and advances the cursor.  Past the last unit
-  // every offset is kOOB: the stage receives zeros that are never read, and every step keeps
-  // issuing exactly L loads per wave, which the vmcnt accounting relies on.
+  // Issues the loader cursor's K tile into stage st and advances the cursor.  Every step issues
+  // exactly L loads per wave (zeros past the last unit), which the vmcnt accounting relies on.
   auto issue = [&](auto st) {
     const uint32_t sa = lds_addr(SA(st)), sb = lds_addr(SB(st));
-    const bool live = l_u < args.units;
-    const int64_t k0 = (lun.kt0 + l_k) * BK;
-    const uint32_t kb = live ? (uint32_t)(k0 * 2) : 0u;
+    const uint32_t kb = l_kb;
     if constexpr (MODE == MODE_NT) {
-      // a chunk past K would read the next row's data: only the last tile of an unaligned K
-      // needs the per-lane test
-      const bool whole = live && k0 + BK <= args.K;
-      const int kleft = (int)(args.K - k0);
+      if (!k_tail || l_kleft >= BK) {
 #pragma unroll
-      for (int i = 0; i < AI; ++i)
-        dma16(a_rsrc, sa + (wave * AI + i) * 1024, whole || (live && a_kc[i] < kleft) ? a_off[i] : kOOB, kb);
+        for (int i = 0; i < AI; ++i) dma16(a_rsrc, sa + (wave * AI + i) * 1024, a_off[i], kb);
 #pragma unroll
-      for (int i = 0; i < BI; ++i)
-        dma16(b_rsrc, sb + (wave * BI + i) * 1024, whole || (live && b_kc[i] < kleft) ? b_off[i] : kOOB, kb);
+        for (int i = 0; i < BI; ++i) dma16(b_rsrc, sb + (wave * BI + i) * 1024, b_off[i], kb);
+      } else {
+        // the last tile of an unaligned K: a chunk past K would read the next row's data
+#pragma unroll
+        for (int i = 0; i < AI; ++i)
+          dma16(a_rsrc, sa + (wave * AI + i) * 1024, a_kc[i] < l_kleft ? a_off[i] : kOOB, kb);
+#pragma unroll
+        for (int i = 0; i < BI; ++i)
+          dma16(b_rsrc, sb + (wave * BI + i) * 1024, b_kc[i] < l_kleft ? b_off[i] : kOOB, kb);
+      }
     } else {
       // K = taps * Cp is a whole number of tiles and a tile never straddles two taps.
 #pragma unroll
-      for (int i = 0; i < AI; ++i) dma16(a_rsrc, sa + (wave * AI + i) * 1024, live ? a_off[i] : kOOB, kb);
-      const int tap_el = (l_ky * (int)args.dh * (int)args.W + l_kx * (int)args.dw) * (int)args.Cp;
+      for (int i = 0; i < AI; ++i) dma16(a_rsrc, sa + (wave * AI + i) * 1024, a_off[i], kb);
       const uint32_t chb = (uint32_t)l_ch * 2u;
 #pragma unroll
       for (int i = 0; i < BI; ++i) {
-        const bool in = live && ((c_mask[i] >> l_tap) & 1u);
-        dma16(b_rsrc, sb + (wave * BI + i) * 1024, in ? (uint32_t)(c_base[i] + tap_el) * 2u : kOOB, chb);
+        const bool in = (c_mask[i] >> l_tap) & 1u;
+        dma16(b_rsrc, sb + (wave * BI + i) * 1024, in ? (uint32_t)(c_base[i] + l_tap_el) * 2u : kOOB, chb);
       }
-      if (live) {
-        l_ch += BK;
-        if (l_ch == (int)args.Cp) {
-          l_ch = 0;
-          ++l_tap;
-          if (++l_kx == (int)args.KW) {
-            l_kx = 0;
-            ++l_ky;
-          }
-        }
-      }
+      // Advance (channel, tap) with selects: a branchy update lets the compiler merge the
+      // counters' stores through a selected address, which keeps them out of registers.
+      const int Cp = (int)args.Cp;
+      const int nch = l_ch + BK;
+      const bool next_tap = nch == Cp;
+      const int nkx = l_kx + (next_tap ? 1 : 0);
+      const bool next_row = nkx == (int)args.KW;
+      l_ch = next_tap ? 0 : nch;
+      l_tap += next_tap ? 1 : 0;
+      l_kx = next_row ? 0 : nkx;
+      l_tap_el += (next_tap ? (int)args.dw * Cp : 0) +
+                  (next_row ? ((int)args.dh * (int)args.W - (int)args.KW * (int)args.dw) * Cp : 0);
     }
-    if (live && ++l_k == lun.nkt) {
+    l_kb += BK * 2;
+    l_kleft -= BK;
+    if (++l_k == l_nkt) {
       l_k = 0;
       l_u += G;
-      if (l_u < args.units) set_loader();
+      set_loader();
     }
   };
 
@@ -258,9 +283,9 @@ __global__ __launch_bounds__(256) void gemm_dtl_kernel(const GemmArgs args) {
   };
 
   uint32_t c_u = blockIdx.x;
-  int64_t c_k = 0;
-  if (c_u >= args.units) return;  // (the launcher sizes the grid to at most `units`)
-  GemmUnit cun = decode_unit<BM, BN>(args, c_u, nk_total);
+  if (c_u >= units) return;  // (the launcher sizes the grid to at most `units`)
+  int c_k = 0;
+  int c_nkt = (int)decode_unit<BM, BN>(args, c_u, nk_total).nkt;
 
   auto step = [&](auto st) -> bool {
     constexpr int s = decltype(st)::value;
@@ -268,13 +293,13 @@ __global__ __launch_bounds__(256) void gemm_dtl_kernel(const GemmArgs args) {
     __builtin_amdgcn_s_barrier();
     issue(ic<(s + S - 1) % S>{});
     compute(st);
-    if (++c_k == cun.nkt) {
-      gemm_finish_unit<T, BM, BN, WGM, EPI, ACT>(args, cun, acc, lane, wm, wn);
+    if (++c_k == c_nkt) {
+      gemm_finish_unit<T, BM, BN, WGM, EPI, ACT>(args, decode_unit<BM, BN>(args, c_u, nk_total), acc, lane, wm, wn);
       zero_acc();
       c_k = 0;
       c_u += G;
-      if (c_u >= args.units) return false;
-      cun = decode_unit<BM, BN>(args, c_u, nk_total);
+      if (c_u >= units) return false;
+      c_nkt = (int)decode_unit<BM, BN>(args, c_u, nk_total).nkt;
     }
     return true;
   };
