@@ -151,8 +151,8 @@ def run_resnet(args):
         "config": {"workload": "configs[1] ResNet sub-block fp16: x[2,320,64,64], GN(32), SiLU, conv3x3 320->320, residual",
                    "batch": 2, "channels": 320, "hw": [64, 64]},
         "roofline": {
-            "kernel": "conv3x3 launch: gemm_kernel<fp16, 64x64, MODE_CONV, EPI_CONV> over 2 K slices + "
-                      "gemm_splitk_reduce_kernel (bias and residual fused in the reduction)",
+            "kernel": "conv3x3 launch: gemm_dtl_kernel<64x64, 3 LDS stages, MODE_CONV, EPI_CONV> "
+                      "(direct-to-LDS implicit GEMM, one K slice; bias and residual fused in the epilogue)",
             "bound": "mfma",
             "achieved": round(conv_tflops, 3),
             "peak": PEAK["fp16_mfma_tflops"],
