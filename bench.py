@@ -114,7 +114,7 @@ def run_resnet(args):
         if marks:
             marks[0].record()
         _lib.check(L.mthip_conv2d_nhwc(0, _lib.F16, xn.ptr, wp, bbd.data_ptr(), y.data_ptr(), B, C, H, W, O, 3, 3,
-                                       1, 1, 1, 1, 1, 1, xd.data_ptr()))
+                                       1, 1, 1, 1, 1, 1, xd.data_ptr(), None, 0))
         if marks:
             marks[1].record()
 

@@ -219,11 +219,15 @@ int mthip_conv2d_prepacked(int device, int dtype, const void* x, const void* wp,
  * packed weight, channels C..Cp-1 zero), e.g. as written by mthip_group_norm_nhwc; the output
  * (and residual) stay NCHW.  This is the GroupNorm -> SiLU -> conv hand-off of every SD ResNet
  * block: the normalised activation is written once, in the layout the conv reads, instead of
- * NCHW plus a transposing copy.  Launches only the GEMM. */
+ * NCHW plus a transposing copy.  chan_add (optional, NULL for none) adds
+ * chan_add[b * chan_add_ld + o] to every pixel of output plane (b, o) after the bias and before
+ * the residual -- the `h + t[:, :, None, None]` time-embedding add of an SD ResNet block
+ * (binary add, tensor.cpp:18965), narrowed as that separate add narrows.  Launches only the GEMM. */
 int mthip_conv2d_nhwc(int device, int dtype, const void* x_nhwc, const void* wp, const void* b, void* y,
                       int64_t B, int64_t C, int64_t H, int64_t W, int64_t O, int64_t KH, int64_t KW,
                       int64_t stride_h, int64_t stride_w, int64_t pad_h, int64_t pad_w,
-                      int64_t dil_h, int64_t dil_w, const void* residual);
+                      int64_t dil_h, int64_t dil_w, const void* residual, const void* chan_add,
+                      int64_t chan_add_ld);
 
 /* ===================================================================== attention */
 

@@ -66,7 +66,8 @@ _SIGNATURES = {
     "mthip_conv2d_prepacked": (_int, [_int, _int, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i64,
                                       _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _c_void_p]),
     "mthip_conv2d_nhwc": (_int, [_int, _int, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i64,
-                                 _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _c_void_p]),
+                                 _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _c_void_p,
+                                 _c_void_p, _i64]),
     "mthip_sdpa": (_int, [_int, _int, _c_void_p, _i64p, _c_void_p, _i64p, _c_void_p, _i64p, _c_void_p, _i64p,
                           _i64, _i64, _i64, _i64, _i64, _i64, _i64, _int, _int, _c_void_p, _i64p, _int, _dbl]),
     "mthip_group_norm": (_int, [_int, _int, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i64,

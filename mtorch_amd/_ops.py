@@ -662,16 +662,19 @@ def _conv_residual(residual, out):
 
 
 def group_norm_silu_conv2d(x: Tensor, num_groups: int, gn_weight: Tensor, gn_bias: Tensor, eps, w: Tensor,
-                           b: Tensor = None, stride=1, padding=0, dilation=1, residual: Tensor = None) -> Tensor:
-    """conv2d(silu(group_norm(x, num_groups, gn_weight, gn_bias, eps)), w, b, ...) (+ residual):
-    the GroupNorm -> SiLU -> conv chain of an SD ResNet block (the reference runs it as three
-    ops, tensor.cpp:18643, 16480, 26490).  On the device the normalised activation is written
+                           b: Tensor = None, stride=1, padding=0, dilation=1, residual: Tensor = None,
+                           chan_add: Tensor = None) -> Tensor:
+    """conv2d(silu(group_norm(x, num_groups, gn_weight, gn_bias, eps)), w, b, ...)
+    (+ chan_add[:, :, None, None]) (+ residual): the GroupNorm -> SiLU -> conv chain of an SD
+    ResNet block, with its time-embedding add (the reference runs these as separate ops,
+    tensor.cpp:18643, 16480, 26490, 18965).  On the device the normalised activation is written
     once, channels-last, in the layout the implicit-GEMM conv reads (mthip_group_norm_nhwc then
-    mthip_conv2d_nhwc); values equal the unfused sequence's.  fp32 GroupNorm parameters over an
-    fp16 input mean the upcast pattern silu(group_norm(x.float(), ...).half())."""
+    mthip_conv2d_nhwc), and the adds happen in the conv's epilogue; values equal the unfused
+    sequence's.  chan_add is [B, O] (rows may be strided).  fp32 GroupNorm parameters over an fp16
+    input mean the upcast pattern silu(group_norm(x.float(), ...).half())."""
     pdt = _norm_param_dtype("group_norm", x, gn_weight, gn_bias)
-    _same_dtype("conv2d", [x, w, b], "tensors")
-    dev = _gpu("group_norm_silu_conv2d", x, gn_weight, gn_bias, w, b, residual)
+    _same_dtype("conv2d", [x, w, b, chan_add], "tensors")
+    dev = _gpu("group_norm_silu_conv2d", x, gn_weight, gn_bias, w, b, residual, chan_add)
     if x.dim() != 4:
         raise ValueError("group_norm_silu_conv2d expects a 4-D input tensor")
     _group_norm_check(x, num_groups, gn_weight, gn_bias)
@@ -679,6 +682,13 @@ def group_norm_silu_conv2d(x: Tensor, num_groups: int, gn_weight: Tensor, gn_bia
     B, C, H, W, O, KH, KW = p["B"], p["C"], p["H"], p["W"], p["O"], p["KH"], p["KW"]
     out = _empty([B, O, p["OH"], p["OW"]], x.dtype, dev)
     rc = _conv_residual(residual, out)
+    ca, ca_ld = None, 0
+    if chan_add is not None:
+        if list(chan_add.shape) != [B, O]:
+            raise ValueError("group_norm_silu_conv2d: chan_add must be [batch, out_channels]")
+        ok = chan_add.stride(1) == 1 and (B == 1 or chan_add.stride(0) >= O)
+        ca = chan_add if ok else chan_add.contiguous()
+        ca_ld = ca.stride(0) if B > 1 else O
     if out.numel():
         L = _L()
         vec = 8 if x.dtype is T.float16 else 4
@@ -689,7 +699,8 @@ def group_norm_silu_conv2d(x: Tensor, num_groups: int, gn_weight: Tensor, gn_bia
                                            pdt))
         wp = _conv_packed_weight(w.contiguous(), dev, O, C, KH, KW)
         _lib.check(L.mthip_conv2d_nhwc(dev, x.dtype.code, xn.ptr, wp, _ptr(_contig(b)), out.data_ptr(), B, C, H, W, O,
-                                       KH, KW, p["sh"], p["sw"], p["ph"], p["pw"], p["dh"], p["dw"], _ptr(rc)))
+                                       KH, KW, p["sh"], p["sw"], p["ph"], p["pw"], p["dh"], p["dw"], _ptr(rc), _ptr(ca),
+                                       ca_ld))
         del xn  # stream-ordered free: reused only by later work
     return out
 
@@ -711,7 +722,7 @@ def conv2d_tokens(tok: Tensor, w: Tensor, b: Tensor, H: int, W: int, residual: T
     tc = tok.contiguous()
     wp = _conv_packed_weight(w.contiguous().reshape(O, C, 1, 1), dev, O, C, 1, 1)
     _lib.check(_L().mthip_conv2d_nhwc(dev, tok.dtype.code, tc.data_ptr(), wp, _ptr(_contig(b)), out.data_ptr(), B, C, H,
-                                      W, O, 1, 1, 1, 1, 0, 0, 1, 1, _ptr(rc)))
+                                      W, O, 1, 1, 1, 1, 0, 0, 1, 1, _ptr(rc), None, 0))
     return out
 
 

@@ -103,7 +103,8 @@ int launch_pack_weight(const void* w, void* wp, int64_t O, int64_t C, int64_t KH
 template <typename T>
 int run_conv_gemm_nhwc(int device, int dtype, const void* xp, const void* wp, const void* b, void* y, int64_t B,
                        int64_t C, int64_t H, int64_t W, int64_t O, int64_t KH, int64_t KW, int64_t sh, int64_t sw,
-                       int64_t ph, int64_t pw, int64_t dh, int64_t dw, const void* residual, hipStream_t s) {
+                       int64_t ph, int64_t pw, int64_t dh, int64_t dw, const void* residual, hipStream_t s,
+                       const void* chan_add = nullptr, int64_t chan_add_ld = 0) {
   const int64_t OH = (H + 2 * ph - dh * (KH - 1) - 1) / sh + 1;
   const int64_t OW = (W + 2 * pw - dw * (KW - 1) - 1) / sw + 1;
   if (B == 0 || OH <= 0 || OW <= 0) return MTHIP_OK;
@@ -121,6 +122,8 @@ int run_conv_gemm_nhwc(int device, int dtype, const void* xp, const void* wp, co
   a.c = y;
   a.bias = b;
   a.residual = residual;
+  a.chan_add = chan_add;
+  a.chan_add_ld = chan_add_ld;
   a.H = H;
   a.W = W;
   a.Cp = Cp;
@@ -249,8 +252,9 @@ extern "C" int mthip_conv2d_prepacked(int device, int dtype, const void* x, cons
 extern "C" int mthip_conv2d_nhwc(int device, int dtype, const void* x_nhwc, const void* wp, const void* b, void* y,
                                  int64_t B, int64_t C, int64_t H, int64_t W, int64_t O, int64_t KH, int64_t KW,
                                  int64_t stride_h, int64_t stride_w, int64_t pad_h, int64_t pad_w, int64_t dil_h,
-                                 int64_t dil_w, const void* residual) {
+                                 int64_t dil_w, const void* residual, const void* chan_add, int64_t chan_add_ld) {
   MTHIP_REQUIRE(dtype == MTHIP_F16 || dtype == MTHIP_F32, "mthip_conv2d_nhwc: dtype must be F16 or F32");
+  MTHIP_REQUIRE(chan_add == nullptr || chan_add_ld >= O, "mthip_conv2d_nhwc: chan_add row stride below O");
   MTHIP_REQUIRE(B >= 0 && C > 0 && H > 0 && W > 0 && O > 0 && KH > 0 && KW > 0, "mthip_conv2d_nhwc: bad extents");
   MTHIP_REQUIRE(stride_h > 0 && stride_w > 0 && dil_h > 0 && dil_w > 0 && pad_h >= 0 && pad_w >= 0,
                 "mthip_conv2d_nhwc: bad stride/padding/dilation");
@@ -261,7 +265,7 @@ extern "C" int mthip_conv2d_nhwc(int device, int dtype, const void* x_nhwc, cons
   if (int rc = use_device(device)) return rc;
   if (dtype == MTHIP_F16)
     return run_conv_gemm_nhwc<uint16_t>(device, dtype, x_nhwc, wp, b, y, B, C, H, W, O, KH, KW, stride_h, stride_w,
-                                        pad_h, pad_w, dil_h, dil_w, residual, s);
+                                        pad_h, pad_w, dil_h, dil_w, residual, s, chan_add, chan_add_ld);
   return run_conv_gemm_nhwc<float>(device, dtype, x_nhwc, wp, b, y, B, C, H, W, O, KH, KW, stride_h, stride_w, pad_h,
-                                   pad_w, dil_h, dil_w, residual, s);
+                                   pad_w, dil_h, dil_w, residual, s, chan_add, chan_add_ld);
 }

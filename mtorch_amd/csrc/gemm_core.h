@@ -118,6 +118,10 @@ struct GemmArgs {
   int xcd_remap;  // 1: number units XCD-contiguously (see decode_unit)
   // EPI_GEGLU: gelu of every fp16 value (65536 entries, mtorch's fp16 gelu bit for bit)
   const uint16_t* gelu_tab;
+  // EPI_CONV: per-(image, output channel) addend chan_add[img * chan_add_ld + row] (an SD
+  // ResNet block's time embedding), added after the bias and before the residual
+  const void* chan_add;
+  int64_t chan_add_ld;
 };
 
 // Stores the first nv (1..4) of 4 consecutive outputs, narrowed once each; one 8-byte (fp16)
@@ -190,14 +194,19 @@ __device__ __forceinline__ void emit4(const GemmArgs& args, int64_t bz, int row,
     const int OHW = (int)(args.OH * args.OW);
     const T* bias = reinterpret_cast<const T*>(args.bias);
     const T* res = reinterpret_cast<const T*>(args.residual);
+    const T* cadd = reinterpret_cast<const T*>(args.chan_add);
     const float bv = bias ? Elem<T>::load(bias, row) : 0.0f;
+    // conv + bias, then (+ chan_add), then (+ residual), each add narrowed as the unfused op
+    // sequence narrows it
     if (OHW % 4 == 0) {
       // col0 is a multiple of 4, so the 4 pixels lie in one image and are contiguous.
       const int img = (int)args.div_ohw.div((uint32_t)col0);
       const int64_t addr = ((int64_t)img * M + row) * OHW + (col0 - img * OHW);
+      const float av = cadd ? Elem<T>::load(cadd, img * args.chan_add_ld + row) : 0.0f;
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
         float x = v[t] + bv;
+        if (cadd) x = Elem<T>::round_trip(x) + av;
         if (res) x = Elem<T>::round_trip(x) + (t < nv ? Elem<T>::load(res, addr + t) : 0.0f);
         v[t] = x;
       }
@@ -208,6 +217,7 @@ __device__ __forceinline__ void emit4(const GemmArgs& args, int64_t bz, int row,
         const int im = (int)args.div_ohw.div((uint32_t)c), px = c - im * OHW;
         const int64_t addr = ((int64_t)im * M + row) * OHW + px;
         float x = v[t] + bv;
+        if (cadd) x = Elem<T>::round_trip(x) + Elem<T>::load(cadd, im * args.chan_add_ld + row);
         if (res) x = Elem<T>::round_trip(x) + Elem<T>::load(res, addr);
         Elem<T>::store(Cptr, addr, x);
       }

@@ -459,87 +459,117 @@ __global__ __launch_bounds__(256) void layer_norm_kernel(const T* __restrict__ x
   }
 }
 
+// V consecutive parameters (V a multiple of the 16-byte vector width of P) as floats.
+template <typename P, int V>
+__device__ __forceinline__ void load_params(const P* p, float (&f)[V]) {
+  constexpr int PV = Vec16<P>::N;
+#pragma unroll
+  for (int k = 0; k < V; k += PV) {
+    float part[PV];
+    Vec16<P>::load(p + k, part);
+#pragma unroll
+    for (int q = 0; q < PV; ++q) f[k + q] = part[q];
+  }
+}
+
 // Rows whose length is a whole number of 16-byte chunks (every SD LayerNorm: 320..1280
-// channels): one wave per row, CPL chunks per lane, the affine parameters requested together
-// with the row so all loads are in flight at once.
-template <typename T, typename P, int CPL>
+// channels).  One wave per RPW rows; a row lives in registers as CPL 16-byte chunks per lane.  The affine
+// parameters are loaded once per wave as 16-byte vectors, and all RPW rows are requested before
+// the first is reduced, so their loads are in flight together.
+template <typename T, typename P, int CPL, int RPW>
 __global__ __launch_bounds__(256) void layer_norm_vec_kernel(const T* __restrict__ x, const P* __restrict__ w,
                                                              const P* __restrict__ b, T* __restrict__ y, int64_t rows,
                                                              int64_t N, float eps) {
   constexpr int V = Vec16<T>::N;
   const int lane = threadIdx.x & 63;
-  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (row >= rows) return;
+  const int64_t row0 = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * RPW;
+  if (row0 >= rows) return;
   const int chunks = (int)(N / V);
-  const T* xr = x + row * N;
-  float v[CPL][V], wv[CPL][V], bv[CPL][V];
+  float v[RPW][CPL][V];
+#pragma unroll
+  for (int r = 0; r < RPW; ++r)
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+      const int c = lane + 64 * j;
+      if (row0 + r < rows && c < chunks) {
+        Vec16<T>::load(x + (row0 + r) * N + c * V, v[r][j]);
+      } else {
+#pragma unroll
+        for (int k = 0; k < V; ++k) v[r][j][k] = 0.0f;
+      }
+    }
+  float wv[CPL][V], bv[CPL][V];
 #pragma unroll
   for (int j = 0; j < CPL; ++j) {
     const int c = lane + 64 * j;
 #pragma unroll
     for (int k = 0; k < V; ++k) {
-      v[j][k] = 0.0f;
       wv[j][k] = 1.0f;
       bv[j][k] = 0.0f;
     }
     if (c < chunks) {
-      Vec16<T>::load(xr + c * V, v[j]);
-#pragma unroll
-      for (int k = 0; k < V; ++k) {
-        if (w) wv[j][k] = Elem<P>::load(w, c * V + k);
-        if (b) bv[j][k] = Elem<P>::load(b, c * V + k);
-      }
+      if (w) load_params<P, V>(w + c * V, wv[j]);
+      if (b) load_params<P, V>(b + c * V, bv[j]);
     }
   }
-  float s = 0.0f;
-#pragma unroll
-  for (int j = 0; j < CPL; ++j)
-#pragma unroll
-    for (int k = 0; k < V; ++k) s += v[j][k];
   const float n = (float)N;
-  const float mean = wave_sum(s) / n;
-  float var;
-  if constexpr (sizeof(P) == 2) {
-    // fp16: two-pass centred variance (tensor.cpp:17531-17545).
-    float css = 0.0f;
+#pragma unroll
+  for (int r = 0; r < RPW; ++r) {
+    if (row0 + r >= rows) break;
+    float s = 0.0f;
 #pragma unroll
     for (int j = 0; j < CPL; ++j)
-      if (lane + 64 * j < chunks)
+#pragma unroll
+      for (int k = 0; k < V; ++k) s += v[r][j][k];
+    float mean, var;
+    if constexpr (sizeof(P) == 2) {
+      // fp16: two-pass centred variance (tensor.cpp:17531-17545).
+      mean = wave_sum(s) / n;
+      float css = 0.0f;
+#pragma unroll
+      for (int j = 0; j < CPL; ++j)
+        if (lane + 64 * j < chunks)
+#pragma unroll
+          for (int k = 0; k < V; ++k) {
+            const float c = v[r][j][k] - mean;
+            css += c * c;
+          }
+      var = fmaxf(0.0f, wave_sum(css) / n);
+    } else {
+      // fp32: one-pass sum of squares (tensor.cpp:17577-17587); both sums reduce together.
+      float ss = 0.0f;
+#pragma unroll
+      for (int j = 0; j < CPL; ++j)
+#pragma unroll
+        for (int k = 0; k < V; ++k) ss += v[r][j][k] * v[r][j][k];
+#pragma unroll
+      for (int off = 32; off >= 1; off >>= 1) {
+        s += __shfl_xor(s, off, 64);
+        ss += __shfl_xor(ss, off, 64);
+      }
+      mean = s / n;
+      var = fmaxf(0.0f, ss / n - mean * mean);
+    }
+    const float inv = 1.0f / sqrtf(var + eps);
+    T* yr = y + (row0 + r) * N;
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+      const int c = lane + 64 * j;
+      if (c < chunks) {
+        float o[V];
 #pragma unroll
         for (int k = 0; k < V; ++k) {
-          const float c = v[j][k] - mean;
-          css += c * c;
+          float t = (v[r][j][k] - mean) * inv;
+          if (w) t = t * wv[j][k];
+          if (b) t = t + bv[j][k];
+          o[k] = t;
         }
-    var = fmaxf(0.0f, wave_sum(css) / n);
-  } else {
-    // fp32: one-pass sum of squares (tensor.cpp:17577-17587).
-    float ss = 0.0f;
-#pragma unroll
-    for (int j = 0; j < CPL; ++j)
-#pragma unroll
-      for (int k = 0; k < V; ++k) ss += v[j][k] * v[j][k];
-    var = fmaxf(0.0f, wave_sum(ss) / n - mean * mean);
-  }
-  const float inv = 1.0f / sqrtf(var + eps);
-  T* yr = y + row * N;
-#pragma unroll
-  for (int j = 0; j < CPL; ++j) {
-    const int c = lane + 64 * j;
-    if (c < chunks) {
-      float o[V];
-#pragma unroll
-      for (int k = 0; k < V; ++k) {
-        float t = (v[j][k] - mean) * inv;
-        if (w) t = t * wv[j][k];
-        if (b) t = t + bv[j][k];
-        o[k] = t;
+        Vec16<T>::store(yr + c * V, o);
       }
-      Vec16<T>::store(yr + c * V, o);
     }
   }
 }
 
-// Rows too long for registers: one workgroup per row, three passes over the row.
 template <typename T, typename P>
 __global__ __launch_bounds__(256) void layer_norm_long_kernel(const T* __restrict__ x, const P* __restrict__ w,
                                                               const P* __restrict__ b, T* __restrict__ y, int64_t N,
@@ -711,16 +741,28 @@ int run_layer_norm(const void* x, const void* w, const void* b, void* y, int64_t
   const P* bp = (const P*)b;
   T* yp = (T*)y;
   constexpr int V = Vec16<T>::N;
-  if (N % V == 0 && (uintptr_t)x % 16 == 0 && (uintptr_t)y % 16 == 0 && N <= 64 * V * 4) {
+  const bool params_aligned = (uintptr_t)w % 16 == 0 && (uintptr_t)b % 16 == 0;
+  if (N % V == 0 && (uintptr_t)x % 16 == 0 && (uintptr_t)y % 16 == 0 && params_aligned && N <= 64 * V * 4) {
     const int64_t chunks = N / V;
+    // two rows per wave once there are enough rows to keep >= 4 waves per SIMD
+    const bool two = rows >= 8192;
+    const unsigned g = (unsigned)ceil_div(rows, two ? 8 : 4);
+#define MTHIP_LN_VEC(CPL)                                                                                           \
+  do {                                                                                                             \
+    if (two)                                                                                                       \
+      hipLaunchKernelGGL((layer_norm_vec_kernel<T, P, CPL, 2>), dim3(g), dim3(256), 0, s, xp, wp, bp, yp, rows, N, e); \
+    else                                                                                                           \
+      hipLaunchKernelGGL((layer_norm_vec_kernel<T, P, CPL, 1>), dim3(g), dim3(256), 0, s, xp, wp, bp, yp, rows, N, e); \
+  } while (0)
     if (chunks <= 64)
-      hipLaunchKernelGGL((layer_norm_vec_kernel<T, P, 1>), dim3(grid4), dim3(256), 0, s, xp, wp, bp, yp, rows, N, e);
+      MTHIP_LN_VEC(1);
     else if (chunks <= 128)
-      hipLaunchKernelGGL((layer_norm_vec_kernel<T, P, 2>), dim3(grid4), dim3(256), 0, s, xp, wp, bp, yp, rows, N, e);
+      MTHIP_LN_VEC(2);
     else if (chunks <= 192)
-      hipLaunchKernelGGL((layer_norm_vec_kernel<T, P, 3>), dim3(grid4), dim3(256), 0, s, xp, wp, bp, yp, rows, N, e);
+      MTHIP_LN_VEC(3);
     else
-      hipLaunchKernelGGL((layer_norm_vec_kernel<T, P, 4>), dim3(grid4), dim3(256), 0, s, xp, wp, bp, yp, rows, N, e);
+      MTHIP_LN_VEC(4);
+#undef MTHIP_LN_VEC
     return check_launch("layer_norm_vec_kernel");
   }
   if (N <= 64 * 4)

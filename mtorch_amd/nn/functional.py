@@ -60,11 +60,12 @@ def group_norm_silu(input, num_groups, weight=None, bias=None, eps=1e-5):
 
 
 def group_norm_silu_conv2d(input, num_groups, gn_weight, gn_bias, eps, weight, bias=None, stride=1, padding=0,
-                           dilation=1, residual=None):
+                           dilation=1, residual=None, chan_add=None):
     """conv2d(silu(group_norm(input, num_groups, gn_weight, gn_bias, eps)), weight, bias, ...)
-    (+ residual), with the normalised activation handed to the conv channels-last"""
+    (+ chan_add[:, :, None, None]) (+ residual), with the normalised activation handed to the
+    conv channels-last and both adds in the conv's epilogue"""
     return _ops.group_norm_silu_conv2d(input, num_groups, gn_weight, gn_bias, eps, weight, bias, stride, padding,
-                                       dilation, residual)
+                                       dilation, residual, chan_add)
 
 
 def conv2d_residual(input, weight, bias, residual, stride=1, padding=0, dilation=1, groups=1):

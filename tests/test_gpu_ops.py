@@ -489,6 +489,36 @@ def test_group_norm_silu_conv2d_channels_last_handoff(dt, B, C, H, W, O, G):
     assert rel(val(got), val(orc.conv2d(h, w, None, stride=2, padding=1))) <= TOL[dt]
 
 
+@pytest.mark.parametrize("dt", ["float32", "float16"])
+@pytest.mark.parametrize("B,C,H,W,O,G", [(2, 64, 16, 16, 48, 32), (2, 40, 9, 7, 40, 8), (1, 16, 8, 8, 24, 4)])
+def test_group_norm_silu_conv2d_channel_add_is_the_separate_add(dt, B, C, H, W, O, G):
+    """The time-embedding add fused into the conv epilogue (chan_add, here a strided slice of a
+    wider projection) gives exactly the unfused conv -> add (-> residual add) sequence, and both
+    match the oracle."""
+    g = Gen(B * 2000 + C + O)
+    x = g.randn((B, C, H, W), dt)
+    gamma = g.randn((C,), dt)
+    beta = g.randn((C,), dt)
+    w = g.randn((O, C, 3, 3), dt, 1.0 / np.sqrt(9 * C))
+    b = g.randn((O,), dt)
+    r = g.randn((B, O, H, W), dt)
+    proj = dev(g.randn((B, O + 24), dt))
+    t = proj[:, 16:16 + O]  # row stride O + 24
+    args = (G, dev(gamma), dev(beta), 1e-5, dev(w), dev(b))
+    xd, rd = dev(x), dev(r)
+    plain = F.group_norm_silu_conv2d(xd, *args, padding=1)
+    sep = plain + t.unsqueeze(-1).unsqueeze(-1)
+    fused = F.group_norm_silu_conv2d(xd, *args, padding=1, chan_add=t)
+    assert np.array_equal(host(fused).view(np.uint8), host(sep).view(np.uint8))
+    sep_res = sep + rd
+    fused_res = F.group_norm_silu_conv2d(xd, *args, padding=1, chan_add=t, residual=rd)
+    assert np.array_equal(host(fused_res).view(np.uint8), host(sep_res).view(np.uint8))
+    h = orc.silu(orc.group_norm(x, G, gamma, beta, 1e-5))
+    tt = np.asarray(val(host(t)), dtype=np.float64)[:, :, None, None]
+    ref = val(orc.conv2d(h, w, b, padding=1)) + tt + val(r)
+    assert rel(val(host(fused_res)), ref) <= TOL[dt]
+
+
 def test_sd_group_norm_scenario_fixture():
     hidden, w, b = closed_form.sd_group_norm_inputs()
     exp = np.load(os.path.join(HERE, "golden", "sd_group_norm_1x320x16x16.npz"))["y"]
