@@ -86,15 +86,14 @@ __device__ __forceinline__ uint16_t f2h_bits(float value) {
   return (uint16_t)(sign | (rounded >= 0x7c00u ? 0x7c00u : rounded));
 }
 
-// Bit-identical to f2h_bits for every input, branch-free and short (it is inlined into every
-// narrowing store).  mtorch's rule is round-to-nearest with ties away from zero, overflowing to
+// Bit-identical to f2h_bits for every input, and branch-free.  mtorch's rule is round-to-nearest with ties away from zero, overflowing to
 // inf; the hardware conversion (v_cvt_f16_f32, with fp16 subnormals) rounds to nearest-even
 // and overflows the same way.  The two differ only on exact ties whose kept LSB is 0, where
 // RNE keeps the smaller magnitude: with sh discarded significand bits (13 for normal halves,
 // up to 24 for the smallest subnormal, biased float exponent 102..142), such a tie has
 // significand & (2^(sh+1) - 1) == 2^(sh-1), and one ulp is added to the magnitude.  NaNs keep
 // the top payload bits as mtorch does (the hardware would set the quiet bit).
-__device__ __forceinline__ uint16_t f2h_fast(float value) {
+__device__ __forceinline__ uint16_t f2h_generic(float value) {
   const uint32_t bits = __float_as_uint(value);
   const uint32_t raw = (bits >> 23) & 0xffu;
   uint32_t h = __builtin_bit_cast(uint16_t, (_Float16)value);
@@ -106,6 +105,27 @@ __device__ __forceinline__ uint16_t f2h_fast(float value) {
   const uint32_t payload = (bits & 0x7fffffu) >> 13;
   const uint32_t nan_bits = ((bits >> 16) & 0x8000u) | 0x7c00u | (payload != 0u ? payload : 0x200u);
   return (uint16_t)((bits & 0x7fffffffu) > 0x7f800000u ? nan_bits : h);
+}
+
+// Same function with a short common path: for zero and |value| in [2^-14, 2^16) the result
+// is a normal half (or the overflow to inf), 13 significand bits are discarded, and the RNE
+// result needs the extra ulp exactly when those bits are 0x1000 with the kept LSB 0, i.e.
+// (bits & 0x3fff) == 0x1000 (inside [65520, 65536) the discarded bits are >= 0x3000, so inf
+// is never bumped).  Subnormal results, |value| >= 2^16, infinities and NaNs take
+// f2h_generic, on a branch the whole wave skips unless one of its lanes needs it.  Equal to
+// f2h_generic for all 2^32 inputs (tests/f2h_fast_model.c checks it exhaustively with a CPU
+// model of the hardware conversion).
+__device__ __forceinline__ uint16_t f2h_fast(float value) {
+  const uint32_t bits = __float_as_uint(value);
+  const uint32_t a = bits & 0x7fffffffu;
+  const bool common = a == 0u || a - 0x38800000u < 0x0f000000u;
+  uint32_t h = __builtin_bit_cast(uint16_t, (_Float16)value);
+  h += (bits & 0x3fffu) == 0x1000u ? 1u : 0u;
+  if (__builtin_amdgcn_ballot_w64(!common)) {
+    const uint32_t g = f2h_generic(value);
+    h = common ? h : g;
+  }
+  return (uint16_t)h;
 }
 
 // Exact widening; finite values and infinities match tensor.cpp:317-344 bit for bit.

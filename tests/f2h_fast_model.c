@@ -1,0 +1,72 @@
+/* CPU model of the device fp16 narrowings in mtorch_amd/csrc/common.h, checked over all 2^32
+ * float bit patterns: f2h_fast (short common path + generic fallback) must equal f2h_generic,
+ * and f2h_generic must equal mtorch's rounding (round to nearest, ties away from zero, overflow
+ * to inf, NaN keeping the top payload bits; tensor.cpp:276-315, restated in oracle/oracle.c).
+ * The hardware conversion v_cvt_f16_f32 rounds to nearest-even; F16C's _cvtss_sh with
+ * round-to-nearest is the same IEEE operation. */
+#include <immintrin.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <string.h>
+
+static inline uint32_t rne(uint32_t bits) {
+  float f;
+  memcpy(&f, &bits, 4);
+  return (uint32_t)_cvtss_sh(f, _MM_FROUND_TO_NEAREST_INT);
+}
+
+static uint32_t f2h_generic(uint32_t bits) {
+  const uint32_t raw = (bits >> 23) & 0xffu;
+  uint32_t h = rne(bits);
+  const int d = 126 - (int)raw;
+  const uint32_t sh = (uint32_t)(d < 13 ? 13 : (d > 24 ? 24 : d));
+  const uint32_t sig = (bits & 0x7fffffu) | 0x800000u;
+  const int tie_even = (sig & ((2u << sh) - 1u)) == (1u << (sh - 1u));
+  h += (raw - 102u <= 40u && tie_even) ? 1u : 0u;
+  const uint32_t payload = (bits & 0x7fffffu) >> 13;
+  const uint32_t nan_bits = ((bits >> 16) & 0x8000u) | 0x7c00u | (payload != 0u ? payload : 0x200u);
+  return (bits & 0x7fffffffu) > 0x7f800000u ? nan_bits : (h & 0xffffu);
+}
+
+static uint32_t f2h_fast(uint32_t bits) {
+  const uint32_t a = bits & 0x7fffffffu;
+  const int common = a == 0u || a - 0x38800000u < 0x0f000000u;
+  if (!common) return f2h_generic(bits);
+  return (rne(bits) + ((bits & 0x3fffu) == 0x1000u ? 1u : 0u)) & 0xffffu;
+}
+
+/* mtorch's scalar rule, written independently of the hardware conversion */
+static uint32_t f2h_reference(uint32_t bits) {
+  const uint32_t sign = (bits >> 16) & 0x8000u;
+  const uint32_t a = bits & 0x7fffffffu;
+  if (a > 0x7f800000u) {
+    const uint32_t payload = (bits & 0x7fffffu) >> 13;
+    return sign | 0x7c00u | (payload != 0u ? payload : 0x200u);
+  }
+  if (a == 0x7f800000u) return sign | 0x7c00u;
+  const int exponent = (int)(a >> 23) - 127 + 15;
+  uint32_t mantissa = a & 0x7fffffu;
+  if (exponent <= 0) {
+    if (exponent < -10) return sign;
+    mantissa |= 0x800000u;
+    const int shift = 14 - exponent;
+    uint32_t h = mantissa >> shift;
+    const uint32_t rem = mantissa & ((1u << shift) - 1u);
+    if (rem >= (1u << (shift - 1))) h += 1u; /* half or more: away from zero */
+    return sign | h;
+  }
+  uint32_t r = ((uint32_t)exponent << 10) + ((mantissa + 0x1000u) >> 13);
+  return sign | (r >= 0x7c00u ? 0x7c00u : r);
+}
+
+int main(void) {
+  uint64_t bad_fast = 0, bad_ref = 0;
+  for (uint64_t i = 0; i <= 0xffffffffull; ++i) {
+    const uint32_t b = (uint32_t)i;
+    const uint32_t g = f2h_generic(b);
+    if (f2h_fast(b) != g && bad_fast++ < 5) printf("fast %08x: %04x vs %04x\n", b, f2h_fast(b), g);
+    if (f2h_reference(b) != g && bad_ref++ < 5) printf("ref %08x: %04x vs %04x\n", b, f2h_reference(b), g);
+  }
+  printf("fast!=generic %llu, reference!=generic %llu\n", (unsigned long long)bad_fast, (unsigned long long)bad_ref);
+  return (bad_fast || bad_ref) ? 1 : 0;
+}
