@@ -96,7 +96,8 @@ int launch_tile(int device, GemmArgs a, int64_t batch, hipStream_t s) {
       // ceil(units / slots) rounds of ceil(nk / ksplit) K tiles, and every extra slice adds an
       // fp32 M x N write here plus its read in the reduction kernel.  (640 tiles on 768 slots
       // gain nothing from 2 slices -- 2 rounds of half the K -- and would pay the reduction.)
-      constexpr double kStepUs = 0.6, kReduceFixedUs = 3.0, kReduceBytesPerUs = 3.0e6;
+      constexpr double kStepUs = 0.6, kReduceBytesPerUs = 3.0e6;
+      const double kReduceFixedUs = env_flag("MTHIP_GEMM_REDUCE_US", 3);
       double best = 0.0;
       const int64_t max_split = std::min<int64_t>(16, nk / 8);
       for (int64_t ks = 1; ks <= max_split; ++ks) {

@@ -294,14 +294,15 @@ __global__ __launch_bounds__(256) void group_norm_apply_nhwc_kernel(const T* __r
   }
 }
 
-// fp16 SiLU of every half value, as the fused path computes it (SiLU of the narrowed
-// normalised value, narrowed again): the apply kernel looks the activation up by the fp16 bits
-// instead of evaluating expf and an IEEE divide per element.  Filled once per device.
+// fp16 SiLU of every half value (silu_half, the reference's fp16 SiLU bit for bit): the
+// channels-last apply kernel looks the activation of each narrowed normalised value up by its
+// bits, one gather where evaluating it costs ~20 vector instructions per element.  Filled once
+// per device.
 __device__ uint16_t g_silu_f16_table[65536];
 
 __global__ void silu_f16_table_kernel(uint16_t* tab) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < 65536) tab[i] = f2h_fast(apply_unary<uint16_t>(MTHIP_UNARY_SILU, h2f_bits((uint16_t)i)));
+  if (i < 65536) tab[i] = silu_half((uint16_t)i);
 }
 
 const uint16_t* silu_f16_table(int device, hipStream_t s) {

@@ -139,6 +139,16 @@ def test_activations(dt):
         assert rel(val(got), val(ref)) <= (2e-6 if dt == "float32" else 1e-3), name
 
 
+def test_silu_fp16_every_half_is_bit_exact():
+    """The fp16 SiLU (native 2^x and reciprocal with pinned exceptions) against the reference's
+    f2h(x / (1 + expf(-x))) on all 65536 half inputs, NaNs and infinities included."""
+    allh = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    got = host(F.silu(dev(allh)))
+    ref = orc.silu(allh)
+    bad = np.nonzero(got != ref)[0]
+    assert bad.size == 0, [(hex(i), hex(got[i]), hex(ref[i])) for i in bad[:8]]
+
+
 @pytest.mark.parametrize("dt", ["float32", "float16"])
 @pytest.mark.parametrize("M,N,K,bias", [(77, 64, 40, True), (300, 320, 96, True), (128, 128, 64, False), (8192, 2560, 320, True)])
 def test_linear_geglu_fused(dt, M, N, K, bias):
