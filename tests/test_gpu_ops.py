@@ -352,6 +352,37 @@ def test_split_k_paths(dt):
     assert rel(val(got), val(orc.addmm(inp, m1, m2, 0.5, 1.5))) <= TOL[dt]
 
 
+@pytest.mark.parametrize("tile", range(6))
+def test_direct_to_lds_tile_shapes(tile, monkeypatch):
+    """Every direct-to-LDS tile shape and stage count the launcher can pick (forced through
+    MTHIP_GEMM_DTL_TILE), on shapes with ragged M/N edges, a K tail, split K, the conv's padded
+    taps and channel edges, and the bias/residual/activation epilogues, against the oracle."""
+    monkeypatch.setenv("MTHIP_GEMM_DTL_TILE", str(tile))
+    g = Gen(90 + tile)
+    dt = "float16"
+    x = g.randn((203, 328), dt)  # K = 328: 5 whole K tiles and an 8-wide tail
+    w = g.randn((150, 328), dt, 1.0 / 18)
+    b = g.randn((150,), dt)
+    r = g.randn((203, 150), dt)
+    lin = orc.linear(x, w, b)
+    assert rel(val(host(F.linear(dev(x), dev(w), dev(b)))), val(lin)) <= TOL[dt]
+    got = host(F.linear_residual(dev(x), dev(w), dev(b), dev(r)))
+    assert rel(val(got), val(orc.binary(lin, r, "add"))) <= TOL[dt]
+    assert rel(val(host(F.linear_gelu(dev(x), dev(w), dev(b)))), val(orc.gelu(lin))) <= TOL[dt]
+    xl = g.randn((24, 3072), dt)  # long K, few tiles: split K
+    wl = g.randn((200, 3072), dt, 1.0 / 55)
+    assert rel(val(host(F.linear(dev(xl), dev(wl)))), val(orc.linear(xl, wl, None))) <= TOL[dt]
+    xc = g.randn((2, 128, 13, 11), dt)  # channel count a multiple of the K tile: fast im2col
+    wc = g.randn((136, 128, 3, 3), dt, 1.0 / 34)
+    bc = g.randn((136,), dt)
+    rc = g.randn((2, 136, 13, 11), dt)
+    got = host(F.conv2d_residual(dev(xc), dev(wc), dev(bc), dev(rc), padding=1))
+    ref = orc.binary(orc.conv2d(xc, wc, bc, padding=1), rc, "add")
+    assert rel(val(got), val(ref)) <= TOL[dt]
+    got = host(F.conv2d(dev(xc), dev(wc), dev(bc), stride=2, padding=1))
+    assert rel(val(got), val(orc.conv2d(xc, wc, bc, stride=2, padding=1))) <= TOL[dt]
+
+
 @pytest.mark.parametrize("dt", ["float32", "float16"])
 def test_conv2d_packed_weight_follows_inplace_writes(dt):
     """The packed weight cached on the weight's storage is rebuilt after copy_/fill_."""
