@@ -32,7 +32,9 @@ TileKind pick_tile(int MODE, int64_t M, int64_t N, int64_t batch) {
 
 // Tuning switches for sweeps: MTHIP_GEMM_SPLITK=0 disables K splitting, MTHIP_GEMM_PERSIST=0
 // launches one workgroup per unit, MTHIP_GEMM_XCD=0/1 forces the plain / XCD-contiguous unit
-// order (default: chosen per problem), MTHIP_GEMM_SPLIT_TARGET sets the split-K units per CU.
+// order (default: XCD-contiguous), MTHIP_GEMM_MFAST=0/1 forces which tile dimension varies
+// fastest (default: the one with fewer tiles), MTHIP_GEMM_SPLIT_TARGET sets the split-K units
+// per CU.
 int env_flag(const char* name, int dflt) {
   const char* e = std::getenv(name);
   return e ? std::atoi(e) : dflt;
@@ -133,11 +135,14 @@ int launch_tile(int device, GemmArgs a, int64_t batch, hipStream_t s) {
   }
   int64_t g = persist_enabled() ? std::min(a.units, slots) : a.units;
   if (g > 8 && g < a.units) g = g / 8 * 8;  // a multiple of 8 keeps each XCD on its own run of tiles
-  // Unit order and L2 reuse: dealt round-robin, XCD x sees output columns tn = x (mod 8) when
-  // tiles_n % 8 == 0 (so reads 1/8 of B and all of A); XCD-contiguous, it sees a band of rows
-  // (1/8 of A, all of B).  Take the smaller per-XCD footprint.
+  // Unit order and L2 reuse: each XCD takes a contiguous band of the operand with more tiles
+  // and walks all tiles of the other operand fastest, so it holds 1/8 of the large operand
+  // and all of the small one.  (Dealt round-robin instead, a conv's XCD would see every 8th
+  // pixel tile and fetch every 3x3 halo row from memory: 2.9x the operand bytes, measured.)
   const int xm = xcd_mode();
-  a.xcd_remap = xm == 0 ? 0 : xm == 1 ? 1 : (a.N < a.M || a.tiles_n % 8 != 0) ? 1 : 0;
+  a.xcd_remap = xm == 0 ? 0 : 1;
+  a.m_fast = a.tiles_m * batch <= a.tiles_n ? 1 : 0;
+  if (const char* f = std::getenv("MTHIP_GEMM_MFAST")) a.m_fast = std::atoi(f) != 0;
   void* ws = nullptr;
   if (a.ksplit > 1) {
     a.ld_partial = ceil_div(a.N, 4) * 4;

@@ -116,6 +116,7 @@ struct GemmArgs {
   // Divisors of the index arithmetic (units, pixels and N stay below 2^31).
   FastDiv div_tiles_n, div_tiles_m, div_ksplit, div_ohw, div_ow;
   int xcd_remap;  // 1: number units XCD-contiguously (see decode_unit)
+  int m_fast;     // 1: consecutive units walk the M tiles of one N tile (else the N tiles of one M tile)
   // EPI_GEGLU: gelu of every fp16 value (65536 entries, mtorch's fp16 gelu bit for bit)
   const uint16_t* gelu_tab;
   // EPI_CONV: per-(image, output channel) addend chan_add[img * chan_add_ld + row] (an SD
@@ -238,12 +239,23 @@ __device__ __forceinline__ GemmUnit decode_unit(const GemmArgs& args, uint32_t u
   // XCD-contiguous numbering: workgroups w = x (mod 8) run on XCD x and take units u = x (mod 8)
   // (the grid size is a multiple of 8).  Remapping q = (u % 8) * (U / 8) + u / 8 hands XCD x the
   // contiguous range [x*U/8, (x+1)*U/8) of tiles; the U % 8 tail keeps q = u (a bijection).
+  // Within the range the smaller tile dimension varies fastest (m_fast when M has fewer tiles),
+  // so an XCD holds a band of the large operand and all of the small one in its L2, and a
+  // conv's neighbouring pixel tiles, which share 3x3 halo rows, run on the same XCD.
   const uint32_t U = (uint32_t)args.units, U8 = U / 8;
   const uint32_t q = (args.xcd_remap && u < 8 * U8) ? (u % 8) * U8 + u / 8 : u;
-  const uint32_t t1 = args.div_tiles_n.div(q);
-  const uint32_t tn = q - t1 * args.div_tiles_n.d;
-  const uint32_t t2 = args.div_tiles_m.div(t1);
-  const uint32_t tm = t1 - t2 * args.div_tiles_m.d;
+  uint32_t tm, tn, t2;
+  if (args.m_fast) {
+    const uint32_t t1 = args.div_tiles_m.div(q);
+    tm = q - t1 * args.div_tiles_m.d;
+    t2 = args.div_tiles_n.div(t1);
+    tn = t1 - t2 * args.div_tiles_n.d;
+  } else {
+    const uint32_t t1 = args.div_tiles_n.div(q);
+    tn = q - t1 * args.div_tiles_n.d;
+    t2 = args.div_tiles_m.div(t1);
+    tm = t1 - t2 * args.div_tiles_m.d;
+  }
   const uint32_t bz = args.div_ksplit.div(t2);
   GemmUnit un;
   un.split = t2 - bz * args.div_ksplit.d;
