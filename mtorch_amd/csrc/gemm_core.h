@@ -151,6 +151,96 @@ __device__ __forceinline__ void store_cols(T* p, const float (&v)[4], int nv) {
   }
 }
 
+// Reads the first nv (1..4) of 4 consecutive elements as floats (0 past nv); one 8-byte (fp16)
+// or 16-byte (fp32) load when all four are valid and aligned.
+template <typename T>
+__device__ __forceinline__ void load_cols(const T* p, float (&o)[4], int nv) {
+  if constexpr (sizeof(T) == 2) {
+    if (nv == 4 && ((uintptr_t)p & 7) == 0) {
+      const uint2 u = *reinterpret_cast<const uint2*>(p);
+      o[0] = h2f_bits((uint16_t)(u.x & 0xffffu));
+      o[1] = h2f_bits((uint16_t)(u.x >> 16));
+      o[2] = h2f_bits((uint16_t)(u.y & 0xffffu));
+      o[3] = h2f_bits((uint16_t)(u.y >> 16));
+      return;
+    }
+  } else {
+    if (nv == 4 && ((uintptr_t)p & 15) == 0) {
+      const float4 u = *reinterpret_cast<const float4*>(p);
+      o[0] = u.x;
+      o[1] = u.y;
+      o[2] = u.z;
+      o[3] = u.w;
+      return;
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < 4; ++t) o[t] = t < nv ? Elem<T>::load(p, t) : 0.0f;
+}
+
+// Four consecutive stored elements, read with one 8-byte (fp16) or 16-byte (fp32) load and kept
+// packed until used.
+template <typename T>
+struct Raw4;
+template <>
+struct Raw4<uint16_t> {
+  uint2 u;
+  __device__ __forceinline__ float at(int t) const {
+    const uint32_t w = t < 2 ? u.x : u.y;
+    return h2f_bits((uint16_t)((t & 1) ? (w >> 16) : (w & 0xffffu)));
+  }
+};
+template <>
+struct Raw4<float> {
+  float4 u;
+  __device__ __forceinline__ float at(int t) const { return t == 0 ? u.x : t == 1 ? u.y : t == 2 ? u.z : u.w; }
+};
+// p must be aligned to the load (8 bytes for fp16, 16 for fp32).
+template <typename T>
+__device__ __forceinline__ Raw4<T> load_raw4(const T* p) {
+  Raw4<T> r;
+  if constexpr (sizeof(T) == 2) {
+    r.u = *reinterpret_cast<const uint2*>(p);
+  } else {
+    r.u = *reinterpret_cast<const float4*>(p);
+  }
+  return r;
+}
+
+// The epilogue arithmetic on operands already read: b is the per-column bias (EPI_LINEAR) or
+// the row's bias in every slot (EPI_CONV, 0 without a bias), av the channel addend (EPI_CONV),
+// r the residual.  Values are narrowed once, except where a fused activation or residual needs
+// the narrowed intermediate that the unfused op sequence would have produced.
+template <typename T, int EPI, int ACT>
+__device__ __forceinline__ void epi_math(float (&v)[4], const float (&b)[4], bool has_b, float av, bool has_av,
+                                         const float (&r)[4], bool has_r) {
+  if constexpr (EPI == EPI_LINEAR) {
+    if (has_b) {
+#pragma unroll
+      for (int t = 0; t < 4; ++t) v[t] += b[t];
+    }
+    if (ACT != MTHIP_ACT_NONE || has_r) {
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        float x = Elem<T>::round_trip(v[t]);
+        if constexpr (ACT != MTHIP_ACT_NONE) x = apply_act<T>(ACT, x);
+        if (has_r) x = Elem<T>::round_trip(x) + r[t];
+        v[t] = x;
+      }
+    }
+  } else if constexpr (EPI == EPI_CONV) {
+    // conv + bias, then (+ chan_add), then (+ residual), each add narrowed as the unfused op
+    // sequence narrows it
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      float x = v[t] + b[t];
+      if (has_av) x = Elem<T>::round_trip(x) + av;
+      if (has_r) x = Elem<T>::round_trip(x) + r[t];
+      v[t] = x;
+    }
+  }
+}
+
 // Epilogue for C[row][col0 .. col0+3] of batch bz (row < M checked by the caller; columns
 // past N are skipped).  v holds the fp32 dot products.  Values are narrowed once, except where
 // a fused activation or residual needs the narrowed intermediate that the unfused op sequence
@@ -164,19 +254,10 @@ __device__ __forceinline__ void emit4(const GemmArgs& args, int64_t bz, int row,
   if constexpr (EPI == EPI_LINEAR) {
     const T* bias = reinterpret_cast<const T*>(args.bias);
     const T* res = args.residual ? reinterpret_cast<const T*>(args.residual) + (int64_t)row * args.ld_res : nullptr;
-    if (bias) {
-#pragma unroll
-      for (int t = 0; t < 4; ++t) v[t] += t < nv ? Elem<T>::load(bias, col0 + t) : 0.0f;
-    }
-    if (ACT != MTHIP_ACT_NONE || res) {
-#pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        float x = Elem<T>::round_trip(v[t]);
-        if constexpr (ACT != MTHIP_ACT_NONE) x = apply_act<T>(ACT, x);
-        if (res) x = Elem<T>::round_trip(x) + (t < nv ? Elem<T>::load(res, col0 + t) : 0.0f);
-        v[t] = x;
-      }
-    }
+    float b[4] = {0.0f, 0.0f, 0.0f, 0.0f}, r[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (bias) load_cols<T>(bias + col0, b, nv);
+    if (res) load_cols<T>(res + col0, r, nv);
+    epi_math<T, EPI, ACT>(v, b, bias != nullptr, 0.0f, false, r, res != nullptr);
     store_cols<T>(Cptr + (int64_t)row * args.ldc + col0, v, nv);
   } else if constexpr (EPI == EPI_GEMM) {
     const T* cin = reinterpret_cast<const T*>(args.c_in);
@@ -197,20 +278,15 @@ __device__ __forceinline__ void emit4(const GemmArgs& args, int64_t bz, int row,
     const T* res = reinterpret_cast<const T*>(args.residual);
     const T* cadd = reinterpret_cast<const T*>(args.chan_add);
     const float bv = bias ? Elem<T>::load(bias, row) : 0.0f;
-    // conv + bias, then (+ chan_add), then (+ residual), each add narrowed as the unfused op
-    // sequence narrows it
     if (OHW % 4 == 0) {
       // col0 is a multiple of 4, so the 4 pixels lie in one image and are contiguous.
       const int img = (int)args.div_ohw.div((uint32_t)col0);
       const int64_t addr = ((int64_t)img * M + row) * OHW + (col0 - img * OHW);
       const float av = cadd ? Elem<T>::load(cadd, img * args.chan_add_ld + row) : 0.0f;
-#pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        float x = v[t] + bv;
-        if (cadd) x = Elem<T>::round_trip(x) + av;
-        if (res) x = Elem<T>::round_trip(x) + (t < nv ? Elem<T>::load(res, addr + t) : 0.0f);
-        v[t] = x;
-      }
+      const float b[4] = {bv, bv, bv, bv};
+      float r[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+      if (res) load_cols<T>(res + addr, r, nv);
+      epi_math<T, EPI, ACT>(v, b, true, av, cadd != nullptr, r, res != nullptr);
       store_cols<T>(Cptr + addr, v, nv);
     } else {
       for (int t = 0; t < nv; ++t) {
@@ -269,10 +345,37 @@ __device__ __forceinline__ GemmUnit decode_unit(const GemmArgs& args, uint32_t u
   return un;
 }
 
+// Whether a unit's EPI_LINEAR / EPI_CONV epilogue can take the straight-line path: every column
+// of the tile exists, bias and residual rows are aligned to 4-element loads and (conv) the tile's
+// pixels lie in one image.  The test is uniform across the workgroup.
+template <typename T, int EPI, int BN>
+__device__ __forceinline__ bool epi_tile_fast(const GemmArgs& args, const GemmUnit& un) {
+  constexpr uintptr_t kAlign = sizeof(T) == 2 ? 7 : 15;
+  if (un.n0 + BN > args.N) return false;
+  if constexpr (EPI == EPI_LINEAR) {
+    if (args.bias && ((uintptr_t)args.bias & kAlign)) return false;
+    if (args.residual && (((uintptr_t)args.residual & kAlign) || (args.ld_res & 3))) return false;
+    return true;
+  } else if constexpr (EPI == EPI_CONV) {
+    const int64_t OHW = args.OH * args.OW;
+    if (OHW % 4) return false;
+    if (args.div_ohw.div((uint32_t)un.n0) != args.div_ohw.div((uint32_t)(un.n0 + BN - 1))) return false;
+    if (args.residual && ((uintptr_t)args.residual & kAlign)) return false;
+    return true;
+  } else {
+    return false;
+  }
+}
+
 // Epilogue of one unit.  Fragment (i, j), register r of lane l holds
 //   C[row][col], row = m0 + wm*WM + i*32 + l%32,
 //   col = n0 + wn*WN + j*32 + 8*(r/4) + 4*(l/32) + r%4     (4 consecutive cols per r/4),
 // with (wm, wn) the wave's position in the workgroup's WGM x (4/WGM) grid of wave tiles.
+//
+// Every read of an epilogue is issued before its first use.  A load's result is waited for
+// where it is used and the wait counter drains in issue order, behind the next unit's operand
+// loads already in flight: reads interleaved with their uses would each pay that wait, reads
+// issued together share one.
 template <typename T, int BM, int BN, int WGM, int EPI, int ACT, int FM, int FN>
 __device__ __forceinline__ void gemm_finish_unit(const GemmArgs& args, const GemmUnit& un, floatx16 (&acc)[FM][FN],
                                                  int lane, int wm, int wn) {
@@ -285,33 +388,84 @@ __device__ __forceinline__ void gemm_finish_unit(const GemmArgs& args, const Gem
     // B rows come interleaved in 32-row blocks (values, then the matching gates), and each
     // wave owns 64 columns = fragment 0 (values) + fragment 1 (gates) of 32 output columns:
     // out[row][col] = value * gelu(gate), each factor narrowed as the unfused
-    // linear -> chunk -> gelu -> mul sequence narrows it.
+    // linear -> chunk -> gelu -> mul sequence narrows it.  N is a multiple of 64 (the launcher
+    // requires 32 output columns per block), so all 64 columns of a tile exist.
     static_assert(FN == 2 && WGN == 1 && BN == 64, "GEGLU epilogue pairs two 32-column fragments");
     const T* bias = reinterpret_cast<const T*>(args.bias);
     T* Cp = reinterpret_cast<T*>(args.c);
     const int Nout = (int)args.N / 2;
+    const bool has_b = bias != nullptr;
+    float bval[4][4], bgate[4][4];
+    if (has_b && ((uintptr_t)bias & (sizeof(T) == 2 ? 7 : 15)) == 0) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int pc = (int)un.n0 + 8 * g + lane_col;  // permuted column of the value
+        const Raw4<T> bv = load_raw4<T>(bias + pc), bg = load_raw4<T>(bias + pc + 32);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          bval[g][t] = bv.at(t);
+          bgate[g][t] = bg.at(t);
+        }
+      }
+    } else if (has_b) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int pc = (int)un.n0 + 8 * g + lane_col;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          bval[g][t] = Elem<T>::load(bias, pc + t);
+          bgate[g][t] = Elem<T>::load(bias, pc + 32 + t);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+#pragma unroll
+        for (int t = 0; t < 4; ++t) bval[g][t] = bgate[g][t] = 0.0f;
+    }
 #pragma unroll
     for (int i = 0; i < FM; ++i) {
       const int row = (int)un.m0 + wm * WM + i * 32 + (lane & 31);
+      float gl[4][4];
+      if constexpr (sizeof(T) == 2) {
+        // the gates' fp16 values, then all 16 table reads, then the first use
+        uint32_t gh[4][4];
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            float gate = acc[i][1][4 * g + t];
+            if (has_b) gate += bgate[g][t];
+            gh[g][t] = f2h_fast(gate);
+          }
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+#pragma unroll
+          for (int t = 0; t < 4; ++t) gl[g][t] = h2f_bits(args.gelu_tab[gh[g][t]]);
+      } else {
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            float gate = acc[i][1][4 * g + t];
+            if (has_b) gate += bgate[g][t];
+            gl[g][t] = gelu_ref_f32(gate);
+          }
+      }
       if (row < M) {
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
-          const int pc = (int)un.n0 + 8 * g + lane_col;  // permuted column of the value
           const int col0 = (int)un.n0 / 2 + 8 * g + lane_col;
           if (col0 < Nout) {
             float v[4];
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
-              float val = acc[i][0][4 * g + t], gate = acc[i][1][4 * g + t];
-              if (bias) {
-                val += Elem<T>::load(bias, pc + t);
-                gate += Elem<T>::load(bias, pc + 32 + t);
-              }
+              float val = acc[i][0][4 * g + t];
+              if (has_b) val += bval[g][t];
               if constexpr (sizeof(T) == 2) {
-                const float gl = h2f_bits(args.gelu_tab[f2h_fast(gate)]);
-                v[t] = h2f_bits(f2h_fast(val)) * gl;
+                v[t] = h2f_bits(f2h_fast(val)) * gl[g][t];
               } else {
-                v[t] = val * gelu_ref_f32(gate);
+                v[t] = val * gl[g][t];
               }
             }
             store_cols<T>(Cp + (int64_t)row * args.ldc + col0, v, Nout - col0 < 4 ? Nout - col0 : 4);
@@ -321,26 +475,126 @@ __device__ __forceinline__ void gemm_finish_unit(const GemmArgs& args, const Gem
     }
     return;
   }
+  if (args.ksplit > 1) {
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+      const int row = (int)un.m0 + wm * WM + i * 32 + (lane & 31);
+      if (row < M) {
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            const int col0 = (int)un.n0 + wn * WN + j * 32 + 8 * g + lane_col;
+            if (col0 < (int)args.N)
+              *reinterpret_cast<float4*>(args.partial + (un.split * args.M + row) * args.ld_partial + col0) =
+                  make_float4(acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]);
+          }
+      }
+    }
+    return;
+  }
+  if constexpr (EPI == EPI_LINEAR || EPI == EPI_CONV) {
+    if (epi_tile_fast<T, EPI, BN>(args, un)) {
+      const T* bias = reinterpret_cast<const T*>(args.bias);
+      const T* res = reinterpret_cast<const T*>(args.residual);
+      T* Cptr = reinterpret_cast<T*>(args.c);
+      const bool has_b = bias != nullptr, has_r = res != nullptr;
+      const int col_base = (int)un.n0 + wn * WN + lane_col;  // + j*32 + 8*g
+      int rows[FM], rrows[FM];  // rows, and rows clamped into the matrix for the reads
+#pragma unroll
+      for (int i = 0; i < FM; ++i) {
+        rows[i] = (int)un.m0 + wm * WM + i * 32 + (lane & 31);
+        rrows[i] = rows[i] < M ? rows[i] : M - 1;
+      }
+      Raw4<T> rz[FM][FN][4] = {};
+      if constexpr (EPI == EPI_LINEAR) {
+        Raw4<T> bz[FN][4] = {};
+        if (has_b) {
+#pragma unroll
+          for (int j = 0; j < FN; ++j)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) bz[j][g] = load_raw4<T>(bias + col_base + j * 32 + 8 * g);
+        }
+        if (has_r) {
+#pragma unroll
+          for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int j = 0; j < FN; ++j)
+#pragma unroll
+              for (int g = 0; g < 4; ++g)
+                rz[i][j][g] = load_raw4<T>(res + (int64_t)rrows[i] * args.ld_res + col_base + j * 32 + 8 * g);
+        }
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+          for (int j = 0; j < FN; ++j)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+              float v[4], b[4], r[4];
+#pragma unroll
+              for (int t = 0; t < 4; ++t) {
+                v[t] = acc[i][j][4 * g + t];
+                b[t] = bz[j][g].at(t);
+                r[t] = rz[i][j][g].at(t);
+              }
+              epi_math<T, EPI, ACT>(v, b, has_b, 0.0f, false, r, has_r);
+              if (rows[i] < M) store_cols<T>(Cptr + (int64_t)rows[i] * args.ldc + col_base + j * 32 + 8 * g, v, 4);
+            }
+      } else {
+        // conv: row = output channel, col = output pixel; the tile lies in image img (NCHW store)
+        const T* cadd = reinterpret_cast<const T*>(args.chan_add);
+        const int OHW = (int)(args.OH * args.OW);
+        const int img = (int)args.div_ohw.div((uint32_t)un.n0);
+        const int pix_base = col_base - img * OHW;
+        float bv[FM], av[FM];
+#pragma unroll
+        for (int i = 0; i < FM; ++i) {
+          bv[i] = has_b ? Elem<T>::load(bias, rrows[i]) : 0.0f;
+          av[i] = cadd ? Elem<T>::load(cadd, img * args.chan_add_ld + rrows[i]) : 0.0f;
+        }
+        if (has_r) {
+#pragma unroll
+          for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int j = 0; j < FN; ++j)
+#pragma unroll
+              for (int g = 0; g < 4; ++g)
+                rz[i][j][g] = load_raw4<T>(res + ((int64_t)img * M + rrows[i]) * OHW + pix_base + j * 32 + 8 * g);
+        }
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+          for (int j = 0; j < FN; ++j)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+              float v[4], r[4];
+              const float b[4] = {bv[i], bv[i], bv[i], bv[i]};
+#pragma unroll
+              for (int t = 0; t < 4; ++t) {
+                v[t] = acc[i][j][4 * g + t];
+                r[t] = rz[i][j][g].at(t);
+              }
+              epi_math<T, EPI, ACT>(v, b, true, av[i], cadd != nullptr, r, has_r);
+              if (rows[i] < M)
+                store_cols<T>(Cptr + ((int64_t)img * M + rows[i]) * OHW + pix_base + j * 32 + 8 * g, v, 4);
+            }
+      }
+      return;
+    }
+  }
 #pragma unroll
   for (int i = 0; i < FM; ++i) {
     const int row = (int)un.m0 + wm * WM + i * 32 + (lane & 31);
-    const bool row_ok = row < M;
+    if (row < M) {
 #pragma unroll
-    for (int j = 0; j < FN; ++j) {
+      for (int j = 0; j < FN; ++j) {
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int col0 = (int)un.n0 + wn * WN + j * 32 + 8 * g + lane_col;
-        float v[4];
+        for (int g = 0; g < 4; ++g) {
+          const int col0 = (int)un.n0 + wn * WN + j * 32 + 8 * g + lane_col;
+          float v[4];
 #pragma unroll
-        for (int t = 0; t < 4; ++t) v[t] = acc[i][j][4 * g + t];
-        if (row_ok) {
-          if (args.ksplit > 1) {
-            if (col0 < (int)args.N)
-              *reinterpret_cast<float4*>(args.partial + (un.split * args.M + row) * args.ld_partial + col0) =
-                  make_float4(v[0], v[1], v[2], v[3]);
-          } else {
-            emit4<T, EPI, ACT>(args, un.bz, row, col0, v);
-          }
+          for (int t = 0; t < 4; ++t) v[t] = acc[i][j][4 * g + t];
+          emit4<T, EPI, ACT>(args, un.bz, row, col0, v);
         }
       }
     }
