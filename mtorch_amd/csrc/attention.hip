@@ -7,9 +7,10 @@
 // of query (l % 32) against 16 keys: a query's online-softmax max/sum is an in-register
 // reduction plus one exchange with lane l^32.  Those accumulator registers, converted to fp16,
 // are exactly the B operand of O^T += V^T . P^T (register r <-> key 8*(r/4) + 4*(l/32) + r%4 in
-// both products), so P never leaves registers.  K is staged in LDS row-major and V transposed
-// (keys contiguous); the next tile's K/V are fetched into registers with 16-byte range-checked
-// buffer loads while the current tile is multiplied.  Scores are kept in log2 units
+// both products), so P never leaves registers.  K and V are staged in LDS row-major with
+// 16-byte writes; the V^T operand of the PV product comes out of LDS through gfx950's
+// transposing read (ds_read_b64_tr_b16).  The next tile's K/V are fetched into registers with
+// 16-byte range-checked buffer loads while the current tile is multiplied.  Scores are kept in log2 units
 // (scale * log2 e folded in) so the exponentials are single v_exp_f32.  Softmax statistics and
 // the output accumulator are fp32; fully masked rows end as 0/0 = NaN, as the reference's
 // softmax of an all -inf row does (tensor.cpp:30429-30442).
@@ -58,27 +59,49 @@ __device__ __forceinline__ uint4 bload(const __amdgpu_buffer_rsrc_t& r, uint32_t
 
 constexpr uint32_t kOOB = 0x80000000u;
 
+typedef short shortx4 __attribute__((ext_vector_type(4)));
+
+// ds_read_b64_tr_b16: lane j of each 16-lane group receives halves [j%4] of the 8-byte rows read
+// by lanes j/4, j/4+4, j/4+8 and j/4+12 of the group (p points into LDS).
+__device__ __forceinline__ halfx4 tr_read16(const uint16_t* p) {
+  return __builtin_bit_cast(halfx4, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                                        (__attribute__((address_space(3))) shortx4*)(const_cast<uint16_t*>(p))));
+}
+
 // DK: head dim padded to a multiple of 16 (QK^T K-steps); the value dim is covered by
 // DVB = ceil(DK/32) 32-row blocks.  VEC: E and Ev are multiples of 8 and every row stride a
 // multiple of 8 elements with 16-byte aligned bases, so K/V/Q move in 16-byte chunks.
 // MASK: the mask kind (MTHIP_MASK_*) fixed at compile time, or -1 to read it at run time.
-// WAVES: wave64s per workgroup (32 queries each).
-template <int DK, bool VEC, int MASK, int WAVES>
-__global__ __launch_bounds__(64 * WAVES) void flash_fwd_f16_kernel(const FlashArgs a) {
-  constexpr int NT = 64 * WAVES;
+// WAVES: query waves per workgroup (32 queries each).  KG: key groups -- KG sets of WAVES
+// waves take the same queries and alternate 64-key tiles (group g the tiles g, g+KG, ...),
+// each with its own LDS tile and online softmax; at the end group 0 folds in the others'
+// (max, sum, accumulator).  KG = 2 doubles the waves per SIMD on the large self-attentions,
+// where one wave's chain (score MFMAs -> softmax VALU -> PV MFMAs) would otherwise leave the
+// MFMA and VALU pipes idle.
+template <int DK, bool VEC, int MASK, int WAVES, int KG = 1>
+__global__ __launch_bounds__(64 * WAVES * KG) __attribute__((amdgpu_waves_per_eu(KG > 1 ? 4 : 1)))
+void flash_fwd_f16_kernel(const FlashArgs a) {
+  constexpr int NT = 64 * WAVES;  // threads of one key group
   constexpr int NSTEP = DK / 16;
   constexpr int DVB = (DK + 31) / 32;
   constexpr int BKV = 64;
   constexpr int KP = DK + 8;    // LDS pitch of the K tile (halves)
-  constexpr int VP = BKV + 8;   // LDS pitch of the transposed V tile (halves)
+  constexpr int VRP = DVB * 32 + 8;  // LDS pitch of a V row (halves; 16-byte multiple)
   constexpr int KCHR = DK / 8;  // 16-byte chunks per K row
   constexpr int VCHR = DVB * 4; // 16-byte chunks per V row (DVB*32 dims)
   constexpr int KCH = (BKV * KCHR + NT - 1) / NT;
   constexpr int VCH = (BKV * VCHR + NT - 1) / NT;
-  __shared__ __align__(16) uint16_t Ks[BKV * KP];
-  __shared__ __align__(16) uint16_t Vt[DVB * 32 * VP];
+  static_assert(KG == 1 || KG == 2, "one or two key groups");
+  // One K/V tile per key group; after the key loop the same memory holds the group merge (one
+  // lane's (max, sum) or 16 accumulator values, pitch 17 floats).
+  constexpr int TILE = BKV * KP + BKV * VRP;  // halves of one K tile + V tile (16-byte multiple)
+  constexpr int XCH = KG > 1 ? NT * 17 * 2 : 0;  // halves of the merge buffer
+  __shared__ __align__(16) uint16_t smem[KG * TILE > XCH ? KG * TILE : XCH];
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int grp = KG > 1 ? __builtin_amdgcn_readfirstlane((int)(threadIdx.x / NT)) : 0;  // wave-uniform
+  const int tid = (int)threadIdx.x - grp * NT, lane = tid & 63, wave = tid >> 6;
+  uint16_t* const Ks = smem + grp * TILE;
+  uint16_t* const Vr = Ks + BKV * KP;
   const int hh = lane >> 5, col = lane & 31;
   const int64_t bh = blockIdx.y;
   const int64_t b = bh / a.H, head = bh - b * a.H;
@@ -123,8 +146,8 @@ __global__ __launch_bounds__(64 * WAVES) void flash_fwd_f16_kernel(const FlashAr
         const bool ok = c < BKV * KCHR && kv0 + key < Lk && d0 < E;
         kreg[i] = bload(k_rsrc, ok ? (uint32_t)(((int64_t)(kv0 + key) * a.ks[2] + d0) * 2) : kOOB);
       }
-      // V chunks go key-fastest across lanes so the transposed LDS writes below hit
-      // consecutive addresses (d-fastest lanes would land 2*VP bytes apart: same banks).
+      // V chunks go key-fastest across lanes: consecutive rows of pitch VRP put 16 lanes'
+      // 16-byte writes on distinct banks.
 #pragma unroll
       for (int i = 0; i < VCH; ++i) {
         const int c = tid + i * NT;
@@ -144,13 +167,7 @@ __global__ __launch_bounds__(64 * WAVES) void flash_fwd_f16_kernel(const FlashAr
 #pragma unroll
       for (int i = 0; i < VCH; ++i) {
         const int c = tid + i * NT;
-        if (c < BKV * VCHR) {
-          const int key = c % BKV, d0 = (c / BKV) * 8;
-          uint16_t h[8];
-          __builtin_memcpy(h, &vreg[i], 16);
-#pragma unroll
-          for (int j = 0; j < 8; ++j) Vt[(d0 + j) * VP + key] = h[j];
-        }
+        if (c < BKV * VCHR) *reinterpret_cast<uint4*>(&Vr[(c % BKV) * VRP + (c / BKV) * 8]) = vreg[i];
       }
     } else {
       for (int idx = tid; idx < BKV * DK; idx += NT) {
@@ -163,7 +180,7 @@ __global__ __launch_bounds__(64 * WAVES) void flash_fwd_f16_kernel(const FlashAr
         const int key = idx / (DVB * 32), d = idx - key * (DVB * 32);
         uint16_t bits = 0;
         if (kv0 + key < Lk && d < Ev) bits = V[(int64_t)(kv0 + key) * a.vs[2] + d];
-        Vt[d * VP + key] = bits;
+        Vr[key * VRP + d] = bits;
       }
     }
   };
@@ -193,12 +210,15 @@ __global__ __launch_bounds__(64 * WAVES) void flash_fwd_f16_kernel(const FlashAr
       mrow_f = reinterpret_cast<const float*>(a.mask) + off;
   }
 
-  fetch(0);
-  for (int kv0 = 0; kv0 < Lk; kv0 += BKV) {
+  fetch(grp * BKV);
+  const int iters = (Lk + BKV * KG - 1) / (BKV * KG);
+  for (int it = 0; it < iters; ++it) {
+    const int kv0 = (it * KG + grp) * BKV;
     __syncthreads();  // every wave is done with the previous tile
     stage(kv0);
     __syncthreads();
-    if (kv0 + BKV < Lk) fetch(kv0 + BKV);  // next tile's loads overlap this tile's math
+    if (kv0 + KG * BKV < Lk) fetch(kv0 + KG * BKV);  // next tile's loads overlap this tile's math
+    if (KG > 1 && kv0 >= Lk) continue;  // a key group past the last tile only keeps the barriers
 
     // Raw scores (unscaled; an additive mask enters divided by the scale) and their max.
     float s[2][16];
@@ -276,14 +296,54 @@ __global__ __launch_bounds__(64 * WAVES) void flash_fwd_f16_kernel(const FlashAr
         for (int j = 0; j < 8; ++j) pf[j] = (_Float16)s[sb][st * 8 + j];
 #pragma unroll
         for (int i = 0; i < DVB; ++i) {
-          const uint16_t* vrow = &Vt[(i * 32 + col) * VP + sb * 32 + st * 16 + hh * 4];
-          const halfx4 lo = *reinterpret_cast<const halfx4*>(vrow);
-          const halfx4 hi = *reinterpret_cast<const halfx4*>(vrow + 8);
+          // Lane l needs V[k][i*32 + l%32] for keys k = K0+0..3 and K0+8..11, K0 = sb*32 +
+          // st*16 + 4*(l/32).  In each 16-lane group the transposing read hands lane j the
+          // halves [j%4] of the rows read by lanes j/4, j/4+4, j/4+8, j/4+12; so lane r of
+          // the group points at key K0 + r/4, dims 16*((l/16)%2) + 4*(r%4) .. +3.
+          const uint16_t* v0 = &Vr[(sb * 32 + st * 16 + hh * 4 + ((lane & 15) >> 2)) * VRP + i * 32 +
+                                   16 * ((lane >> 4) & 1) + 4 * (lane & 3)];
+          const halfx4 lo = tr_read16(v0);
+          const halfx4 hi = tr_read16(v0 + 8 * VRP);
           const halfx8 vf = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
           acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf, acc[i], 0, 0, 0);
         }
       }
     }
+  }
+
+  if constexpr (KG > 1) {
+    // Fold group 1's (max, sum, accumulator) into group 0: the same lane of both groups holds
+    // the same query and the same output dims.  A group that saw no key (or only masked ones)
+    // has max -inf and contributes nothing; if neither saw one, the sum stays 0 (NaN output).
+    float* xl = reinterpret_cast<float*>(smem) + tid * 17;
+    __syncthreads();  // every wave is done with the last tile
+    if (grp == 1) {
+      xl[0] = m_run;
+      xl[1] = l_run;
+    }
+    __syncthreads();
+    float a0 = 1.0f, a1 = 0.0f;
+    if (grp == 0) {
+      const float m1 = xl[0], l1 = xl[1];
+      const float m = fmaxf(m_run, m1);
+      a0 = m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m_run - m);
+      a1 = m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m1 - m);
+      l_run = l_run * a0 + l1 * a1;
+    }
+#pragma unroll
+    for (int i = 0; i < DVB; ++i) {
+      __syncthreads();
+      if (grp == 1) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) xl[r] = acc[i][r];
+      }
+      __syncthreads();
+      if (grp == 0) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[i][r] = acc[i][r] * a0 + xl[r] * a1;
+      }
+    }
+    if (grp != 0) return;
   }
 
   if (!qok) return;
@@ -362,18 +422,18 @@ __global__ __launch_bounds__(256) void attention_rowwise_kernel(const FlashArgs 
   }
 }
 
-template <int DK, int WAVES>
+template <int DK, int WAVES, int KG>
 void launch_flash_w(const FlashArgs& a, int64_t bh, hipStream_t s, bool vec) {
   const dim3 grid((unsigned)ceil_div(a.Lq, 32 * WAVES), (unsigned)bh);
-  const dim3 block(64 * WAVES);
+  const dim3 block(64 * WAVES * KG);
   if (!vec) {
-    hipLaunchKernelGGL((flash_fwd_f16_kernel<DK, false, -1, WAVES>), grid, block, 0, s, a);
+    hipLaunchKernelGGL((flash_fwd_f16_kernel<DK, false, -1, WAVES, KG>), grid, block, 0, s, a);
   } else if (a.mask_kind == MTHIP_MASK_NONE) {
-    hipLaunchKernelGGL((flash_fwd_f16_kernel<DK, true, MTHIP_MASK_NONE, WAVES>), grid, block, 0, s, a);
+    hipLaunchKernelGGL((flash_fwd_f16_kernel<DK, true, MTHIP_MASK_NONE, WAVES, KG>), grid, block, 0, s, a);
   } else if (a.mask_kind == MTHIP_MASK_BOOL) {
-    hipLaunchKernelGGL((flash_fwd_f16_kernel<DK, true, MTHIP_MASK_BOOL, WAVES>), grid, block, 0, s, a);
+    hipLaunchKernelGGL((flash_fwd_f16_kernel<DK, true, MTHIP_MASK_BOOL, WAVES, KG>), grid, block, 0, s, a);
   } else {
-    hipLaunchKernelGGL((flash_fwd_f16_kernel<DK, true, MTHIP_MASK_ADD, WAVES>), grid, block, 0, s, a);
+    hipLaunchKernelGGL((flash_fwd_f16_kernel<DK, true, MTHIP_MASK_ADD, WAVES, KG>), grid, block, 0, s, a);
   }
 }
 
@@ -382,7 +442,17 @@ void launch_flash_w(const FlashArgs& a, int64_t bh, hipStream_t s, bool vec) {
 // idle: each wave then stages a quarter of the K/V tile, and the shared tile serves 128 queries.
 template <int DK>
 void launch_flash(const FlashArgs& a, int64_t bh, hipStream_t s, bool vec) {
-  launch_flash_w<DK, 4>(a, bh, s, vec);
+  // Two key groups (8 waves) for small heads over long key sequences, where the extra waves per
+  // SIMD hide the score -> softmax -> PV chain (SD self-attention at 64x64: -6 %); with few
+  // keys (cross-attention on 77 tokens) the merge costs more than it saves.
+  if constexpr (DK <= 48) {
+    if (a.Lk >= 1024 && vec && a.mask_kind == MTHIP_MASK_NONE) {
+      hipLaunchKernelGGL((flash_fwd_f16_kernel<DK, true, MTHIP_MASK_NONE, 4, 2>),
+                         dim3((unsigned)ceil_div(a.Lq, 128), (unsigned)bh), dim3(512), 0, s, a);
+      return;
+    }
+  }
+  launch_flash_w<DK, 4, 1>(a, bh, s, vec);
 }
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }

@@ -416,8 +416,11 @@ def test_conv2d_residual_epilogue(dt):
 
 
 @pytest.mark.parametrize("dt", ["float16", "float32"])
-@pytest.mark.parametrize("Lq,Lk,E", [(256, 256, 40), (300, 77, 40), (130, 130, 80), (64, 200, 160), (33, 17, 64), (5, 9, 7)])
+@pytest.mark.parametrize("Lq,Lk,E", [(256, 256, 40), (300, 77, 40), (130, 130, 80), (64, 200, 160), (33, 17, 64), (5, 9, 7),
+                                     (200, 1100, 40), (96, 1024, 32)])
 def test_sdpa(dt, Lq, Lk, E):
+    """(200, 1100, 40) and (96, 1024, 32) take the two-key-group kernel (>= 1024 keys, head dim
+    <= 48): an odd number of 64-key tiles, a ragged last tile, and a query block past Lq."""
     g = Gen(Lq + Lk + E)
     q = g.randn((2, 3, Lq, E), dt)
     k = g.randn((2, 3, Lk, E), dt)
