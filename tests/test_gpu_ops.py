@@ -573,7 +573,7 @@ def test_sd_group_norm_scenario_fixture():
 
 
 @pytest.mark.parametrize("dt", ["float32", "float16"])
-@pytest.mark.parametrize("rows,n", [(2048, 320), (77, 768), (50, 1280), (13, 3000), (9, 100)])
+@pytest.mark.parametrize("rows,n", [(2048, 320), (2049, 320), (1000, 640), (77, 768), (50, 1280), (13, 3000), (9, 100)])
 def test_layer_norm(dt, rows, n):
     g = Gen(81 + n)
     x = g.randn((rows, n), dt, 2.0)
