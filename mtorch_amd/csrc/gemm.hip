@@ -488,7 +488,10 @@ int mthip_gemm(int device, int dtype, int64_t batch, int64_t M, int64_t N, int64
     }
   }
   if (rc == MTHIP_OK) {
-      a.a_bytes = ((M - 1) * a.lda + a.K) * es;
+    // A row is read in whole 16-byte chunks and the buffer range check drops any dword that
+    // crosses a_bytes, so the extent covers the last row's final chunk (the padded copy holds
+    // zeros there; unpadded rows have K a multiple of the chunk).
+    a.a_bytes = ((M - 1) * a.lda + ceil_div(a.K, vec) * vec) * es;
     a.b_bytes = b_trans ? ((N - 1) * a.ldb + a.K) * es : ((K - 1) * a.ldb + ceil_div(N, vec) * vec) * es;
     if (a.a_bytes > kMaxBufferBytes || a.b_bytes > kMaxBufferBytes) {
       rc = fail(MTHIP_ERR_UNSUPPORTED, "mthip_gemm: operands above 2 GiB per batch are not supported");
