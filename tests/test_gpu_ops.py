@@ -270,6 +270,21 @@ def test_matmul_batched_broadcast_and_transposes(dt):
 
 
 @pytest.mark.parametrize("dt", ["float32", "float16"])
+@pytest.mark.parametrize("K", [77, 1, 9, 13])
+def test_matmul_unaligned_depth_every_row(dt, K):
+    """K not a whole number of 16-byte chunks: A is staged through a zero-padded copy and its
+    last row's final chunk must still be read (probabilities @ values over 77 text tokens)."""
+    g = Gen(33 + K)
+    a = g.randn((3, 64, K), dt)
+    b = g.randn((3, K, 40), dt)
+    got = val(host(mt.bmm(dev(a), dev(b))))
+    ref = val(orc.matmul(a, b))
+    for r in (0, 62, 63):
+        assert rel(got[:, r], ref[:, r]) <= TOL[dt], r
+    assert rel(got, ref) <= TOL[dt]
+
+
+@pytest.mark.parametrize("dt", ["float32", "float16"])
 def test_addmm_and_baddbmm(dt):
     g = Gen(32)
     inp = g.randn((40,), dt)
@@ -397,7 +412,7 @@ def test_conv2d_packed_weight_follows_inplace_writes(dt):
     wd.copy_(dev(w2))
     assert rel(val(host(F.conv2d(xd, wd, padding=1))), val(orc.conv2d(x, w2, None, padding=1))) <= TOL[dt]
     wd.fill_(0.25)
-    w3 = np.full_like(w2, orc.f2h(np.float32(0.25))[0] if dt == "float16" else 0.25)
+    w3 = np.full_like(w2, orc.f2h(np.float32(0.25)) if dt == "float16" else 0.25)
     assert rel(val(host(F.conv2d(xd, wd, padding=1))), val(orc.conv2d(x, w3, None, padding=1))) <= TOL[dt]
 
 
