@@ -103,6 +103,22 @@ int mthip_copy_strided(int device, int dtype, const void* src, int rank, const i
 /* dst[i] = value for n contiguous elements.  Serves full/zeros/ones/fill_ (tensor.h:143-149). */
 int mthip_fill(int device, int dtype, void* dst, int64_t n, double value);
 
+/* dst viewed through sizes/strides (element units), rank <= 8 <- value, narrowed as mthip_fill
+ * narrows it.  Serves item assignment of a scalar into a non-contiguous view
+ * (Tensor.__setitem__, mtorch/__init__.py Tensor.__setitem__ -> Tensor::fill_ on the view). */
+int mthip_fill_strided(int device, int dtype, void* dst, int rank, const int64_t* sizes, const int64_t* strides,
+                       double value);
+
+/* out (contiguous, out_sizes, dtype) = mask != 0 ? value : x; x and the BOOL mask viewed through
+ * strides (0 on broadcast axes), rank <= 8; value narrowed once as mthip_fill narrows it.
+ * Serves masked_fill (tensor.cpp:13497-13610). */
+int mthip_masked_fill(int device, int dtype, const void* x, const int64_t* x_strides, const void* mask,
+                      const int64_t* mask_strides, double value, void* out, int rank, const int64_t* out_sizes);
+
+/* y = !x over n contiguous BOOL bytes (nonzero is true).  Serves logical_not (tensor.cpp:14616)
+ * and ~ on bool tensors. */
+int mthip_logical_not(int device, const void* x, void* y, int64_t n);
+
 /* Concatenation of `count` contiguous inputs along `dim` of an output of rank `rank` and
  * shape out_sizes (each input shares every other extent).  Serves mtorch::cat (tensor.cpp:32141). */
 int mthip_cat(int device, int dtype, int count, const void* const* inputs, const int64_t* dim_sizes,

@@ -8,12 +8,15 @@ runs as a hand-written HIP kernel in libmthip (include/mthip.h).
 from __future__ import annotations
 
 from . import _lib, cuda, nn
+from ._einsum import einsum
 from ._ops import (
     addmm,
     arange,
     baddbmm,
     bmm,
     cat,
+    logical_not,
+    masked_fill,
     matmul,
 )
 from ._ops import add as _add
@@ -45,6 +48,7 @@ from ._tensor import (
     zeros,
 )
 from .nn import functional as _F
+from .serialization import load, save
 
 bool = bool_  # noqa: A001 - mtorch exposes mtorch.bool
 
@@ -117,5 +121,5 @@ __all__ = [
     "manual_seed", "initial_seed", "Generator", "no_grad", "enable_grad", "set_grad_enabled", "is_grad_enabled",
     "matmul", "bmm", "addmm", "baddbmm", "cat", "arange", "softmax", "sigmoid", "relu", "silu", "gelu", "add",
     "mul", "sub", "exp", "sin", "cos", "chunk", "split", "reshape", "transpose", "permute", "flatten", "unsqueeze",
-    "nn", "cuda",
+    "einsum", "masked_fill", "logical_not", "save", "load", "nn", "cuda",
 ]

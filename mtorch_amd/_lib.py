@@ -47,6 +47,9 @@ _SIGNATURES = {
     "mthip_cast": (_int, [_int, _int, _c_void_p, _int, _c_void_p, _i64]),
     "mthip_copy_strided": (_int, [_int, _int, _c_void_p, _int, _i64p, _i64p, _c_void_p]),
     "mthip_fill": (_int, [_int, _int, _c_void_p, _i64, _dbl]),
+    "mthip_fill_strided": (_int, [_int, _int, _c_void_p, _int, _i64p, _i64p, _dbl]),
+    "mthip_masked_fill": (_int, [_int, _int, _c_void_p, _i64p, _c_void_p, _i64p, _dbl, _c_void_p, _int, _i64p]),
+    "mthip_logical_not": (_int, [_int, _c_void_p, _c_void_p, _i64]),
     "mthip_cat": (_int, [_int, _int, _int, ctypes.POINTER(_c_void_p), _i64p, _int, _i64p, _int, _c_void_p]),
     "mthip_upsample_nearest2d": (_int, [_int, _int, _c_void_p, _c_void_p, _i64, _i64, _i64, _i64, _i64]),
     "mthip_binary": (_int, [_int, _int, _int, _c_void_p, _i64p, _c_void_p, _i64p, _c_void_p, _int, _i64p]),

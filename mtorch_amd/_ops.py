@@ -190,12 +190,44 @@ def fill_(t: Tensor, value) -> None:
             view[...] = value
         t._storage.version += 1
         return
-    if not t.is_contiguous():
-        raise unsupported("fill_ on a non-contiguous view", "cuda")
     n = t.numel()
-    if n:
+    if n and t.is_contiguous():
         _lib.check(_L().mthip_fill(t._dev(), t.dtype.code, t.data_ptr(), n, float(value)))
+    elif n:
+        _lib.check(_L().mthip_fill_strided(t._dev(), t.dtype.code, t.data_ptr(), t.dim(), _lib.int64_array(t.shape),
+                                           _lib.int64_array(t.stride()), float(value)))
     t._storage.version += 1
+
+
+def masked_fill(x: Tensor, mask: Tensor, value) -> Tensor:
+    """masked_fill (tensor.cpp:13497-13610): a new contiguous tensor of x's dtype holding value
+    (narrowed once, fp16 as float_to_half_bits((float)value)) where the bool mask -- broadcast to
+    x's shape -- is true, x elsewhere."""
+    if isinstance(value, Tensor):
+        value = value.item()
+    if mask.dtype is not T.bool_:
+        raise ValueError("masked_fill mask must be a bool tensor")
+    if list(T._broadcast_shape(list(x.shape), list(mask.shape))) != list(x.shape):
+        raise ValueError("masked_fill mask is not broadcastable to input")
+    dev = _gpu("masked_fill", x, mask)
+    out = _empty(list(x.shape), x.dtype, dev)
+    m = mask.expand(x.shape) if list(mask.shape) != list(x.shape) else mask
+    _lib.check(_L().mthip_masked_fill(dev, x.dtype.code, x.data_ptr(), _lib.int64_array(x.stride()), m.data_ptr(),
+                                      _lib.int64_array(m.stride()), float(value), out.data_ptr(), x.dim(),
+                                      _lib.int64_array(x.shape)))
+    return out
+
+
+def logical_not(x: Tensor) -> Tensor:
+    """logical_not (tensor.cpp:14616) of a bool tensor: a new contiguous bool tensor."""
+    if x.dtype is not T.bool_:
+        raise NotImplementedError("mtorch_amd: logical_not is implemented for bool tensors")
+    dev = _gpu("logical_not", x)
+    x = x if x.is_contiguous() else x.contiguous()
+    out = _empty(list(x.shape), T.bool_, dev)
+    if x.numel():
+        _lib.check(_L().mthip_logical_not(dev, x.data_ptr(), out.data_ptr(), x.numel()))
+    return out
 
 
 # ------------------------------------------------------------------------------ elementwise

@@ -400,7 +400,7 @@ class Tensor:
     def numpy(self):
         """Values as a numpy array (fp16 as numpy float16 by value)."""
         t = self if self.device.type == "cpu" else self.cpu()
-        arr = np.ascontiguousarray(t._host_view())
+        arr = np.ascontiguousarray(t._host_view()).reshape(tuple(t._sizes))  # keeps 0-dim shapes
         if t._dtype is float16:
             return arr.view(np.float16).copy()
         if t._dtype is bool_:
@@ -412,7 +412,7 @@ class Tensor:
         if self._dtype is not float16:
             raise TypeError("half_bits() expects a float16 tensor")
         t = self if self.device.type == "cpu" else self.cpu()
-        return np.ascontiguousarray(t._host_view()).copy()
+        return np.ascontiguousarray(t._host_view()).reshape(tuple(t._sizes)).copy()
 
     def tolist(self):
         arr = self.numpy()
@@ -765,6 +765,13 @@ class Tensor:
         strides.extend(self._strides[d:])
         return self._view(sizes, strides, offset)
 
+    def __setitem__(self, key, value):
+        """Item assignment into the view self[key] (a scalar fills it, a tensor is copied in with
+        broadcasting), as the reference's Tensor.__setitem__ does for basic indices."""
+        from . import _ops
+
+        _ops.copy_into(self[key], value)
+
     # ---- arithmetic ---------------------------------------------------------------------
     def __add__(self, other):
         from . import _ops
@@ -810,6 +817,21 @@ class Tensor:
         from . import _ops
 
         return _ops.unary(self, "neg")
+
+    def __invert__(self):
+        from . import _ops
+
+        return _ops.logical_not(self)
+
+    def logical_not(self):
+        from . import _ops
+
+        return _ops.logical_not(self)
+
+    def masked_fill(self, mask, value):
+        from . import _ops
+
+        return _ops.masked_fill(self, mask, value)
 
     def __matmul__(self, other):
         from . import _ops

@@ -232,6 +232,45 @@ __global__ void binary_strided_kernel(int op, const T* __restrict__ a, const T* 
   }
 }
 
+// out[i] = mask[i] ? fill : x[i] over a strided (broadcast) mask and input, as raw element bits
+// (masked_fill, tensor.cpp:13497-13610: the fill value is narrowed once on the host).
+template <typename U>
+__global__ void masked_fill_kernel(const U* __restrict__ x, const uint8_t* __restrict__ mask, U fill, U* __restrict__ out,
+                                   Shape s, int64_t n) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+    int64_t rem = i, ox = 0, om = 0;
+    for (int d = s.rank - 1; d >= 0; --d) {
+      const int64_t idx = rem % s.sizes[d];
+      rem /= s.sizes[d];
+      ox += idx * s.a_strides[d];
+      om += idx * s.b_strides[d];
+    }
+    out[i] = mask[om] ? fill : x[ox];
+  }
+}
+
+// dst viewed through strides (a_strides) <- value bits.
+template <typename U>
+__global__ void fill_strided_kernel(U* __restrict__ dst, U value, Shape s, int64_t n) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+    int64_t rem = i, o = 0;
+    for (int d = s.rank - 1; d >= 0; --d) {
+      const int64_t idx = rem % s.sizes[d];
+      rem /= s.sizes[d];
+      o += idx * s.a_strides[d];
+    }
+    dst[o] = value;
+  }
+}
+
+// bool not (logical_not, tensor.cpp:14616): any nonzero byte is true.
+__global__ void logical_not_kernel(const uint8_t* __restrict__ x, uint8_t* __restrict__ y, int64_t n) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) y[i] = x[i] ? 0 : 1;
+}
+
 // Tensor-scalar ops run in double and are narrowed once, as the reference's double path does.
 template <typename T>
 __global__ void binary_scalar_kernel(int op, const T* __restrict__ x, double scalar, int scalar_first,
@@ -395,43 +434,129 @@ int mthip_copy_strided(int device, int dtype, const void* src, int rank, const i
   return check_launch("mthip_copy_strided");
 }
 
+// The storage bits of `value` written as `dtype` (F16: float_to_half_bits((float)value),
+// tensor.cpp:276-315, restated on the host for one value; F32 through (float); BOOL as value != 0).
+static uint64_t host_fill_bits(int dtype, double value) {
+  switch (dtype) {
+    case MTHIP_F16: {
+      const float f = (float)value;
+      uint32_t bits;
+      std::memcpy(&bits, &f, 4);
+      const uint32_t sign = (bits >> 16) & 0x8000u, raw = (bits >> 23) & 0xffu;
+      const uint32_t man = bits & 0x7fffffu;
+      if (raw == 0xffu) return sign | 0x7c00u | (man ? ((man >> 13) ? (man >> 13) : 0x200u) : 0u);
+      const int32_t e = (int32_t)raw - 112;
+      if (e <= 0) return e < -10 ? sign : (sign | ((((man | 0x800000u) >> (1 - e)) + 0x1000u) >> 13));
+      const uint32_t r = ((uint32_t)e << 10) + ((man + 0x1000u) >> 13);
+      return sign | (r >= 0x7c00u ? 0x7c00u : r);
+    }
+    case MTHIP_F32: {
+      const float f = (float)value;
+      uint32_t bits;
+      std::memcpy(&bits, &f, 4);
+      return bits;
+    }
+    case MTHIP_F64: {
+      uint64_t bits;
+      std::memcpy(&bits, &value, 8);
+      return bits;
+    }
+    case MTHIP_I32: return (uint32_t)(int32_t)value;
+    case MTHIP_I64: return (uint64_t)(int64_t)value;
+    default: return value != 0.0 ? 1u : 0u;
+  }
+}
+
 int mthip_fill(int device, int dtype, void* dst, int64_t n, double value) {
-  MTHIP_REQUIRE(elem_size(dtype) != 0, "mthip_fill: unknown dtype");
+  const int es = elem_size(dtype);
+  MTHIP_REQUIRE(es != 0, "mthip_fill: unknown dtype");
   if (n <= 0) return MTHIP_OK;
   hipStream_t s = stream_for(device);
   if (!s) return MTHIP_ERR_HIP;
   if (int rc = use_device(device)) return rc;
   const unsigned g = grid_for(n);
-  switch (dtype) {
-    case MTHIP_F16: {
-      // f2h_bits is a device function; the host restatement below mirrors it for one value.
-      float f = (float)value;
-      uint32_t bits;
-      std::memcpy(&bits, &f, 4);
-      const uint32_t sign = (bits >> 16) & 0x8000u, raw = (bits >> 23) & 0xffu;
-      uint32_t man = bits & 0x7fffffu;
-      uint16_t h;
-      if (raw == 0xffu) {
-        h = (uint16_t)(sign | 0x7c00u | (man ? ((man >> 13) ? (man >> 13) : 0x200u) : 0u));
-      } else {
-        int32_t e = (int32_t)raw - 112;
-        if (e <= 0) {
-          h = e < -10 ? (uint16_t)sign : (uint16_t)(sign | ((((man | 0x800000u) >> (1 - e)) + 0x1000u) >> 13));
-        } else {
-          const uint32_t r = ((uint32_t)e << 10) + ((man + 0x1000u) >> 13);
-          h = (uint16_t)(sign | (r >= 0x7c00u ? 0x7c00u : r));
-        }
-      }
-      hipLaunchKernelGGL(fill_kernel<uint16_t>, dim3(g), dim3(kThreads), 0, s, (uint16_t*)dst, n, h);
-      break;
-    }
-    case MTHIP_F32: hipLaunchKernelGGL(fill_kernel<float>, dim3(g), dim3(kThreads), 0, s, (float*)dst, n, (float)value); break;
-    case MTHIP_F64: hipLaunchKernelGGL(fill_kernel<double>, dim3(g), dim3(kThreads), 0, s, (double*)dst, n, value); break;
-    case MTHIP_I32: hipLaunchKernelGGL(fill_kernel<int32_t>, dim3(g), dim3(kThreads), 0, s, (int32_t*)dst, n, (int32_t)value); break;
-    case MTHIP_I64: hipLaunchKernelGGL(fill_kernel<int64_t>, dim3(g), dim3(kThreads), 0, s, (int64_t*)dst, n, (int64_t)value); break;
-    default: hipLaunchKernelGGL(fill_kernel<uint8_t>, dim3(g), dim3(kThreads), 0, s, (uint8_t*)dst, n, (uint8_t)(value != 0.0)); break;
+  const uint64_t bits = host_fill_bits(dtype, value);
+  switch (es) {
+    case 1: hipLaunchKernelGGL(fill_kernel<uint8_t>, dim3(g), dim3(kThreads), 0, s, (uint8_t*)dst, n, (uint8_t)bits); break;
+    case 2: hipLaunchKernelGGL(fill_kernel<uint16_t>, dim3(g), dim3(kThreads), 0, s, (uint16_t*)dst, n, (uint16_t)bits); break;
+    case 4: hipLaunchKernelGGL(fill_kernel<uint32_t>, dim3(g), dim3(kThreads), 0, s, (uint32_t*)dst, n, (uint32_t)bits); break;
+    default: hipLaunchKernelGGL(fill_kernel<uint64_t>, dim3(g), dim3(kThreads), 0, s, (uint64_t*)dst, n, bits); break;
   }
   return check_launch("mthip_fill");
+}
+
+int mthip_fill_strided(int device, int dtype, void* dst, int rank, const int64_t* sizes, const int64_t* strides,
+                       double value) {
+  const int es = elem_size(dtype);
+  MTHIP_REQUIRE(es != 0, "mthip_fill_strided: unknown dtype");
+  MTHIP_REQUIRE(rank >= 0 && rank <= kMaxRank, "mthip_fill_strided: rank must be <= 8");
+  int64_t n = 1;
+  for (int d = 0; d < rank; ++d) n *= sizes[d];
+  if (n == 0) return MTHIP_OK;
+  hipStream_t s = stream_for(device);
+  if (!s) return MTHIP_ERR_HIP;
+  if (int rc = use_device(device)) return rc;
+  Shape sh{};
+  int64_t unused[kMaxRank];
+  int64_t* outs[2] = {sh.a_strides, unused};
+  const int64_t* ins[2] = {strides, strides};
+  sh.rank = collapse(rank, sizes, ins, 2, sh.sizes, outs);
+  if (sh.rank == 0) sh.rank = 1, sh.sizes[0] = 1, sh.a_strides[0] = 0;
+  const unsigned g = grid_for(n);
+  const uint64_t bits = host_fill_bits(dtype, value);
+  switch (es) {
+    case 1: hipLaunchKernelGGL(fill_strided_kernel<uint8_t>, dim3(g), dim3(kThreads), 0, s, (uint8_t*)dst, (uint8_t)bits, sh, n); break;
+    case 2: hipLaunchKernelGGL(fill_strided_kernel<uint16_t>, dim3(g), dim3(kThreads), 0, s, (uint16_t*)dst, (uint16_t)bits, sh, n); break;
+    case 4: hipLaunchKernelGGL(fill_strided_kernel<uint32_t>, dim3(g), dim3(kThreads), 0, s, (uint32_t*)dst, (uint32_t)bits, sh, n); break;
+    default: hipLaunchKernelGGL(fill_strided_kernel<uint64_t>, dim3(g), dim3(kThreads), 0, s, (uint64_t*)dst, bits, sh, n); break;
+  }
+  return check_launch("mthip_fill_strided");
+}
+
+int mthip_masked_fill(int device, int dtype, const void* x, const int64_t* x_strides, const void* mask,
+                      const int64_t* mask_strides, double value, void* out, int rank, const int64_t* out_sizes) {
+  const int es = elem_size(dtype);
+  MTHIP_REQUIRE(es != 0, "mthip_masked_fill: unknown dtype");
+  MTHIP_REQUIRE(rank >= 0 && rank <= kMaxRank, "mthip_masked_fill: rank must be <= 8");
+  int64_t n = 1;
+  for (int d = 0; d < rank; ++d) n *= out_sizes[d];
+  if (n == 0) return MTHIP_OK;
+  hipStream_t s = stream_for(device);
+  if (!s) return MTHIP_ERR_HIP;
+  if (int rc = use_device(device)) return rc;
+  int64_t out_strides[kMaxRank];
+  {
+    int64_t acc = 1;
+    for (int d = rank - 1; d >= 0; --d) {
+      out_strides[d] = acc;
+      acc *= out_sizes[d];
+    }
+  }
+  Shape sh{};
+  int64_t o_str[kMaxRank];
+  int64_t* outs[3] = {sh.a_strides, sh.b_strides, o_str};
+  const int64_t* ins[3] = {x_strides, mask_strides, out_strides};
+  sh.rank = collapse(rank, out_sizes, ins, 3, sh.sizes, outs);
+  if (sh.rank == 0) sh.rank = 1, sh.sizes[0] = 1, sh.a_strides[0] = 0, sh.b_strides[0] = 0;
+  const unsigned g = grid_for(n);
+  const uint64_t bits = host_fill_bits(dtype, value);
+  const uint8_t* m = static_cast<const uint8_t*>(mask);
+  switch (es) {
+    case 1: hipLaunchKernelGGL(masked_fill_kernel<uint8_t>, dim3(g), dim3(kThreads), 0, s, (const uint8_t*)x, m, (uint8_t)bits, (uint8_t*)out, sh, n); break;
+    case 2: hipLaunchKernelGGL(masked_fill_kernel<uint16_t>, dim3(g), dim3(kThreads), 0, s, (const uint16_t*)x, m, (uint16_t)bits, (uint16_t*)out, sh, n); break;
+    case 4: hipLaunchKernelGGL(masked_fill_kernel<uint32_t>, dim3(g), dim3(kThreads), 0, s, (const uint32_t*)x, m, (uint32_t)bits, (uint32_t*)out, sh, n); break;
+    default: hipLaunchKernelGGL(masked_fill_kernel<uint64_t>, dim3(g), dim3(kThreads), 0, s, (const uint64_t*)x, m, bits, (uint64_t*)out, sh, n); break;
+  }
+  return check_launch("mthip_masked_fill");
+}
+
+int mthip_logical_not(int device, const void* x, void* y, int64_t n) {
+  if (n <= 0) return MTHIP_OK;
+  hipStream_t s = stream_for(device);
+  if (!s) return MTHIP_ERR_HIP;
+  if (int rc = use_device(device)) return rc;
+  hipLaunchKernelGGL(logical_not_kernel, dim3(grid_for(n)), dim3(kThreads), 0, s, (const uint8_t*)x, (uint8_t*)y, n);
+  return check_launch("mthip_logical_not");
 }
 
 int mthip_cat(int device, int dtype, int count, const void* const* inputs, const int64_t* dim_sizes, int rank,

@@ -11,6 +11,7 @@ from .modules import (
     Linear,
     Module,
     ModuleList,
+    MultiheadAttention,
     Parameter,
     Sequential,
     SiLU,
@@ -20,5 +21,5 @@ from .modules import (
 
 __all__ = [
     "functional", "init", "Module", "Parameter", "Linear", "Conv2d", "GroupNorm", "LayerNorm", "SiLU", "GELU",
-    "Dropout", "Identity", "Sequential", "ModuleList", "Softmax", "Upsample",
+    "Dropout", "Identity", "Sequential", "ModuleList", "Softmax", "Upsample", "MultiheadAttention",
 ]

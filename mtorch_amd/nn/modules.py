@@ -324,3 +324,209 @@ class Upsample(Module):
 
     def forward(self, input):
         return functional.interpolate(input, self.size, self.scale_factor, self.mode)
+
+
+def _logical_and(a, b):
+    """Bool AND with broadcasting: a (broadcast to the joint shape) with False wherever b is
+    false -- one masked_fill launch, no separate kernel."""
+    shape = T._broadcast_shape(list(a.shape), list(b.shape))
+    return _ops.masked_fill(a.expand(shape), b.logical_not(), False)
+
+
+def _keep_mask_to_bias(mask):
+    """where(mask, 0.0, -inf) in float32 (mtorch/__init__.py:4413-4418)."""
+    zeros = T.zeros(list(mask.shape), dtype=T.float32, device=mask.device)
+    return _ops.masked_fill(zeros, mask.logical_not(), float("-inf"))
+
+
+class MultiheadAttention(Module):
+    """nn.MultiheadAttention (mtorch/__init__.py:4297-4578) over the device kernels: the fused
+    (3E x E) input projection when query, key and value are one tensor, the flash SDPA kernel
+    for the heads, and out_proj.  Deterministic default weights as the reference's
+    `_initial_weight(row, col, width)` (:4383-4385), input-projection bias zero, and the same
+    mask merging: a bool attn_mask / key_padding_mask marks positions to EXCLUDE and is inverted
+    into SDPA's keep mask; bool and float masks combine as an additive -inf bias."""
+
+    def __init__(self, embed_dim, num_heads, dropout=0.0, bias=True, add_bias_kv=False, add_zero_attn=False,
+                 kdim=None, vdim=None, batch_first=False, device=None, dtype=None):
+        super().__init__()
+        self.embed_dim = int(embed_dim)
+        self.num_heads = int(num_heads)
+        self.dropout = float(dropout)
+        self.batch_first = batch_first
+        self.head_dim = self.embed_dim // self.num_heads
+        if self.head_dim * self.num_heads != self.embed_dim:
+            raise ValueError("embed_dim must be divisible by num_heads")
+        self.kdim = self.embed_dim if kdim is None else int(kdim)
+        self.vdim = self.embed_dim if vdim is None else int(vdim)
+        self._qkv_same_embed_dim = self.kdim == self.embed_dim and self.vdim == self.embed_dim
+        self.add_zero_attn = bool(add_zero_attn)
+        E = self.embed_dim
+        if self._qkv_same_embed_dim:
+            self.in_proj_weight = Parameter(_make(self._initial(3 * E, E, E), [3 * E, E], dtype, device))
+            self.q_proj_weight = self.k_proj_weight = self.v_proj_weight = None
+        else:
+            self.in_proj_weight = None
+            self.q_proj_weight = Parameter(_make(self._initial(E, E, E), [E, E], dtype, device))
+            self.k_proj_weight = Parameter(_make(self._initial(E, self.kdim, self.kdim), [E, self.kdim], dtype, device))
+            self.v_proj_weight = Parameter(_make(self._initial(E, self.vdim, self.vdim), [E, self.vdim], dtype, device))
+        self.in_proj_bias = Parameter(_make(np.zeros(3 * E), [3 * E], dtype, device)) if bias else None
+        if add_bias_kv:
+            self.bias_k = Parameter(_make(self._initial(1, E, E), [1, 1, E], dtype, device))
+            self.bias_v = Parameter(_make(self._initial(2, E, E)[E:], [1, 1, E], dtype, device))
+        else:
+            self.bias_k = self.bias_v = None
+        self.out_proj = Linear(E, E, bias=bias, device=device, dtype=dtype)
+
+    @staticmethod
+    def _initial(rows, cols, width):
+        """_initial_weight(row, col, width) for row < rows, col < cols, in float64."""
+        span = max(1, width)
+        r = np.arange(rows, dtype=np.int64)[:, None]
+        c = np.arange(cols, dtype=np.int64)[None, :]
+        return (((r * width + c) % (2 * span + 1)) - span).astype(np.float64).reshape(-1) / float(span * span)
+
+    # ---- layout ------------------------------------------------------------------------
+    def _as_batch_first(self, x):
+        if x.dim() == 2:
+            return x.reshape(1, x.shape[0], x.shape[1]), True
+        if x.dim() != 3:
+            raise ValueError("MultiheadAttention input must be 2-D or 3-D")
+        return (x, False) if self.batch_first else (x.transpose(0, 1), False)
+
+    def _restore_layout(self, x, unbatched):
+        if unbatched:
+            return x.squeeze(0)
+        return x if self.batch_first else x.transpose(0, 1)
+
+    def _split_heads(self, x):
+        b, n, _ = x.shape
+        return x.reshape(b, n, self.num_heads, self.head_dim).transpose(1, 2)
+
+    def _merge_heads(self, x):
+        b, _, n, _ = x.shape
+        return x.transpose(1, 2).contiguous().reshape(b, n, self.embed_dim)
+
+    # ---- masks -------------------------------------------------------------------------
+    @staticmethod
+    def _pad_source_mask(mask):
+        if mask is None:
+            return None
+        pad = T.zeros(list(mask.shape[:-1]) + [1], dtype=mask.dtype, device=mask.device)
+        return _ops.cat([mask, pad], dim=mask.dim() - 1)
+
+    def _append_bias_kv(self, k, v, kpm, am):
+        if self.bias_k is None:
+            return k, v, kpm, am
+        b = k.shape[0]
+        k = _ops.cat([k, self.bias_k.expand(b, 1, self.embed_dim)], dim=1)
+        v = _ops.cat([v, self.bias_v.expand(b, 1, self.embed_dim)], dim=1)
+        return k, v, self._pad_source_mask(kpm), self._pad_source_mask(am)
+
+    def _append_zero_kv(self, k, v, kpm, am):
+        if not self.add_zero_attn:
+            return k, v, kpm, am
+        k = _ops.cat([k, T.zeros([k.shape[0], 1, k.shape[2]], dtype=k.dtype, device=k.device)], dim=1)
+        v = _ops.cat([v, T.zeros([v.shape[0], 1, v.shape[2]], dtype=v.dtype, device=v.device)], dim=1)
+        return k, v, self._pad_source_mask(kpm), self._pad_source_mask(am)
+
+    def _merge_attention_masks(self, attn_mask, key_padding_mask, batch, source_length):
+        """mtorch/__init__.py:4439-4470."""
+        merged = None
+        if attn_mask is not None:
+            merged = attn_mask.logical_not() if attn_mask.dtype is T.bool_ else attn_mask
+        if key_padding_mask is not None:
+            kpm = key_padding_mask
+            if kpm.dim() == 1:
+                if kpm.shape[0] != source_length:
+                    raise ValueError("key_padding_mask source length does not match key")
+                kpm = kpm.reshape(1, source_length)
+            elif kpm.dim() != 2:
+                raise ValueError("key_padding_mask must be 1-D or 2-D")
+            if kpm.shape[0] != batch or kpm.shape[1] != source_length:
+                raise ValueError("key_padding_mask shape must be (batch, source_length)")
+            km = kpm.logical_not() if kpm.dtype is T.bool_ else kpm
+            km = km.reshape(batch, 1, 1, source_length)
+            if merged is None:
+                merged = km
+            elif merged.dtype is T.bool_ and km.dtype is T.bool_:
+                merged = _logical_and(merged, km)
+            else:
+                if merged.dtype is T.bool_:
+                    merged = _keep_mask_to_bias(merged)
+                if km.dtype is T.bool_:
+                    km = _keep_mask_to_bias(km)
+                merged = merged + km
+        return merged
+
+    def _attention_weights(self, q, k, mask, is_causal, average, unbatched):
+        """The per-head probabilities SDPA used (the reference runs SDPA against an identity value,
+        mtorch/__init__.py:4472-4491): softmax(q k^T / sqrt(head_dim) + mask) computed in float32
+        as SDPA does, averaged over heads before the one narrowing to the query dtype."""
+        b, h, lq, d = q.shape
+        lk = k.shape[2]
+        q32 = q if q.dtype is T.float32 else q.float()
+        k32 = k if k.dtype is T.float32 else k.float()
+        scores = _ops.matmul(q32, k32.transpose(-1, -2).contiguous()) * (1.0 / float(np.sqrt(d)))
+        if mask is not None:
+            if mask.dtype is T.bool_:
+                scores = _ops.masked_fill(scores, _broadcast_to(mask, scores.shape).logical_not(), float("-inf"))
+            else:
+                scores = scores + (mask if mask.dtype is T.float32 else mask.float())
+        if is_causal:
+            keep = T.from_numpy(np.tril(np.ones((lq, lk), dtype=bool))).to(q.device)
+            scores = _ops.masked_fill(scores, keep.logical_not(), float("-inf"))
+        w = _ops.softmax(scores, dim=-1)
+        if average:
+            ones = T.ones([1, h], dtype=T.float32, device=q.device)
+            w = (_ops.matmul(ones, w.reshape(b, h, lq * lk)) * (1.0 / h)).reshape(b, lq, lk)
+        if w.dtype is not q.dtype:
+            w = w.to(dtype=q.dtype)
+        return w.squeeze(0) if unbatched else w
+
+    def forward(self, query, key, value, key_padding_mask=None, need_weights=True, attn_mask=None,
+                average_attn_weights=True, is_causal=False):
+        q_bf, q_unb = self._as_batch_first(query)
+        k_bf, k_unb = self._as_batch_first(key)
+        v_bf, v_unb = self._as_batch_first(value)
+        if k_unb != q_unb or v_unb != q_unb:
+            raise ValueError("query, key, and value must agree on batching")
+        if q_bf.shape[2] != self.embed_dim or k_bf.shape[2] != self.kdim or v_bf.shape[2] != self.vdim:
+            raise ValueError("query, key, and value embedding dimensions must match configured dimensions")
+        E = self.embed_dim
+        ib = self.in_proj_bias
+        bq = None if ib is None else ib.narrow(0, 0, E)
+        bk = None if ib is None else ib.narrow(0, E, E)
+        bv = None if ib is None else ib.narrow(0, 2 * E, E)
+        if self._qkv_same_embed_dim and query is key and key is value:
+            qkv = functional.linear(q_bf, self.in_proj_weight, ib)  # one (3E x E) GEMM
+            q_p, k_p, v_p = qkv.narrow(2, 0, E), qkv.narrow(2, E, E), qkv.narrow(2, 2 * E, E)
+        elif self._qkv_same_embed_dim:
+            w = self.in_proj_weight
+            q_p = functional.linear(q_bf, w.narrow(0, 0, E), bq)
+            k_p = functional.linear(k_bf, w.narrow(0, E, E), bk)
+            v_p = functional.linear(v_bf, w.narrow(0, 2 * E, E), bv)
+        else:
+            q_p = functional.linear(q_bf, self.q_proj_weight, bq)
+            k_p = functional.linear(k_bf, self.k_proj_weight, bk)
+            v_p = functional.linear(v_bf, self.v_proj_weight, bv)
+        k_p, v_p, key_padding_mask, attn_mask = self._append_bias_kv(k_p, v_p, key_padding_mask, attn_mask)
+        k_p, v_p, key_padding_mask, attn_mask = self._append_zero_kv(k_p, v_p, key_padding_mask, attn_mask)
+        qh, kh, vh = self._split_heads(q_p), self._split_heads(k_p), self._split_heads(v_p)
+        merged = None
+        if attn_mask is not None or key_padding_mask is not None:
+            merged = self._merge_attention_masks(attn_mask, key_padding_mask, qh.shape[0], kh.shape[2])
+        p = self.dropout if self.training else 0.0
+        att = functional.scaled_dot_product_attention(qh, kh, vh, merged, p, is_causal)
+        m = self._merge_heads(att)
+        b, n, _ = m.shape
+        out = self.out_proj(m.reshape(b * n, E)).reshape(b, n, E)
+        weights = None
+        if need_weights:
+            weights = self._attention_weights(qh, kh, merged, is_causal, average_attn_weights, q_unb)
+        return self._restore_layout(out, q_unb), weights
+
+
+def _broadcast_to(t, shape):
+    shape = list(shape)
+    return t if list(t.shape) == shape else t.expand(shape)

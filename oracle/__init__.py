@@ -96,15 +96,17 @@ def _p(a):
 
 
 def f2h(x) -> np.ndarray:
+    shape = np.shape(x)  # ascontiguousarray lifts 0-dim inputs to 1-dim
     x = np.ascontiguousarray(x, dtype=np.float32)
-    out = np.empty(x.shape, np.uint16)
+    out = np.empty(shape, np.uint16)
     lib().orc_f2h_array(x.ctypes.data, out.ctypes.data, x.size)
     return out
 
 
 def h2f(h) -> np.ndarray:
+    shape = np.shape(h)
     h = np.ascontiguousarray(h, dtype=np.uint16)
-    out = np.empty(h.shape, np.float32)
+    out = np.empty(shape, np.float32)
     lib().orc_h2f_array(h.ctypes.data, out.ctypes.data, h.size)
     return out
 

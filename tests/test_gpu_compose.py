@@ -1,0 +1,428 @@
+"""GPU parity for the attention paths SD code composes by hand and for the device model lifecycle:
+
+* the legacy attention ``baddbmm -> masked_fill(~mask, -10000) -> softmax -> bmm (+ query)`` of the
+  reference benchmark ``stable_diffusion_half_legacy_baddbmm_attention_16x64x77x40``
+  (tests/compat/benchmarking.py:567-639), fp16 and the fp32-upcast variant;
+* einsum lowered onto the GEMM (mtorch/__init__.py:1063; native patterns module.cpp:6282-6365);
+* nn.MultiheadAttention (mtorch/__init__.py:4297-4578) against torch.nn.MultiheadAttention in
+  float64 on the CPU -- the checker the reference's own tests use
+  (tests/compat/test_nn_modules.py:196-874) -- on the same scenario values, then at SD shapes;
+* masked_fill / logical_not / item assignment bit-exact;
+* mtorch.save / mtorch.load round trips of device tensors and modules.
+
+Tolerances: the oracle chain (each op's own rounding) within max|d|/max|ref| <= 1e-4 (fp32),
+1e-2 (fp16); against a float64 restatement the reference benchmark's rtol = atol = 4e-3; the
+MultiheadAttention scenarios the reference's rtol = atol = 1e-5 (fp32).
+"""
+
+import io
+import os
+import sys
+
+import numpy as np
+import pytest
+
+import mtorch_amd as mt
+import oracle as orc
+
+pytestmark = pytest.mark.gpu
+HERE = os.path.dirname(__file__)
+sys.path.insert(0, HERE)
+from test_gpu_ops import Gen, TOL, dev, host, rel, val  # noqa: E402
+
+F = mt.nn.functional
+
+
+@pytest.fixture(autouse=True)
+def _no_grad():
+    with mt.no_grad():
+        yield
+
+
+# ------------------------------------------------------------------ masked_fill / logical_not
+
+
+@pytest.mark.parametrize("dt", ["float16", "float32", "int64", "bool"])
+def test_masked_fill_bit_exact(dt):
+    rng = np.random.default_rng(5)
+    if dt == "float16":
+        x = orc.f2h(rng.standard_normal((4, 6, 33)).astype(np.float32))
+    elif dt == "float32":
+        x = rng.standard_normal((4, 6, 33)).astype(np.float32)
+    elif dt == "int64":
+        x = rng.integers(-1000, 1000, (4, 6, 33)).astype(np.int64)
+    else:
+        x = rng.random((4, 6, 33)) < 0.5
+    mask = rng.random((4, 1, 33)) < 0.3
+    xt = dev(x) if dt != "bool" else mt.from_numpy(x).to("cuda")
+    for value in (-10000.0, 0.1, float("-inf"), 3.0, 0.0):
+        if dt in ("int64", "bool") and not np.isfinite(value):
+            continue
+        got = xt.masked_fill(mt.from_numpy(mask).to("cuda"), value)
+        assert got.is_contiguous() and list(got.shape) == [4, 6, 33]
+        if dt == "float16":
+            fill = orc.f2h(np.float32(value))  # float_to_half_bits((float)value)
+        elif dt == "float32":
+            fill = np.float32(value)
+        elif dt == "int64":
+            fill = np.int64(value)
+        else:
+            fill = np.bool_(value != 0.0)
+        ref = np.where(np.broadcast_to(mask, x.shape), fill, x).astype(x.dtype)
+        out = host(got) if dt != "bool" else got.cpu().numpy()
+        assert np.array_equal(out.view(np.uint8), ref.view(np.uint8)), value
+    # strided input (a transposed view) and a mask of lower rank
+    xv = xt.transpose(0, 2)
+    m2 = rng.random((4,)) < 0.5
+    got = xv.masked_fill(mt.from_numpy(m2).to("cuda"), 2.0)
+    base = np.ascontiguousarray(x.transpose(2, 1, 0))
+    fill = orc.f2h(np.float32(2.0)) if dt == "float16" else np.array(2.0).astype(x.dtype)
+    ref = np.where(np.broadcast_to(m2, base.shape), fill, base).astype(x.dtype)
+    out = host(got) if dt != "bool" else got.cpu().numpy()
+    assert np.array_equal(out.view(np.uint8), ref.view(np.uint8))
+
+
+def test_masked_fill_rejects_bad_masks():
+    x = mt.zeros((2, 3), dtype=mt.float32, device="cuda")
+    with pytest.raises(ValueError, match="bool"):
+        x.masked_fill(mt.ones((2, 3), dtype=mt.float32, device="cuda"), 1.0)
+    with pytest.raises(ValueError, match="broadcastable"):
+        x.masked_fill(mt.ones((4, 2, 3), dtype=mt.bool, device="cuda"), 1.0)
+
+
+def test_logical_not_and_item_assignment():
+    rng = np.random.default_rng(6)
+    m = rng.random((3, 5, 7)) < 0.5
+    d = mt.from_numpy(m).to("cuda")
+    assert np.array_equal((~d).cpu().numpy(), ~m)
+    assert np.array_equal(mt.logical_not(d).cpu().numpy(), ~m)
+    # the reference setups build the text mask with item assignment; on the device it is a strided fill
+    t = mt.ones((16, 1, 77), dtype=mt.bool, device="cuda")
+    t[:, :, 70:] = False
+    exp = np.ones((16, 1, 77), bool)
+    exp[:, :, 70:] = False
+    assert np.array_equal(t.cpu().numpy(), exp)
+    h = dev(orc.f2h(rng.standard_normal((8, 12)).astype(np.float32)))
+    ref = host(h).copy()
+    h[2:6, ::3] = 0.1
+    ref[2:6, ::3] = orc.f2h(np.float32(0.1))
+    src = dev(orc.f2h(rng.standard_normal((12,)).astype(np.float32)))
+    h[7] = src
+    ref[7] = host(src)
+    assert np.array_equal(host(h), ref)
+
+
+# ------------------------------------------------------------------ legacy SD attention
+
+
+def _sd_rank3_inputs():
+    """tests/compat/benchmarking.py:567-584: 16 batch-heads x 64 queries x 77 keys x 40, fp16, the
+    last 7 keys masked out."""
+    bh, lq, lk, e = 16, 64, 77, 40
+    qb = np.arange(bh * lq * e, dtype=np.float32).reshape(bh, lq, e)
+    kb = np.arange(bh * lk * e, dtype=np.float32).reshape(bh, lk, e)
+    q = orc.f2h(np.sin(qb * np.float32(0.013)) * np.float32(0.2))
+    k = orc.f2h(np.cos(kb * np.float32(0.011)) * np.float32(0.2))
+    v = orc.f2h(np.sin(kb * np.float32(0.017) + np.float32(0.25)) * np.float32(0.2))
+    mask = np.ones((bh, 1, lk), bool)
+    mask[:, :, lk - 7:] = False
+    return q, k, v, mask
+
+
+def _legacy_path(q, k, v, text_mask, upcast):
+    """The reference benchmark path, op for op (benchmarking.py:601-639)."""
+    if not upcast:
+        scores = mt.baddbmm(mt.zeros((q.shape[0], q.shape[1], k.shape[1]), dtype=q.dtype, device="cuda"), q,
+                            k.transpose(1, 2).contiguous(), beta=0.0, alpha=0.125)
+    else:
+        scores = mt.baddbmm(mt.zeros((q.shape[0], q.shape[1], k.shape[1]), dtype=mt.float32, device="cuda"),
+                            q.to(dtype=mt.float32), k.transpose(1, 2).contiguous().to(dtype=mt.float32),
+                            beta=0.0, alpha=0.125)
+    scores = scores.masked_fill(~text_mask, -10000.0)
+    p = mt.softmax(scores, dim=-1)
+    if upcast:
+        p = p.to(dtype=mt.float16)
+    return mt.bmm(p, v) + q
+
+
+def _legacy_oracle(q, k, v, mask, upcast):
+    """The same chain through the oracle's per-op restatements (each op's own rounding)."""
+    bh, lq, _ = q.shape
+    lk = k.shape[1]
+    kt = np.ascontiguousarray(k.transpose(0, 2, 1))
+    if not upcast:
+        zeros = np.zeros((lq, lk), np.uint16)
+        s = np.stack([orc.addmm(zeros, q[i], kt[i], 0.0, 0.125) for i in range(bh)])
+        s = np.where(np.broadcast_to(mask, s.shape), s, orc.f2h(np.float32(-10000.0)))
+        p = orc.softmax_lastdim(s)
+    else:
+        zeros = np.zeros((lq, lk), np.float32)
+        q32, k32 = orc.h2f(q), orc.h2f(kt)
+        s = np.stack([orc.addmm(zeros, q32[i], k32[i], 0.0, 0.125) for i in range(bh)])
+        s = np.where(np.broadcast_to(mask, s.shape), s, np.float32(-10000.0)).astype(np.float32)
+        p = orc.f2h(orc.softmax_lastdim(s))
+    o = orc.matmul(p, v)
+    return orc.binary(o, q, "add")
+
+
+@pytest.mark.parametrize("upcast", [False, True], ids=["half", "upcast"])
+def test_legacy_baddbmm_attention_sd_16x64x77x40(upcast):
+    q, k, v, mask = _sd_rank3_inputs()
+    text_mask = mt.ones((16, 1, 77), dtype=mt.bool)
+    text_mask[:, :, 70:] = False  # built on the host as the benchmark setup does, then moved
+    got = host(_legacy_path(dev(q), dev(k), dev(v), text_mask.to("cuda"), upcast))
+    exp = _legacy_oracle(q, k, v, mask, upcast)
+    assert rel(orc.h2f(got), orc.h2f(exp)) <= TOL["float16"]
+    # against float64 math (masked keys dropped), at the benchmark's tolerance
+    qf, kf, vf = (orc.h2f(a).astype(np.float64) for a in (q, k, v))
+    s = np.einsum("bqd,bkd->bqk", qf, kf) * 0.125
+    s = np.where(mask, s, -np.inf)
+    pr = np.exp(s - s.max(-1, keepdims=True))
+    pr /= pr.sum(-1, keepdims=True)
+    ref = np.einsum("bqk,bkd->bqd", pr, vf) + qf
+    assert np.allclose(orc.h2f(got), ref, rtol=4e-3, atol=4e-3)
+    # and the fused SDPA path the reference benchmarks beside it (benchmarking.py:587-598)
+    sd = host(F.scaled_dot_product_attention(dev(q), dev(k), dev(v), attn_mask=text_mask.to("cuda"), scale=0.125)
+              + dev(q))
+    assert np.allclose(orc.h2f(sd), orc.h2f(got), rtol=4e-3, atol=4e-3)
+
+
+# ------------------------------------------------------------------ einsum
+
+
+EINSUM_CASES = [
+    ("ij,jk", [(33, 20), (20, 45)]),
+    ("ij,jk->ik", [(64, 40), (40, 77)]),
+    ("bij,bjk->bik", [(4, 25, 30), (4, 30, 40)]),
+    ("...ij,...jk->...ik", [(2, 3, 17, 20), (2, 3, 20, 9)]),
+    ("bhij,bhjd->bhid", [(2, 8, 64, 77), (2, 8, 77, 40)]),
+    ("bhid,bhjd->bhij", [(2, 8, 64, 40), (2, 8, 77, 40)]),
+    ("bhqd,bhkd->bhqk", [(2, 4, 33, 64), (2, 4, 50, 64)]),
+    ("bid,bjd->bij", [(16, 64, 40), (16, 77, 40)]),
+    ("bnm,bmd->bnd", [(3, 20, 30), (3, 30, 8)]),
+    ("abcd,aecd->abe", [(2, 5, 3, 4), (2, 6, 3, 4)]),
+    ("bqhd,bkhd->bhqk", [(2, 33, 4, 40), (2, 50, 4, 40)]),
+    ("...ij,jk->...ik", [(3, 2, 10, 12), (12, 7)]),
+    ("i,j->ij", [(13,), (17,)]),
+    ("i,i->", [(300,), (300,)]),
+    ("ij->ji", [(5, 9)]),
+    ("ij,jk,kl->il", [(8, 12), (12, 10), (10, 6)]),
+    ("bij,jk->bik", [(1, 9, 11), (11, 5)]),
+    ("bij,bjk->bik", [(1, 9, 11), (4, 11, 5)]),
+]
+
+
+@pytest.mark.parametrize("dt", ["float32", "float16"])
+@pytest.mark.parametrize("eq,shapes", EINSUM_CASES, ids=[c[0] for c in EINSUM_CASES])
+def test_einsum(dt, eq, shapes):
+    g = Gen(40 + len(eq))
+    ops = [g.randn(s, dt) for s in shapes]
+    got = mt.einsum(eq, *[dev(a) for a in ops])
+    ref = np.einsum(eq, *[val(a).astype(np.float64) for a in ops])
+    assert list(got.shape) == list(ref.shape)
+    assert rel(val(host(got.contiguous())), ref) <= TOL[dt]
+
+
+def test_einsum_native_patterns_match_matmul_bit_for_bit():
+    """The patterns the reference's native einsum maps to matmul (module.cpp:6282-6365) give the
+    matmul result itself."""
+    g = Gen(47)
+    q, k, v = g.randn((2, 8, 64, 40), "float16"), g.randn((2, 8, 77, 40), "float16"), g.randn((2, 8, 77, 40), "float16")
+    s = mt.einsum("bhid,bhjd->bhij", dev(q), dev(k))
+    assert np.array_equal(host(s), host(mt.matmul(dev(q), dev(k).transpose(-1, -2))))
+    o = mt.einsum("bhij,bhjd->bhid", s, dev(v))
+    assert np.array_equal(host(o), host(mt.matmul(s, dev(v))))
+    assert np.array_equal(host(mt.einsum("ij,jk", dev(q[0, 0]), dev(k[0, 0].T.copy()))),
+                          host(mt.matmul(dev(q[0, 0]), dev(k[0, 0].T.copy()))))
+
+
+def test_einsum_unsupported_forms_raise():
+    x = mt.zeros((4, 4), dtype=mt.float32, device="cuda")
+    with pytest.raises(NotImplementedError):
+        mt.einsum("ii->i", x)
+    with pytest.raises(NotImplementedError):
+        mt.einsum("ij->i", x)
+    with pytest.raises(NotImplementedError):
+        mt.einsum("ij,jk->i", x, x)
+    with pytest.raises(ValueError):
+        mt.einsum("ij,jk->ik", x)
+    with pytest.raises(ValueError):
+        mt.einsum("ij,jk->ik", x, mt.zeros((5, 4), dtype=mt.float32, device="cuda"))
+
+
+# ------------------------------------------------------------------ MultiheadAttention
+
+# scenario values of tests/compat/test_nn_modules.py:196-229
+_IN_W = [[0.25, -0.5, 0.75, 1.0], [-0.25, 0.5, 1.0, -0.75], [1.0, 0.25, -0.5, 0.5], [-1.0, 0.75, 0.25, -0.25],
+         [0.5, -1.0, 0.25, 0.75], [1.0, 0.5, -0.5, 1.5], [-0.25, 0.75, 1.0, -1.0], [0.25, -0.75, 0.5, 1.0],
+         [1.0, -0.5, 0.25, 0.75], [0.5, 1.5, -1.0, 0.25], [-0.25, 0.75, 1.0, -0.5], [1.25, -0.25, 0.5, -1.0]]
+_IN_B = [0.1, -0.2, 0.3, -0.4, 0.25, -0.5, 0.75, 0.5, -0.1, 0.2, -0.3, 0.4]
+_OUT_W = [[0.25, -0.5, 0.75, 1.0], [-0.25, 0.5, 1.0, -0.75], [1.0, 0.25, -0.5, 0.5], [-1.0, 0.75, 0.25, -0.25]]
+_OUT_B = [0.5, -0.25, 0.75, -0.5]
+_X = [[[0.25, -0.5, 1.0, 0.75], [1.5, 0.25, -0.75, 0.5], [-1.0, 0.5, 0.25, 1.25]]]
+
+
+def _torch():
+    return pytest.importorskip("torch")
+
+
+def _pair(params, dtype="float32", **kw):
+    """(torch float64 module, mtorch_amd module on the GPU) with the same parameters."""
+    torch = _torch()
+    tm = torch.nn.MultiheadAttention(dropout=0.0, **kw).double()
+    mm = mt.nn.MultiheadAttention(dropout=0.0, dtype=getattr(mt, dtype), **kw)
+    for name, value in params.items():
+        arr = np.asarray(value, np.float64)
+        obj_t, obj_m = tm, mm
+        *path, leaf = name.split(".")
+        for p in path:
+            obj_t, obj_m = getattr(obj_t, p), getattr(obj_m, p)
+        with torch.no_grad():
+            getattr(obj_t, leaf).copy_(torch.tensor(arr))
+        getattr(obj_m, leaf).copy_(mt.tensor(arr, dtype=getattr(mt, dtype)))
+    return tm, mm.to("cuda")
+
+
+def _scenario_params(**extra):
+    p = {"in_proj_weight": _IN_W, "in_proj_bias": _IN_B, "out_proj.weight": _OUT_W, "out_proj.bias": _OUT_B}
+    p.update(extra)
+    return p
+
+
+def _cmp(got, exp, tol):
+    g = got.cpu().numpy().astype(np.float64)
+    e = exp.detach().numpy()
+    assert g.shape == e.shape, (g.shape, e.shape)
+    assert np.allclose(g, e, rtol=tol, atol=tol), float(np.max(np.abs(g - e)))
+
+
+def test_mha_scenarios_match_torch():
+    torch = _torch()
+    x = np.asarray(_X, np.float64)
+    tx, mx = torch.tensor(x), mt.tensor(x, dtype=mt.float32, device="cuda")
+    am = np.array([[False, True, False], [False, False, False], [True, False, False]])
+    kpm = np.array([[False, False, True]])
+    tam, mam = torch.tensor(am), mt.from_numpy(am).to("cuda")
+    tkp, mkp = torch.tensor(kpm), mt.from_numpy(kpm).to("cuda")
+    # self-attention, fused input projection (test_nn_modules.py:664-684)
+    tm, mm = _pair(_scenario_params(), embed_dim=4, num_heads=2, batch_first=True)
+    _cmp(mm(mx, mx, mx, need_weights=False)[0], tm(tx, tx, tx, need_weights=False)[0], 1e-5)
+    # cross attention with weights (:687-730)
+    q = np.asarray([[[0.25, -0.5, 1.0, 0.75], [1.5, 0.25, -0.75, 0.5]]])
+    k = np.asarray([[[0.5, -1.0, 0.25, 1.25], [1.0, 0.5, -0.5, 0.75], [-0.25, 0.75, 1.0, -1.0]]])
+    v = np.asarray([[[1.0, -0.5, 0.25, 0.75], [0.5, 1.5, -1.0, 0.25], [-0.25, 0.75, 1.0, -0.5]]])
+    to, tw = tm(torch.tensor(q), torch.tensor(k), torch.tensor(v), need_weights=True)
+    mo, mw = mm(*(mt.tensor(a, dtype=mt.float32, device="cuda") for a in (q, k, v)), need_weights=True)
+    _cmp(mo, to, 1e-5)
+    _cmp(mw, tw, 1e-5)
+    # bool attn_mask + key_padding_mask (:733-780)
+    _cmp(mm(mx, mx, mx, key_padding_mask=mkp, need_weights=False, attn_mask=mam)[0],
+         tm(tx, tx, tx, key_padding_mask=tkp, need_weights=False, attn_mask=tam)[0], 1e-5)
+    # per-head weights, not averaged
+    _cmp(mm(mx, mx, mx, attn_mask=mam, average_attn_weights=False)[1],
+         tm(tx, tx, tx, attn_mask=tam, average_attn_weights=False)[1], 1e-5)
+    # add_zero_attn (:783-803)
+    tm, mm = _pair(_scenario_params(), embed_dim=4, num_heads=2, batch_first=True, add_zero_attn=True)
+    _cmp(mm(mx, mx, mx, key_padding_mask=mkp, need_weights=False)[0],
+         tm(tx, tx, tx, key_padding_mask=tkp, need_weights=False)[0], 1e-5)
+    # add_bias_kv (:806-832)
+    tm, mm = _pair(_scenario_params(bias_k=[[[0.25, -0.5, 0.75, -1.0]]], bias_v=[[[1.0, 0.5, -0.25, 0.75]]]),
+                   embed_dim=4, num_heads=2, batch_first=True, add_bias_kv=True)
+    _cmp(mm(mx, mx, mx, need_weights=False, attn_mask=mam)[0], tm(tx, tx, tx, need_weights=False, attn_mask=tam)[0],
+         1e-5)
+    # separate kdim / vdim (:835-876)
+    params = {"q_proj_weight": _OUT_W,
+              "k_proj_weight": [[0.5, -1.0, 0.25], [1.0, 0.5, -0.5], [-0.25, 0.75, 1.0], [0.25, -0.75, 0.5]],
+              "v_proj_weight": [[1.0, -0.5, 0.25, 0.75, -1.0], [0.5, 1.5, -1.0, 0.25, 0.5],
+                                [-0.25, 0.75, 1.0, -0.5, 1.25], [1.25, -0.25, 0.5, -1.0, 0.75]],
+              "in_proj_bias": _IN_B, "out_proj.weight": _OUT_W, "out_proj.bias": _OUT_B}
+    tm, mm = _pair(params, embed_dim=4, num_heads=2, kdim=3, vdim=5, batch_first=True)
+    k3 = np.asarray([[[0.5, -1.0, 0.25], [1.0, 0.5, -0.5], [-0.25, 0.75, 1.0]]])
+    v5 = np.asarray([[[1.0, -0.5, 0.25, 0.75, -1.0], [0.5, 1.5, -1.0, 0.25, 0.5], [-0.25, 0.75, 1.0, -0.5, 1.25]]])
+    _cmp(mm(*(mt.tensor(a, dtype=mt.float32, device="cuda") for a in (q, k3, v5)), need_weights=False)[0],
+         tm(torch.tensor(q), torch.tensor(k3), torch.tensor(v5), need_weights=False)[0], 1e-5)
+
+
+@pytest.mark.parametrize("dt", ["float32", "float16"])
+def test_mha_sd_shapes_match_torch(dt):
+    """SD-sized attention: 320 channels, 8 heads, 64 queries over 77 text tokens (sequence-first
+    layout, float attn mask, padding mask, causal self-attention, unbatched input)."""
+    torch = _torch()
+    rng = np.random.default_rng(9)
+    E, H, L, S, B = 320, 8, 64, 77, 2
+    params = {"in_proj_weight": rng.standard_normal((3 * E, E)) / np.sqrt(E), "in_proj_bias": rng.standard_normal(3 * E) * 0.1,
+              "out_proj.weight": rng.standard_normal((E, E)) / np.sqrt(E), "out_proj.bias": rng.standard_normal(E) * 0.1}
+    if dt == "float16":  # both sides see the same (fp16-representable) parameters and inputs
+        params = {k: orc.h2f(orc.f2h(np.asarray(v, np.float32))).astype(np.float64) for k, v in params.items()}
+    tm, mm = _pair(params, dtype=dt, embed_dim=E, num_heads=H)
+
+    def inp(*shape):
+        a = rng.standard_normal(shape).astype(np.float32)
+        a = orc.h2f(orc.f2h(a)) if dt == "float16" else a
+        return torch.tensor(a.astype(np.float64)), mt.tensor(a, dtype=getattr(mt, dt), device="cuda")
+
+    tol = 1e-3 if dt == "float32" else 1e-2
+    tq, mq = inp(L, B, E)
+    tk, mk = inp(S, B, E)
+    kpm = np.zeros((B, S), bool)
+    kpm[:, S - 7:] = True
+    fm = rng.standard_normal((L, S)).astype(np.float32) * 0.5
+    to, tw = tm(tq, tk, tk, key_padding_mask=torch.tensor(kpm), attn_mask=torch.tensor(fm.astype(np.float64)))
+    mo, mw = mm(mq, mk, mk, key_padding_mask=mt.from_numpy(kpm).to("cuda"),
+                attn_mask=mt.from_numpy(fm).to("cuda"))
+    assert rel(mo.float().cpu().numpy(), to.detach().numpy()) <= tol
+    assert rel(mw.float().cpu().numpy(), tw.detach().numpy()) <= tol
+    # self-attention through the fused projection, causal
+    causal = np.triu(np.ones((L, L), bool), 1)
+    to, _ = tm(tq, tq, tq, attn_mask=torch.tensor(causal), need_weights=False)
+    mo, _ = mm(mq, mq, mq, attn_mask=mt.from_numpy(causal).to("cuda"), need_weights=False)
+    assert rel(mo.float().cpu().numpy(), to.detach().numpy()) <= tol
+    # unbatched (2-D) input
+    to, tw = tm(tq[:, 0], tk[:, 0], tk[:, 0])
+    mo, mw = mm(mq[:, 0], mk[:, 0], mk[:, 0])
+    assert rel(mo.float().cpu().numpy(), to.detach().numpy()) <= tol
+    assert rel(mw.float().cpu().numpy(), tw.detach().numpy()) <= tol
+
+
+# ------------------------------------------------------------------ save / load
+
+
+def test_save_load_device_tensors_bit_exact(tmp_path):
+    rng = np.random.default_rng(11)
+    h = dev(orc.f2h(rng.standard_normal((5, 7)).astype(np.float32)))
+    f = mt.from_numpy(rng.standard_normal((3, 4)).astype(np.float32)).to("cuda")
+    b = mt.from_numpy(rng.random((6,)) < 0.5).to("cuda")
+    i = mt.from_numpy(rng.integers(-5, 5, (4,)).astype(np.int64)).to("cuda")
+    obj = {"h": h, "nested": (f, [b, i]), "step": 3}
+    path = tmp_path / "ckpt.pt"
+    mt.save(obj, str(path))
+    back = mt.load(str(path), map_location="cuda")
+    assert back["step"] == 3
+    h2, (f2, (b2, i2)) = back["h"], back["nested"]
+    for a, c in ((h, h2), (f, f2), (b, b2), (i, i2)):
+        assert c.device.type == "cuda" and c.dtype is a.dtype and list(c.shape) == list(a.shape)
+    assert np.array_equal(host(h2), host(h))
+    assert np.array_equal(f2.cpu().numpy().view(np.uint32), f.cpu().numpy().view(np.uint32))
+    assert np.array_equal(b2.cpu().numpy(), b.cpu().numpy())
+    assert np.array_equal(i2.cpu().numpy(), i.cpu().numpy())
+    cpu = mt.load(str(path))
+    assert cpu["h"].device.type == "cpu" and np.array_equal(cpu["h"].half_bits(), host(h))
+
+
+def test_module_state_dict_save_load_on_device():
+    """A device module's state_dict saved and loaded into a fresh device module reproduces its
+    outputs exactly."""
+    m1 = mt.nn.MultiheadAttention(64, 4, dtype=mt.float16).to("cuda")
+    rng = np.random.default_rng(12)
+    with mt.no_grad():
+        for p in m1.parameters():
+            p.copy_(mt.from_numpy(rng.standard_normal(list(p.shape)).astype(np.float32) * 0.1).to("cuda"))
+    buf = io.BytesIO()
+    mt.save(m1.state_dict(), buf)
+    buf.seek(0)
+    m2 = mt.nn.MultiheadAttention(64, 4, dtype=mt.float16).to("cuda")
+    m2.load_state_dict(mt.load(buf, map_location="cuda"))
+    x = dev(orc.f2h(rng.standard_normal((10, 2, 64)).astype(np.float32)))
+    o1, w1 = m1(x, x, x)
+    o2, w2 = m2(x, x, x)
+    assert np.array_equal(host(o1), host(o2)) and np.array_equal(host(w1), host(w2))
