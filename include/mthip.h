@@ -283,6 +283,18 @@ int mthip_group_norm_nhwc(int device, int dtype, const void* x, const void* weig
                           void* y_nhwc, int64_t B, int64_t C, int64_t HW, int64_t groups, double eps,
                           int fuse_silu, int param_dtype);
 
+/* group_norm(cat([x0, x1], dim=1)) written channels-last as mthip_group_norm_nhwc writes it,
+ * reading the two NCHW inputs x0[B][C0][HW] and x1[B][C1][HW] in place instead of a
+ * concatenated copy (mtorch's torch.cat, tensor.cpp:32141, followed by group_norm,
+ * tensor.cpp:18643-18963: the input of every SD up-block ResBlock).  raw_nhwc (NULL to skip)
+ * receives the concatenated input itself channels-last, [B][HW][C0+C1] -- the operand of the
+ * block's 1x1 shortcut conv (mthip_conv2d_nhwc).  F16 data only; C0+C1 and HW multiples of 8,
+ * C0 even; y_nhwc and raw_nhwc have C0+C1 channels (no padding). */
+int mthip_group_norm_nhwc_cat(int device, int dtype, const void* x0, int64_t C0, const void* x1,
+                              int64_t C1, const void* weight, const void* bias, void* y_nhwc,
+                              void* raw_nhwc, int64_t B, int64_t HW, int64_t groups, double eps,
+                              int fuse_silu, int param_dtype);
+
 /* layer_norm over the trailing N elements of contiguous x[rows, N] (tensor.cpp:17386-17708;
  * py_layer_norm module.cpp:7461-7516); weight/bias [N] or NULL.  fp16 uses the two-pass
  * centred variance, fp32 the one-pass form, as the reference does.  param_dtype as for

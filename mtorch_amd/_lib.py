@@ -77,6 +77,8 @@ _SIGNATURES = {
                                 _i64, _dbl, _int, _int]),
     "mthip_group_norm_nhwc": (_int, [_int, _int, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i64,
                                      _i64, _dbl, _int, _int]),
+    "mthip_group_norm_nhwc_cat": (_int, [_int, _int, _c_void_p, _i64, _c_void_p, _i64, _c_void_p, _c_void_p, _c_void_p,
+                                          _c_void_p, _i64, _i64, _i64, _dbl, _int, _int]),
     "mthip_layer_norm": (_int, [_int, _int, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i64, _dbl, _int]),
     "mthip_softmax_lastdim": (_int, [_int, _int, _c_void_p, _c_void_p, _i64, _i64, _int]),
     "mthip_generator_create": (_c_void_p, [ctypes.c_uint64]),

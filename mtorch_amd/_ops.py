@@ -737,6 +737,60 @@ def group_norm_silu_conv2d(x: Tensor, num_groups: int, gn_weight: Tensor, gn_bia
     return out
 
 
+def group_norm_silu_conv2d_cat(x0: Tensor, x1: Tensor, num_groups: int, gn_weight: Tensor, gn_bias: Tensor, eps,
+                               w: Tensor, b: Tensor, padding, chan_add: Tensor, shortcut_w: Tensor, shortcut_b: Tensor):
+    """The entry of an SD up-block ResBlock on x = cat([x0, x1], dim=1) (tensor.cpp:32141):
+    returns (group_norm_silu_conv2d(x, ...), conv2d(x, shortcut_w, shortcut_b)) without the
+    concatenated copy -- mthip_group_norm_nhwc_cat reads x0 and x1 in place and writes both the
+    normalised activation and x itself channels-last, and the two convs read those.  Values
+    equal the unfused cat -> group_norm -> silu -> conv2d / conv2d sequence's bit for bit.
+    Returns None when the inputs do not fit the channels-last fp16 kernel (the caller then
+    concatenates)."""
+    if x0.dtype is not T.float16 or x1.dtype is not T.float16 or x0.dim() != 4 or x1.dim() != 4:
+        return None
+    B, C0, H, W = x0.shape
+    C1 = x1.shape[1]
+    C = C0 + C1
+    if list(x1.shape) != [B, C1, H, W] or C % 8 or C0 % 2 or (H * W) % 8 or C % num_groups:
+        return None
+    pdt = _norm_param_dtype("group_norm", x0, gn_weight, gn_bias)
+    _same_dtype("conv2d", [x0, x1, w, b, chan_add, shortcut_w, shortcut_b], "tensors")
+    dev = _gpu("group_norm_silu_conv2d", x0, x1, gn_weight, gn_bias, w, b, chan_add, shortcut_w, shortcut_b)
+    for t in (gn_weight, gn_bias):
+        if t is not None and list(t.shape) != [C]:
+            raise ValueError("group_norm weight and bias must have one entry per channel")
+    O, KH, KW = w.shape[0], w.shape[2], w.shape[3]
+    So = shortcut_w.shape[0]
+    if list(w.shape[1:2]) != [C] or list(shortcut_w.shape[1:]) != [C, 1, 1]:
+        raise ValueError("group_norm_silu_conv2d_cat: weight shapes do not match the concatenated input")
+    ph, pw = _pair(padding, "padding")
+    OH, OW = H + 2 * ph - KH + 1, W + 2 * pw - KW + 1
+    out = _empty([B, O, OH, OW], x0.dtype, dev)
+    sc = _empty([B, So, H, W], x0.dtype, dev)
+    ca, ca_ld = None, 0
+    if chan_add is not None:
+        if list(chan_add.shape) != [B, O]:
+            raise ValueError("group_norm_silu_conv2d: chan_add must be [batch, out_channels]")
+        ok = chan_add.stride(1) == 1 and (B == 1 or chan_add.stride(0) >= O)
+        ca = chan_add if ok else chan_add.contiguous()
+        ca_ld = ca.stride(0) if B > 1 else O
+    L = _L()
+    xn = T._DeviceBuffer(B * H * W * C * 2, dev)
+    raw = T._DeviceBuffer(B * H * W * C * 2, dev)
+    _lib.check(L.mthip_group_norm_nhwc_cat(dev, x0.dtype.code, x0.contiguous().data_ptr(), C0,
+                                           x1.contiguous().data_ptr(), C1, _ptr(_contig(gn_weight)),
+                                           _ptr(_contig(gn_bias)), xn.ptr, raw.ptr, B, H * W, num_groups, float(eps), 1,
+                                           pdt))
+    wp = _conv_packed_weight(w.contiguous(), dev, O, C, KH, KW)
+    _lib.check(L.mthip_conv2d_nhwc(dev, x0.dtype.code, xn.ptr, wp, _ptr(_contig(b)), out.data_ptr(), B, C, H, W, O, KH,
+                                   KW, 1, 1, ph, pw, 1, 1, None, _ptr(ca), ca_ld))
+    swp = _conv_packed_weight(shortcut_w.contiguous(), dev, So, C, 1, 1)
+    _lib.check(L.mthip_conv2d_nhwc(dev, x0.dtype.code, raw.ptr, swp, _ptr(_contig(shortcut_b)), sc.data_ptr(), B, C, H,
+                                   W, So, 1, 1, 1, 1, 0, 0, 1, 1, None, None, 0))
+    del xn, raw  # stream-ordered free: reused only by later work
+    return out, sc
+
+
 def conv2d_tokens(tok: Tensor, w: Tensor, b: Tensor, H: int, W: int, residual: Tensor = None) -> Tensor:
     """1x1 conv of a channels-last token tensor tok[B, H*W, C] to NCHW [B, O, H, W] (+ residual):
     conv2d(tok.reshape(B, H, W, C).permute(0, 3, 1, 2), w, b) without the permute -- the proj_out

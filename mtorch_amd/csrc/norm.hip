@@ -75,24 +75,48 @@ struct Vec16 {
   }
 };
 
-// Per-chunk (sum, sum of squares) of one (sample, group) range.  VECT: the range and the chunk
-// bounds are whole 16-byte vectors.
-template <typename T, bool VECT>
-__global__ __launch_bounds__(256) void group_norm_stats_kernel(const T* __restrict__ x, float2* __restrict__ partial,
+// The GroupNorm input: NCHW x0[B][C0][HW], optionally followed along channels by x1[B][C1][HW]
+// -- the torch.cat([h, skip], dim=1) that feeds an SD up-block ResBlock, read in place.  Within
+// each source a group's channels are consecutive planes, so element i of group (b, g) lies at
+// i < split ? lo + i : hi + (i - split).
+template <typename T>
+struct GnSource {
+  const T* x0;
+  const T* x1;  // nullptr: one source (C1 == 0)
+  int64_t C0, C1, gc, HW, groups;
+  __device__ __forceinline__ void group(int64_t bg, const T*& lo, const T*& hi, int64_t& split) const {
+    const int64_t b = bg / groups, c = (bg - b * groups) * gc;
+    lo = x0 + (b * C0 + c) * HW;
+    const int64_t n0 = c < C0 ? (C0 - c < gc ? C0 - c : gc) : 0;
+    split = n0 * HW;
+    hi = x1 ? x1 + (b * C1 + (c + n0 - C0)) * HW - split : lo;
+  }
+  __device__ __forceinline__ const T* channel(int64_t b, int64_t c) const {
+    return c < C0 ? x0 + (b * C0 + c) * HW : x1 + (b * C1 + (c - C0)) * HW;
+  }
+};
+
+// Per-chunk (sum, sum of squares) of one (sample, group) range.  VECT: the range, the chunk
+// bounds and the source split are whole 16-byte vectors.
+template <typename T, bool VECT, bool CAT>
+__global__ __launch_bounds__(256) void group_norm_stats_kernel(const GnSource<T> src, float2* __restrict__ partial,
                                                                int64_t group_size, int64_t chunk, int splits) {
   __shared__ float red[8];
   const int64_t bg = blockIdx.y;
   const int split = blockIdx.x;
   const int64_t begin = (int64_t)split * chunk;
   const int64_t end = min(begin + chunk, group_size);
-  const T* base = x + bg * group_size;
+  const T* lo = src.x0 + bg * group_size;  // one source: the (sample, group) block is contiguous
+  const T* hi = lo;
+  int64_t cut = group_size;
+  if constexpr (CAT) src.group(bg, lo, hi, cut);
   float s = 0.0f, ss = 0.0f;
   if constexpr (VECT) {
     constexpr int V = Vec16<T>::N;
 #pragma unroll 4
     for (int64_t i = begin + (int64_t)threadIdx.x * V; i < end; i += 256 * V) {
       float f[V];
-      Vec16<T>::load(base + i, f);
+      Vec16<T>::load((i < cut ? lo : hi) + i, f);
 #pragma unroll
       for (int j = 0; j < V; ++j) {
         s += f[j];
@@ -101,7 +125,7 @@ __global__ __launch_bounds__(256) void group_norm_stats_kernel(const T* __restri
     }
   } else {
     for (int64_t i = begin + threadIdx.x; i < end; i += 256) {
-      const float v = Elem<T>::load(base, i);
+      const float v = Elem<T>::load(i < cut ? lo : hi, i);
       s += v;
       ss += v * v;
     }
@@ -329,13 +353,16 @@ const uint16_t* silu_f16_table(int device, hipStream_t s) {
 // word of the pixel's channel row, and each output pixel row leaves as 16-byte stores of
 // 16-byte LDS reads: 4 LDS instructions per thread where an element-wise transpose needs 32.
 // The fused SiLU is a lookup of the narrowed normalised value (silu_f16_table).
-template <typename P>
+// raw (nullable) also receives the input itself channels-last, [B][HW][Cp]: the operand of a
+// 1x1 shortcut conv on the same (concatenated) input.
+template <typename P, bool CAT>
 __global__ __launch_bounds__(256) void group_norm_apply_nhwc_f16_kernel(
-    const uint16_t* __restrict__ x, const P* __restrict__ gamma, const P* __restrict__ beta, uint16_t* __restrict__ y,
-    const float2* __restrict__ partial, int64_t C, int64_t Cp, int64_t groups, int64_t HW, int splits, float eps,
-    const uint16_t* __restrict__ silu_tab) {
+    const GnSource<uint16_t> src, const P* __restrict__ gamma, const P* __restrict__ beta, uint16_t* __restrict__ y,
+    uint16_t* __restrict__ raw, const float2* __restrict__ partial, int64_t C, int64_t Cp, int64_t groups, int64_t HW,
+    int splits, float eps, const uint16_t* __restrict__ silu_tab) {
   constexpr int PW = 36;  // LDS words per pixel row: 64 channels + 8 pad (16-byte aligned rows)
-  __shared__ uint32_t tile[64 * PW];
+  __shared__ uint32_t tile[(CAT ? 2 : 1) * 64 * PW];
+  uint32_t* const raw_tile = tile + 64 * PW;  // CAT only
   __shared__ float2 st_s[64];
   const int64_t b = blockIdx.z;
   const int64_t p0 = (int64_t)blockIdx.x * 64, c0 = (int64_t)blockIdx.y * 64;
@@ -350,7 +377,7 @@ __global__ __launch_bounds__(256) void group_norm_apply_nhwc_f16_kernel(
   auto load_row = [&](int64_t c, float (&f)[8]) {
     if (c < C && pix < HW) {
       // HW % 8 == 0: an octet is either whole or past the end
-      Vec16<uint16_t>::load(x + (b * C + c) * HW + pix, f);
+      Vec16<uint16_t>::load((CAT ? src.channel(b, c) : src.x0 + (b * C + c) * HW) + pix, f);
     } else {
 #pragma unroll
       for (int j = 0; j < 8; ++j) f[j] = 0.0f;
@@ -389,6 +416,7 @@ __global__ __launch_bounds__(256) void group_norm_apply_nhwc_f16_kernel(
         hb = silu_tab[hb];
       }
       tile[(po * 8 + j) * PW + cp] = ha | (hb << 16);
+      if (CAT && raw) raw_tile[(po * 8 + j) * PW + cp] = (uint32_t)f2h_fast(fa[j]) | ((uint32_t)f2h_fast(fb[j]) << 16);
     }
   }
   __syncthreads();
@@ -402,6 +430,13 @@ __global__ __launch_bounds__(256) void group_norm_apply_nhwc_f16_kernel(
       const uint4 hi = *reinterpret_cast<const uint4*>(&tile[pl * PW + q + 4]);
       if (cq + 8 <= Cp) *reinterpret_cast<uint4*>(yr) = lo;
       if (cq + 16 <= Cp) *reinterpret_cast<uint4*>(yr + 8) = hi;
+      if (CAT && raw) {
+        uint16_t* rr = raw + (b * HW + p) * Cp + cq;
+        const uint4 rlo = *reinterpret_cast<const uint4*>(&raw_tile[pl * PW + q]);
+        const uint4 rhi = *reinterpret_cast<const uint4*>(&raw_tile[pl * PW + q + 4]);
+        if (cq + 8 <= Cp) *reinterpret_cast<uint4*>(rr) = rlo;
+        if (cq + 16 <= Cp) *reinterpret_cast<uint4*>(rr + 8) = rhi;
+      }
     }
   }
 }
@@ -668,15 +703,22 @@ __global__ __launch_bounds__(256) void softmax_long_kernel(const T* __restrict__
 
 // Stats (chunked partials), then the apply pass, which folds its group's partials: NCHW as x
 // (y_nhwc == false) or channels-last with Cp channels.
+// x1 (nullable): a second NCHW input of C - C0 channels concatenated after x's C0 channels
+// (channels-last fp16 output only); raw (nullable, channels-last only) receives the input
+// channels-last too.
 template <typename T, typename P>
 int run_group_norm(int device, const void* x, const void* weight, const void* bias, void* y, int64_t B, int64_t C,
-                   int64_t inner, int64_t groups, double eps, int fuse_silu, bool y_nhwc, int64_t Cp, hipStream_t s) {
+                   int64_t inner, int64_t groups, double eps, int fuse_silu, bool y_nhwc, int64_t Cp, hipStream_t s,
+                   const void* x1 = nullptr, int64_t C0 = -1, void* raw = nullptr) {
   const int64_t group_size = (C / groups) * inner;
+  if (C0 < 0) C0 = C;
+  const GnSource<T> src{(const T*)x, (const T*)x1, C0, C - C0, C / groups, inner, groups};
   const int64_t n_groups = B * groups;
   if (n_groups == 0 || group_size == 0) return MTHIP_OK;
   MTHIP_REQUIRE(n_groups <= 65535, "mthip_group_norm: batch*groups must be <= 65535");
   constexpr int V = Vec16<T>::N;
-  const bool vect = ((uintptr_t)x % 16 == 0) && ((uintptr_t)y % 16 == 0) && inner % V == 0;
+  const bool vect = ((uintptr_t)x % 16 == 0) && ((uintptr_t)y % 16 == 0) && inner % V == 0 &&
+                    ((uintptr_t)x1 % 16 == 0);
   // Stats chunks of >= 2048 elements (4-8 KB per workgroup; the SD tensors give >= 4
   // workgroups per CU, all loads in flight at once), at most 64 per group: the apply kernels
   // fold a group's partials themselves.
@@ -687,17 +729,27 @@ int run_group_norm(int device, const void* x, const void* weight, const void* bi
   void* ws = nullptr;
   if (int rc = mthip_malloc(device, (size_t)(n_groups * splits) * sizeof(float2), &ws)) return rc;
   float2* partial = static_cast<float2*>(ws);
+  // The fp16 channels-last apply (the only one that reads two sources or writes `raw`).
+  const bool nhwc_f16 = y_nhwc && sizeof(T) == 2 && ((uintptr_t)x % 16 == 0) && ((uintptr_t)y % 16 == 0) &&
+                        inner % V == 0 && Cp % V == 0 && ((uintptr_t)x1 % 16 == 0) && ((uintptr_t)raw % 16 == 0) &&
+                        C0 % 2 == 0;
+  if ((x1 || raw) && !nhwc_f16) {
+    mthip_free(device, ws);
+    return fail(MTHIP_ERR_UNSUPPORTED, "mthip_group_norm_nhwc_cat: needs fp16, 16-byte aligned rows and an even split");
+  }
   dim3 grid((unsigned)splits, (unsigned)n_groups);
-  if (vect)
-    hipLaunchKernelGGL((group_norm_stats_kernel<T, true>), grid, dim3(256), 0, s, (const T*)x, partial, group_size,
+  const bool cat = x1 != nullptr;
+  if (vect && cat)
+    hipLaunchKernelGGL((group_norm_stats_kernel<T, true, true>), grid, dim3(256), 0, s, src, partial, group_size, chunk,
+                       (int)splits);
+  else if (vect)
+    hipLaunchKernelGGL((group_norm_stats_kernel<T, true, false>), grid, dim3(256), 0, s, src, partial, group_size,
                        chunk, (int)splits);
   else
-    hipLaunchKernelGGL((group_norm_stats_kernel<T, false>), grid, dim3(256), 0, s, (const T*)x, partial, group_size,
+    hipLaunchKernelGGL((group_norm_stats_kernel<T, false, false>), grid, dim3(256), 0, s, src, partial, group_size,
                        chunk, (int)splits);
   int rc = check_launch("group_norm_stats_kernel");
   // The fp16 channels-last apply looks the fused SiLU up in a table (built on first use).
-  const bool nhwc_f16 = y_nhwc && sizeof(T) == 2 && ((uintptr_t)x % 16 == 0) && ((uintptr_t)y % 16 == 0) &&
-                        inner % V == 0 && Cp % V == 0;
   const uint16_t* silu_tab = nullptr;
   if (rc == MTHIP_OK && nhwc_f16 && fuse_silu) {
     silu_tab = silu_f16_table(device, s);
@@ -708,9 +760,14 @@ int run_group_norm(int device, const void* x, const void* weight, const void* bi
       dim3 g2((unsigned)ceil_div(inner, 64), (unsigned)ceil_div(Cp, 64), (unsigned)B);
       // 16-byte row access: pixel rows and channel rows start on 16-byte boundaries.
       const int vec_io = ((uintptr_t)x % 16 == 0) && ((uintptr_t)y % 16 == 0) && inner % V == 0 && Cp % V == 0;
-      if (nhwc_f16)
-        hipLaunchKernelGGL((group_norm_apply_nhwc_f16_kernel<P>), g2, dim3(256), 0, s, (const uint16_t*)x,
-                           (const P*)weight, (const P*)bias, (uint16_t*)y, (const float2*)partial, C, Cp, groups,
+      const GnSource<uint16_t> src16{(const uint16_t*)x, (const uint16_t*)x1, C0, C - C0, C / groups, inner, groups};
+      if (nhwc_f16 && (cat || raw))
+        hipLaunchKernelGGL((group_norm_apply_nhwc_f16_kernel<P, true>), g2, dim3(256), 0, s, src16, (const P*)weight,
+                           (const P*)bias, (uint16_t*)y, (uint16_t*)raw, (const float2*)partial, C, Cp, groups, inner,
+                           (int)splits, (float)eps, silu_tab);
+      else if (nhwc_f16)
+        hipLaunchKernelGGL((group_norm_apply_nhwc_f16_kernel<P, false>), g2, dim3(256), 0, s, src16, (const P*)weight,
+                           (const P*)bias, (uint16_t*)y, (uint16_t*)nullptr, (const float2*)partial, C, Cp, groups,
                            inner, (int)splits, (float)eps, silu_tab);
       else
         hipLaunchKernelGGL((group_norm_apply_nhwc_kernel<T, P>), g2, dim3(256), 0, s, (const T*)x, (const P*)weight,
@@ -839,6 +896,29 @@ int mthip_group_norm_nhwc(int device, int dtype, const void* x, const void* weig
     return run_group_norm<uint16_t, float>(device, x, weight, bias, y_nhwc, B, C, HW, groups, eps, fuse_silu, true, Cp, s);
   return run_group_norm<uint16_t, uint16_t>(device, x, weight, bias, y_nhwc, B, C, HW, groups, eps, fuse_silu, true, Cp,
                                             s);
+}
+
+int mthip_group_norm_nhwc_cat(int device, int dtype, const void* x0, int64_t C0, const void* x1, int64_t C1,
+                              const void* weight, const void* bias, void* y_nhwc, void* raw_nhwc, int64_t B,
+                              int64_t HW, int64_t groups, double eps, int fuse_silu, int param_dtype) {
+  MTHIP_REQUIRE(dtype == MTHIP_F16 && norm_dtypes_ok(dtype, param_dtype),
+                "mthip_group_norm_nhwc_cat: data must be F16 (parameters F16 or F32)");
+  const int64_t C = C0 + C1;
+  MTHIP_REQUIRE(C0 >= 0 && C1 >= 0 && groups > 0 && C % groups == 0,
+                "mthip_group_norm_nhwc_cat: num_channels must be divisible by num_groups");
+  MTHIP_REQUIRE(C1 == 0 || x1 != nullptr, "mthip_group_norm_nhwc_cat: second input missing");
+  MTHIP_REQUIRE(B >= 0 && HW >= 0 && B <= 65535, "mthip_group_norm_nhwc_cat: bad extents");
+  MTHIP_REQUIRE(C % 8 == 0 && C0 % 2 == 0 && HW % 8 == 0,
+                "mthip_group_norm_nhwc_cat: channel counts and HW must allow 16-byte rows");
+  hipStream_t s = stream_for(device);
+  if (!s) return MTHIP_ERR_HIP;
+  if (int rc = use_device(device)) return rc;
+  const void* second = C1 > 0 ? x1 : nullptr;
+  if (param_dtype == MTHIP_F32)
+    return run_group_norm<uint16_t, float>(device, x0, weight, bias, y_nhwc, B, C, HW, groups, eps, fuse_silu, true, C,
+                                           s, second, C0, raw_nhwc);
+  return run_group_norm<uint16_t, uint16_t>(device, x0, weight, bias, y_nhwc, B, C, HW, groups, eps, fuse_silu, true,
+                                            C, s, second, C0, raw_nhwc);
 }
 
 int mthip_layer_norm(int device, int dtype, const void* x, const void* weight, const void* bias, void* y, int64_t rows,

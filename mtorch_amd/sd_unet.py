@@ -153,6 +153,23 @@ class ResBlock(nn.Module):
         return F.group_norm_silu_conv2d(h, n2.groups, n2.weight, n2.bias, n2.eps, self.conv2.weight, self.conv2.bias,
                                         padding=1, residual=res)
 
+    def forward_cat(self, x0: Tensor, x1: Tensor, temb_silu: Tensor, t: Tensor | None = None) -> Tensor:
+        """forward(cat([x0, x1], dim=1), ...) of an up-block ResBlock without the concatenated
+        copy: the first GroupNorm reads both inputs in place and also hands the shortcut conv its
+        channels-last operand."""
+        n1, n2 = self.norm1, self.norm2
+        if t is None:
+            t = F.linear(temb_silu, self.time_emb_proj.weight, self.time_emb_proj.bias)
+        r = None
+        if self.shortcut is not None:
+            r = _ops.group_norm_silu_conv2d_cat(x0, x1, n1.groups, n1.weight, n1.bias, n1.eps, self.conv1.weight,
+                                                self.conv1.bias, 1, t, self.shortcut.weight, self.shortcut.bias)
+        if r is None:
+            return self.forward(_ops.cat([x0, x1], dim=1), temb_silu, t)
+        h, res = r
+        return F.group_norm_silu_conv2d(h, n2.groups, n2.weight, n2.bias, n2.eps, self.conv2.weight, self.conv2.bias,
+                                        padding=1, residual=res)
+
 
 class Attention(nn.Module):
     def __init__(self, init: _Init, C: int, ctx: int | None, heads: int = 8):
@@ -359,7 +376,8 @@ class UNet(nn.Module):
             i = 0
             while i < len(items):
                 if isinstance(items[i], ResBlock):
-                    h = res(items[i], mt.cat([h, skips.pop()], dim=1))
+                    blk = items[i]
+                    h = blk.forward_cat(h, skips.pop(), temb_silu, t_of[id(blk)])
                     if i + 1 < len(items) and isinstance(items[i + 1], SpatialTransformer):
                         i += 1
                         h = xf(items[i], h)
