@@ -616,6 +616,28 @@ def test_group_norm_silu_conv2d_cat_equals_cat_then_ops(B, C0, C1, H, W, O, G, p
                                            dev(sb)) is None
 
 
+@pytest.mark.parametrize("B,C,H,W,G,pdt", [(2, 1280, 8, 8, 32, "float16"), (2, 640, 16, 16, 32, "float16"),
+                                            (2, 960, 16, 16, 32, "float32"), (1, 64, 8, 8, 8, "float16"),
+                                            (2, 320, 32, 32, 32, "float16"), (2, 2560, 8, 8, 32, "float16")])
+def test_group_norm_channels_last_equals_nchw_bit_for_bit(B, C, H, W, G, pdt):
+    """The channels-last GroupNorm (stats + transposing apply) writes exactly the values of the
+    NCHW group_norm, permuted, at every SD latent size."""
+    from mtorch_amd import sd_unet
+
+    g = Gen(B + C + H)
+    x = g.randn((B, C, H, W), "float16")
+    gamma, beta = g.randn((C,), pdt), g.randn((C,), pdt)
+
+    class Norm:
+        weight, bias, groups, eps = dev(gamma), dev(beta), G, 1e-5
+
+    tok = host(sd_unet._tokens_nhwc(dev(x), Norm))
+    from mtorch_amd import _ops
+
+    ref = host(_ops.group_norm(dev(x), G, dev(gamma), dev(beta), 1e-5, allow_upcast=True))
+    assert np.array_equal(tok, np.ascontiguousarray(ref.transpose(0, 2, 3, 1)).reshape(B, H * W, C))
+
+
 def test_sd_group_norm_scenario_fixture():
     hidden, w, b = closed_form.sd_group_norm_inputs()
     exp = np.load(os.path.join(HERE, "golden", "sd_group_norm_1x320x16x16.npz"))["y"]
