@@ -426,3 +426,42 @@ def test_module_state_dict_save_load_on_device():
     o1, w1 = m1(x, x, x)
     o2, w2 = m2(x, x, x)
     assert np.array_equal(host(o1), host(o2)) and np.array_equal(host(w1), host(w2))
+
+
+# ------------------------------------------------------------------ edge cases
+
+
+def test_empty_and_degenerate_inputs():
+    """Zero-size tensors and zero-length contractions, as the reference's own edge cases have
+    them: empty results keep their shapes, an empty contraction sums to zero."""
+    e = mt.zeros((0, 5), dtype=mt.float16, device="cuda")
+    m = mt.ones((0, 5), dtype=mt.bool, device="cuda")
+    out = e.masked_fill(m, 1.0)
+    assert list(out.shape) == [0, 5]
+    assert list((~m).shape) == [0, 5]
+    e[:, 1:] = 3.0  # filling an empty view is a no-op
+    a = mt.zeros((4, 0), dtype=mt.float32, device="cuda")
+    b = mt.zeros((0, 6), dtype=mt.float32, device="cuda")
+    z = mt.einsum("ij,jk->ik", a, b)
+    assert list(z.shape) == [4, 6] and not np.any(z.cpu().numpy())
+    z = mt.einsum("bij,bjk->bik", mt.zeros((0, 3, 4), device="cuda"), mt.zeros((0, 4, 2), device="cuda"))
+    assert list(z.shape) == [0, 3, 2]
+    buf = io.BytesIO()
+    mt.save({"t": mt.zeros((2, 3), dtype=mt.float16, device="cuda"), "s": mt.tensor(1.5).to("cuda")}, buf)
+    buf.seek(0)
+    back = mt.load(buf, map_location="cuda")
+    assert list(back["t"].shape) == [2, 3] and back["s"].dim() == 0 and back["s"].item() == 1.5
+
+
+def test_mha_eval_mode_and_dropout_in_training():
+    """dropout applies only in training mode (the reference's SDPA path); eval() and dropout=0
+    give the deterministic result."""
+    m = mt.nn.MultiheadAttention(16, 2, dropout=0.5).to("cuda")
+    x = mt.from_numpy(np.random.default_rng(1).standard_normal((5, 1, 16)).astype(np.float32)).to("cuda")
+    m.eval()
+    o1, _ = m(x, x, x)
+    o2, _ = m(x, x, x)
+    assert np.array_equal(o1.cpu().numpy(), o2.cpu().numpy())
+    m.train()
+    with pytest.raises(ValueError, match="dropout"):
+        m(x, x, x)
