@@ -102,3 +102,21 @@ def test_unet_graph_replay_matches_eager(unet_case):
             assert np.array_equal(out.cpu().half_bits(), eager)
             model(latent, t, ctx)  # eager work between replays
         g.reset()
+
+
+def test_denoising_loop_reuses_device_memory(unet_case):
+    """A multi-step denoising loop (latent <- latent - 0.1 * eps, three eager UNet steps) runs
+    on the cached blocks of the first step: reserved device memory does not grow after it, and
+    every step releases what it allocated."""
+    model, latent, t, ctx = unet_case
+    with mt.no_grad():
+        x = latent.clone()
+        x = x - model(x, t, ctx) * 0.1  # first step: fills the cache
+        mt.cuda.synchronize()
+        alloc0, reserved0 = mt.cuda.memory_allocated(), mt.cuda.memory_reserved()
+        for _ in range(3):
+            x = x - model(x, t, ctx) * 0.1
+            mt.cuda.synchronize()
+            assert mt.cuda.memory_reserved() == reserved0
+            assert mt.cuda.memory_allocated() == alloc0
+    assert np.isfinite(x.cpu().float().numpy()).all()
