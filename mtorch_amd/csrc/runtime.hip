@@ -7,6 +7,7 @@
 #include <mutex>
 #include <string>
 #include <unordered_map>
+#include <utility>
 #include <vector>
 
 #include "common.h"
@@ -20,10 +21,12 @@ constexpr int kMaxDevices = 64;
 
 struct DeviceState {
   hipStream_t stream = nullptr;
-  // Caching allocator: free blocks keyed by size; live blocks map ptr -> size.
+  // Caching allocator: free blocks keyed by size; live blocks map ptr -> (block size, rounded
+  // request).  A reused block may be up to 25% larger than the request; `allocated` counts the
+  // rounded requests, so it does not depend on which cached block a request happened to get.
   std::multimap<size_t, void*> free_blocks;
-  std::unordered_map<void*, size_t> live;
-  size_t allocated = 0;  // bytes in live blocks
+  std::unordered_map<void*, std::pair<size_t, size_t>> live;
+  size_t allocated = 0;  // rounded request bytes of live blocks
   size_t reserved = 0;   // bytes obtained from hipMalloc and not yet returned
   // Stream capture: blocks freed while a capture is open (or handed out during it) belong to
   // the graph being recorded and may only be reused inside the same capture.
@@ -180,8 +183,8 @@ int mthip_malloc(int device, size_t nbytes, void** ptr) {
     d.reserved += size;
     b = Block{p, size};
   }
-  d.live[b.ptr] = b.size;
-  d.allocated += b.size;
+  d.live[b.ptr] = {b.size, size};
+  d.allocated += size;
   if (d.capturing) d.capture_touched[b.ptr] = b.size;
   *ptr = b.ptr;
   return MTHIP_OK;
@@ -194,9 +197,9 @@ int mthip_free(int device, void* ptr) {
   DeviceState& d = g_devices[device];
   auto it = d.live.find(ptr);
   if (it == d.live.end()) return fail(MTHIP_ERR_INVALID, "mthip_free: pointer not allocated by mthip_malloc");
-  const size_t size = it->second;
+  const size_t size = it->second.first;
+  d.allocated -= it->second.second;
   d.live.erase(it);
-  d.allocated -= size;
   if (d.capturing) {
     // Reusable only inside this capture; afterwards the graph keeps it.
     d.capture_free.emplace(size, ptr);

@@ -3,6 +3,7 @@ float32 CPU evaluation of the same composition with the same weights: cosine sim
 >= 0.9999 (north_star's UNet bar) and normwise error within the fp16 tolerance; plus
 HIP-graph replays of the whole UNet step matching the eager step bit for bit."""
 
+import gc
 import os
 import sys
 
@@ -110,9 +111,14 @@ def test_denoising_loop_reuses_device_memory(unet_case):
     every step releases what it allocated."""
     model, latent, t, ctx = unet_case
     with mt.no_grad():
+        # Device tensors that earlier tests left in reference cycles are released by the
+        # collector, not by the loop: collect them first so they do not show up as the
+        # loop's own frees.
+        gc.collect()
         x = latent.clone()
         x = x - model(x, t, ctx) * 0.1  # first step: fills the cache
         mt.cuda.synchronize()
+        gc.collect()
         alloc0, reserved0 = mt.cuda.memory_allocated(), mt.cuda.memory_reserved()
         for _ in range(3):
             x = x - model(x, t, ctx) * 0.1
