@@ -1,6 +1,6 @@
 """Benchmark of mtorch's SD-UNet hot path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload resnet|linear_gelu|unet|copy_calibration] [--no-cpu]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload resnet|linear_gelu|unet|copy_calibration|suite] [--no-cpu]
 
 Default workload (fp16 leg): the SD ResNet sub-block on a 64x64
 latent at batch 2 -- x[2,320,64,64] -> GroupNorm(32, eps 1e-5, affine) -> SiLU ->
@@ -296,12 +296,134 @@ def run_unet(args):
     }
 
 
+def _suite_row(name, fn, reps, flops=None, nbytes=None, bound="mfma", peak=None, graph=True):
+    """Time one op: a HIP graph of `reps` back-to-back calls replayed once (so launch gaps do
+    not count against short kernels), averaged per call; then price it against its roofline."""
+    import mtorch_amd as mt
+
+    fn()
+    mt.cuda.synchronize()
+    if graph:
+        g = mt.cuda.CUDAGraph()
+        with mt.cuda.graph(g):
+            for _ in range(reps):
+                fn()
+        g.replay()
+        ms = _time_events(g.replay, 5) / reps
+    else:
+        ms = _time_events(fn, reps)
+    row = {"op": name, "us": round(ms * 1e3, 2), "bound": bound}
+    if flops is not None:
+        row["tflops"] = round(flops / (ms * 1e-3) / 1e12, 2)
+    if nbytes is not None:
+        row["gbs"] = round(nbytes / (ms * 1e-3) / 1e9, 1)
+    if bound == "mfma":
+        row["frac"] = round(row["tflops"] / (peak or PEAK["fp16_mfma_tflops"]), 4)
+    else:
+        row["frac"] = round(row["gbs"] / PEAK["hbm_gbs"], 4)
+    print(json.dumps(row), file=sys.stderr, flush=True)
+    return row
+
+
+def run_suite(args):
+    """Every op row of the hot path at its SD-1.5 shape (BASELINE.json configs[0]-[3]), each
+    priced against the roofline that bounds it: contractions in TFLOP/s against MFMA peak,
+    normalisation / softmax / elementwise in GB/s of algorithmic bytes (read once, written once)
+    against HBM peak.  The HBM-bound ops are also timed on a 64x larger batch, where the
+    working set no longer fits the 256 MB Infinity Cache and a launch lasts long enough for
+    its ramp-up not to dominate."""
+    import mtorch_amd as mt
+    from mtorch_amd import sd_unet
+
+    F = mt.nn.functional
+    mt.manual_seed(0)
+    reps = 20
+    rows = []
+
+    def rnd(*shape, dt=mt.float16, scale=1.0):
+        t = mt.randn(*shape).to("cuda")
+        if scale != 1.0:
+            t = t * scale
+        return t.to(dt)
+
+    # configs[0]: linear + GELU, fp32 and fp16.
+    for dt, peak, tag in ((mt.float32, PEAK["fp32_tflops"], "fp32"), (mt.float16, None, "fp16")):
+        x, w, b = rnd(8192, 320, dt=dt), rnd(1280, 320, dt=dt, scale=0.05), rnd(1280, dt=dt, scale=0.05)
+        rows.append(_suite_row(f"linear+gelu {tag} [8192,320]x[1280,320]^T", lambda: F.linear_gelu(x, w, b),
+                               reps, flops=2.0 * 8192 * 1280 * 320, peak=peak))
+    # configs[1]: the ResNet sub-block pieces.
+    for dt, esz, tag in ((mt.float32, 4, "fp32"), (mt.float16, 2, "fp16")):
+        for nb in (2, 128):
+            x = rnd(nb, 320, 64, 64, dt=dt)
+            g, bb = rnd(320, dt=dt), rnd(320, dt=dt)
+            n = nb * 320 * 64 * 64
+            rows.append(_suite_row(f"group_norm(32) {tag} [{nb},320,64,64]", lambda: F.group_norm(x, 32, g, bb, 1e-5),
+                                   reps if nb == 2 else 3, nbytes=2 * n * esz, bound="hbm"))
+            rows.append(_suite_row(f"group_norm(32)+silu {tag} [{nb},320,64,64]",
+                                   lambda: F.group_norm_silu(x, 32, g, bb, 1e-5),
+                                   reps if nb == 2 else 3, nbytes=2 * n * esz, bound="hbm"))
+            y = rnd(nb, 320, 64, 64, dt=dt)
+            rows.append(_suite_row(f"add {tag} [{nb},320,64,64]", lambda: x + y, reps if nb == 2 else 3,
+                                   nbytes=3 * n * esz, bound="hbm"))
+            rows.append(_suite_row(f"silu {tag} [{nb},320,64,64]", lambda: F.silu(x), reps if nb == 2 else 3,
+                                   nbytes=2 * n * esz, bound="hbm"))
+            rows.append(_suite_row(f"gelu {tag} [{nb},320,64,64]", lambda: F.gelu(x), reps if nb == 2 else 3,
+                                   nbytes=2 * n * esz, bound="hbm"))
+            del x, y
+    xs = rnd(2, 320, 64, 64)
+    ws, bs = rnd(320, 320, 3, 3, scale=0.02), rnd(320, scale=0.02)
+    rows.append(_suite_row("conv2d 3x3 fp16 [2,320,64,64] 320->320", lambda: F.conv2d(xs, ws, bs, padding=1),
+                           reps, flops=2.0 * 2 * 4096 * 320 * 2880))
+    for C, hw in ((640, 32), (1280, 16), (1280, 8)):
+        xc = rnd(2, C, hw, hw)
+        wc, bc = rnd(C, C, 3, 3, scale=0.02), rnd(C, scale=0.02)
+        rows.append(_suite_row(f"conv2d 3x3 fp16 [2,{C},{hw},{hw}] {C}->{C}",
+                               lambda: F.conv2d(xc, wc, bc, padding=1), reps, flops=2.0 * 2 * hw * hw * C * C * 9))
+    # configs[2]: attention, self and cross, at the three latent sizes.
+    for L, C, E in ((4096, 320, 40), (1024, 640, 80), (256, 1280, 160)):
+        q, k, v = rnd(2, 8, L, E), rnd(2, 8, L, E), rnd(2, 8, L, E)
+        rows.append(_suite_row(f"sdpa self fp16 [2,8,{L},{E}]",
+                               lambda: F.scaled_dot_product_attention(q, k, v), reps,
+                               flops=4.0 * 2 * 8 * L * L * E))
+        kc, vc = rnd(2, 8, 77, E), rnd(2, 8, 77, E)
+        nbytes = 2 * (2 * 2 * 8 * L * E + 2 * 2 * 8 * 77 * E)
+        rows.append(_suite_row(f"sdpa cross fp16 [2,8,{L},{E}] x 77 keys",
+                               lambda: F.scaled_dot_product_attention(q, kc, vc), reps,
+                               flops=4.0 * 2 * 8 * L * 77 * E, nbytes=nbytes, bound="hbm"))
+    # softmax / layer_norm rows (attention scores of the legacy path, transformer tokens).
+    for rws, N in ((2 * 8 * 4096, 77), (2 * 8 * 1024, 1024), (2 * 8 * 4096 * 8, 1024)):
+        s = rnd(rws, N)
+        rows.append(_suite_row(f"softmax fp16 [{rws},{N}]", lambda: F.softmax(s, dim=-1), reps,
+                               nbytes=2 * rws * N * 2, bound="hbm"))
+        del s
+    for rws, C in ((8192, 320), (2048, 640), (8192 * 64, 320)):
+        t = rnd(rws, C)
+        lw, lb = rnd(C), rnd(C)
+        rows.append(_suite_row(f"layer_norm fp16 [{rws},{C}]", lambda: F.layer_norm(t, (C,), lw, lb, 1e-5), reps,
+                               nbytes=2 * rws * C * 2, bound="hbm"))
+        del t
+    # configs[3]: the SpatialTransformer block at 32x32.
+    mt.manual_seed(0)
+    st = sd_unet.SpatialTransformer(sd_unet._Init("cuda"), 640)
+    xt, ctx = rnd(2, 640, 32, 32), rnd(2, 77, 768)
+    rows.append(_suite_row("SpatialTransformer fp16 [2,640,32,32] ctx [2,77,768]", lambda: st(xt, ctx), 5,
+                           flops=39.63e9))
+    mfma = [r for r in rows if r["bound"] == "mfma"]
+    return {
+        "metric": "per-op TFLOP/s (vs fp16/fp32 MFMA peak) and GB/s (vs HBM peak) at the SD-1.5 shapes",
+        "value": round(sum(r["frac"] for r in mfma) / len(mfma), 4), "unit": "mean MFMA fraction",
+        "n_gpus": 1, "steps": reps, "warmup": 1, "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "fp16", "data": "synthetic (mtorch generator, seed 0)",
+        "config": {"workload": "configs[0]-[3] op rows, each graph-replayed x20"}, "rows": rows,
+    }
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", default="resnet", choices=["resnet", "linear_gelu", "unet", "copy_calibration"])
+    ap.add_argument("--workload", default="resnet", choices=["resnet", "linear_gelu", "unet", "copy_calibration", "suite"])
     ap.add_argument("--no-cpu", dest="cpu", action="store_false")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -314,7 +436,7 @@ def main():
         raise SystemExit("bench.py: no GPU visible to libmthip")
     with mt.no_grad():
         run = {"resnet": run_resnet, "linear_gelu": run_linear_gelu, "unet": run_unet,
-               "copy_calibration": run_copy_calibration}
+               "copy_calibration": run_copy_calibration, "suite": run_suite}
         out = run[args.workload](args)
     out["device"] = mt.cuda.get_device_name(0)
     print(json.dumps(out), flush=True)

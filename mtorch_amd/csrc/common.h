@@ -37,6 +37,9 @@ hipStream_t stream_for(int device);
 int use_device(int device);
 // After a kernel launch: turns a launch error into a status.
 int check_launch(const char* what);
+// 65536-entry fp16 table of erf-gelu indexed by the input's bits, bit-identical to evaluating
+// it; filled on first use per device (nullptr if that failed).
+const uint16_t* gelu_f16_lookup(int device, hipStream_t s);
 
 __host__ __device__ inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 

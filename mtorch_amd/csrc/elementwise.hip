@@ -298,6 +298,60 @@ __global__ void unary_kernel(int op, const T* __restrict__ x, T* __restrict__ y,
     Elem<T>::store(y, i, apply_unary<T>(op, Elem<T>::load(x, i)));
 }
 
+// 16-byte chunks per lane (8 halves or 4 floats) over 16-byte aligned buffers, the op fixed at
+// compile time.  With `tab` (fp16 erf-gelu, whose evaluation needs a double-precision erf) each
+// half is looked up by its bits instead.
+template <typename T, int OP>
+__global__ void unary_vec_kernel(const uint4* __restrict__ x, uint4* __restrict__ y, int64_t nvec,
+                                 const uint16_t* __restrict__ tab) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < nvec; i += stride) {
+    uint4 r = x[i];
+    uint32_t w[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if constexpr (sizeof(T) == 2) {
+        uint32_t lo = w[j] & 0xffffu, hi = w[j] >> 16;
+        if (tab) {
+          lo = tab[lo];
+          hi = tab[hi];
+        } else if constexpr (OP == MTHIP_UNARY_SILU) {
+          lo = silu_half((uint16_t)lo);
+          hi = silu_half((uint16_t)hi);
+        } else {
+          lo = f2h_fast(apply_unary<T>(OP, h2f_bits((uint16_t)lo)));
+          hi = f2h_fast(apply_unary<T>(OP, h2f_bits((uint16_t)hi)));
+        }
+        w[j] = lo | (hi << 16);
+      } else {
+        w[j] = __float_as_uint(apply_unary<T>(OP, __uint_as_float(w[j])));
+      }
+    }
+    y[i] = make_uint4(w[0], w[1], w[2], w[3]);
+  }
+}
+
+template <typename T>
+void launch_unary_vec(int op, const void* x, void* y, int64_t nvec, const uint16_t* tab, hipStream_t s) {
+  const dim3 grid(grid_for(nvec, 2)), block(kThreads);
+  const uint4* xv = (const uint4*)x;
+  uint4* yv = (uint4*)y;
+  switch (op) {
+#define MTHIP_UNARY_CASE(K) \
+    case K: hipLaunchKernelGGL((unary_vec_kernel<T, K>), grid, block, 0, s, xv, yv, nvec, tab); break;
+    MTHIP_UNARY_CASE(MTHIP_UNARY_SILU)
+    MTHIP_UNARY_CASE(MTHIP_UNARY_GELU)
+    MTHIP_UNARY_CASE(MTHIP_UNARY_GELU_TANH)
+    MTHIP_UNARY_CASE(MTHIP_UNARY_EXP)
+    MTHIP_UNARY_CASE(MTHIP_UNARY_SIN)
+    MTHIP_UNARY_CASE(MTHIP_UNARY_COS)
+    MTHIP_UNARY_CASE(MTHIP_UNARY_NEG)
+    MTHIP_UNARY_CASE(MTHIP_UNARY_SIGMOID)
+    default: MTHIP_UNARY_CASE(MTHIP_UNARY_RELU)
+#undef MTHIP_UNARY_CASE
+  }
+}
+
 template <typename T>
 __global__ void geglu_kernel(const T* __restrict__ x, T* __restrict__ y, int64_t rows, int64_t D) {
   const int64_t n = rows * D;
@@ -674,10 +728,25 @@ int mthip_unary(int device, int op, int dtype, const void* x, void* y, int64_t n
   hipStream_t s = stream_for(device);
   if (!s) return MTHIP_ERR_HIP;
   if (int rc = use_device(device)) return rc;
-  if (dtype == MTHIP_F16)
-    hipLaunchKernelGGL(unary_kernel<uint16_t>, dim3(grid_for(n)), dim3(kThreads), 0, s, op, (const uint16_t*)x, (uint16_t*)y, n);
-  else
-    hipLaunchKernelGGL(unary_kernel<float>, dim3(grid_for(n)), dim3(kThreads), 0, s, op, (const float*)x, (float*)y, n);
+  const int esz = dtype == MTHIP_F16 ? 2 : 4;
+  int64_t done = 0;
+  if ((((uintptr_t)x | (uintptr_t)y) & 15) == 0 && n * esz >= 16) {
+    const int64_t nvec = n * esz / 16;
+    if (dtype == MTHIP_F16)
+      launch_unary_vec<uint16_t>(op, x, y, nvec, op == MTHIP_UNARY_GELU ? gelu_f16_lookup(device, s) : nullptr, s);
+    else
+      launch_unary_vec<float>(op, x, y, nvec, nullptr, s);
+    done = nvec * 16 / esz;
+  }
+  if (done < n) {
+    const int64_t rest = n - done;
+    if (dtype == MTHIP_F16)
+      hipLaunchKernelGGL(unary_kernel<uint16_t>, dim3(grid_for(rest)), dim3(kThreads), 0, s, op,
+                         (const uint16_t*)x + done, (uint16_t*)y + done, rest);
+    else
+      hipLaunchKernelGGL(unary_kernel<float>, dim3(grid_for(rest)), dim3(kThreads), 0, s, op,
+                         (const float*)x + done, (float*)y + done, rest);
+  }
   return check_launch("mthip_unary");
 }
 

@@ -311,6 +311,8 @@ const uint16_t* gelu_f16_table(int device, hipStream_t s) {
 
 }  // namespace
 
+const uint16_t* gelu_f16_lookup(int device, hipStream_t s) { return gelu_f16_table(device, s); }
+
 // Shared with conv.hip.  The fast im2col (tap bitmasks) needs Cp % BK == 0 and <= 32 taps.
 int launch_conv_gemm(int device, int dtype, const GemmArgs& a, hipStream_t s) {
   // With the padded channel count a multiple of BK, no K tile straddles two filter taps.

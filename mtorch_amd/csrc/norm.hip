@@ -677,6 +677,57 @@ __global__ __launch_bounds__(256) void softmax_kernel(const T* __restrict__ x, T
   }
 }
 
+// Rows whose length is a whole number of 16-byte chunks, 16-byte aligned: one wave per row,
+// each lane holding CPL chunks (lane + 64 j) in registers, so every load and store moves 16 bytes
+// per lane.
+template <typename T, int CPL>
+__global__ __launch_bounds__(256) void softmax_vec_kernel(const T* __restrict__ x, T* __restrict__ y, int64_t rows,
+                                                          int64_t cols, int divide) {
+  constexpr int V = Vec16<T>::N;
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int chunks = (int)(cols / V);
+  const T* xr = x + row * cols;
+  float v[CPL][V];
+  float mx = -INFINITY;
+#pragma unroll
+  for (int j = 0; j < CPL; ++j) {
+    const int c = lane + 64 * j;
+    if (c < chunks) {
+      Vec16<T>::load(xr + (int64_t)c * V, v[j]);
+    } else {
+#pragma unroll
+      for (int q = 0; q < V; ++q) v[j][q] = -INFINITY;
+    }
+#pragma unroll
+    for (int q = 0; q < V; ++q) mx = fmaxf(mx, v[j][q]);
+  }
+  mx = wave_max(mx);
+  float s = 0.0f;
+#pragma unroll
+  for (int j = 0; j < CPL; ++j) {
+    const bool in = lane + 64 * j < chunks;
+#pragma unroll
+    for (int q = 0; q < V; ++q) {
+      v[j][q] = in ? expf(v[j][q] - mx) : 0.0f;
+      s += v[j][q];
+    }
+  }
+  s = wave_sum(s);
+  const float inv = 1.0f / s;
+  T* yr = y + row * cols;
+#pragma unroll
+  for (int j = 0; j < CPL; ++j) {
+    const int c = lane + 64 * j;
+    if (c < chunks) {
+#pragma unroll
+      for (int q = 0; q < V; ++q) v[j][q] = divide ? v[j][q] / s : v[j][q] * inv;
+      Vec16<T>::store(yr + (int64_t)c * V, v[j]);
+    }
+  }
+}
+
 template <typename T>
 __global__ __launch_bounds__(256) void softmax_long_kernel(const T* __restrict__ x, T* __restrict__ y, int64_t cols,
                                                            int divide) {
@@ -840,7 +891,18 @@ template <typename T>
 int run_softmax(const void* x, void* y, int64_t rows, int64_t cols, int divide, hipStream_t s) {
   if (rows == 0 || cols == 0) return MTHIP_OK;
   const unsigned grid4 = (unsigned)ceil_div(rows, 4);
-  if (cols <= 64 * 4)
+  constexpr int V = Vec16<T>::N;
+  const int64_t chunks = cols / V;
+  if (cols % V == 0 && (((uintptr_t)x | (uintptr_t)y) & 15) == 0 && chunks <= 64 * 8) {
+    if (chunks <= 64)
+      hipLaunchKernelGGL((softmax_vec_kernel<T, 1>), dim3(grid4), dim3(256), 0, s, (const T*)x, (T*)y, rows, cols, divide);
+    else if (chunks <= 128)
+      hipLaunchKernelGGL((softmax_vec_kernel<T, 2>), dim3(grid4), dim3(256), 0, s, (const T*)x, (T*)y, rows, cols, divide);
+    else if (chunks <= 256)
+      hipLaunchKernelGGL((softmax_vec_kernel<T, 4>), dim3(grid4), dim3(256), 0, s, (const T*)x, (T*)y, rows, cols, divide);
+    else
+      hipLaunchKernelGGL((softmax_vec_kernel<T, 8>), dim3(grid4), dim3(256), 0, s, (const T*)x, (T*)y, rows, cols, divide);
+  } else if (cols <= 64 * 4)
     hipLaunchKernelGGL((softmax_kernel<T, 4>), dim3(grid4), dim3(256), 0, s, (const T*)x, (T*)y, rows, cols, divide);
   else if (cols <= 64 * 16)
     hipLaunchKernelGGL((softmax_kernel<T, 16>), dim3(grid4), dim3(256), 0, s, (const T*)x, (T*)y, rows, cols, divide);
@@ -852,6 +914,7 @@ int run_softmax(const void* x, void* y, int64_t rows, int64_t cols, int divide, 
 }
 
 }  // namespace
+
 }  // namespace mthip
 
 using namespace mthip;
