@@ -212,6 +212,21 @@ __global__ __launch_bounds__(256) void group_norm_apply_kernel(const T* __restri
       const float bt = beta ? Elem<P>::load(beta, c) : 0.0f;
       float f[V];
       Vec16<T>::load(xb + i, f);
+      if constexpr (sizeof(T) == 2) {
+        if (fuse_silu) {
+          // Narrow the normalised value once and apply the fp16 SiLU to its bits: the same
+          // halves as narrowing, widening, SiLU and narrowing again, with one conversion.
+          uint32_t w[4];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const uint32_t lo = silu_half(f2h_fast(gn_value<T, P>(f[2 * j], mean, inv, gm, bt, 0)));
+            const uint32_t hi = silu_half(f2h_fast(gn_value<T, P>(f[2 * j + 1], mean, inv, gm, bt, 0)));
+            w[j] = lo | (hi << 16);
+          }
+          *reinterpret_cast<uint4*>(yb + i) = make_uint4(w[0], w[1], w[2], w[3]);
+          continue;
+        }
+      }
 #pragma unroll
       for (int j = 0; j < V; ++j) f[j] = gn_value<T, P>(f[j], mean, inv, gm, bt, fuse_silu);
       Vec16<T>::store(yb + i, f);

@@ -634,6 +634,18 @@ def test_group_norm_silu_conv2d_cat_equals_cat_then_ops(B, C0, C1, H, W, O, G, p
                                            dev(sb)) is None
 
 
+@pytest.mark.parametrize("shape,groups", [((2, 320, 64, 64), 32), ((1, 640, 16, 16), 32), ((2, 64, 7, 9), 8)])
+def test_group_norm_silu_fp16_equals_group_norm_then_silu(shape, groups):
+    """The fused fp16 GroupNorm+SiLU (SiLU applied to the narrowed halves) writes exactly the
+    halves of group_norm followed by silu."""
+    g = Gen(sum(shape) + groups)
+    x = g.randn(shape, "float16", 2.0)
+    w, b = g.randn((shape[1],), "float16"), g.randn((shape[1],), "float16")
+    fused = host(F.group_norm_silu(dev(x), groups, dev(w), dev(b), 1e-5))
+    sep = host(F.silu(F.group_norm(dev(x), groups, dev(w), dev(b), 1e-5)))
+    assert np.array_equal(fused, sep)
+
+
 @pytest.mark.parametrize("B,C,H,W,G,pdt", [(2, 1280, 8, 8, 32, "float16"), (2, 640, 16, 16, 32, "float16"),
                                             (2, 960, 16, 16, 32, "float32"), (1, 64, 8, 8, 8, "float16"),
                                             (2, 320, 32, 32, 32, "float16"), (2, 2560, 8, 8, 32, "float16")])
