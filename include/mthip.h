@@ -100,6 +100,13 @@ int mthip_cast(int device, int src_dtype, const void* src, int dst_dtype, void* 
 int mthip_copy_strided(int device, int dtype, const void* src, int rank, const int64_t* sizes,
                        const int64_t* src_strides, void* dst);
 
+/* dst viewed through dst_strides <- src viewed through src_strides (element units, same sizes,
+ * rank <= 8, 0 strides broadcast the source).  The two views must not overlap.  Serves copy_ and
+ * item assignment into a non-contiguous view (Tensor::copy_from, tensor.cpp:8292-8340;
+ * Tensor.__setitem__ with a tensor value). */
+int mthip_copy_strided_to(int device, int dtype, const void* src, const int64_t* src_strides, int rank,
+                          const int64_t* sizes, void* dst, const int64_t* dst_strides);
+
 /* dst[i] = value for n contiguous elements.  Serves full/zeros/ones/fill_ (tensor.h:143-149). */
 int mthip_fill(int device, int dtype, void* dst, int64_t n, double value);
 

@@ -46,6 +46,7 @@ _SIGNATURES = {
     "mthip_event_destroy": (_int, [_c_void_p]),
     "mthip_cast": (_int, [_int, _int, _c_void_p, _int, _c_void_p, _i64]),
     "mthip_copy_strided": (_int, [_int, _int, _c_void_p, _int, _i64p, _i64p, _c_void_p]),
+    "mthip_copy_strided_to": (_int, [_int, _int, _c_void_p, _i64p, _int, _i64p, _c_void_p, _i64p]),
     "mthip_fill": (_int, [_int, _int, _c_void_p, _i64, _dbl]),
     "mthip_fill_strided": (_int, [_int, _int, _c_void_p, _int, _i64p, _i64p, _dbl]),
     "mthip_masked_fill": (_int, [_int, _int, _c_void_p, _i64p, _c_void_p, _i64p, _dbl, _c_void_p, _int, _i64p]),

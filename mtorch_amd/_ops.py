@@ -88,6 +88,8 @@ def _float_dtype(op, dt):
 def to(t: Tensor, dt, dev, copy=False) -> Tensor:
     """mtorch::to (tensor.cpp:8479-8508) across host and device."""
     src_dev = t.device
+    if dev.type == "mps":
+        raise NotImplementedError("'mps' device storage is not implemented")
     same_dev = src_dev.type == dev.type and T._device_index(src_dev) == T._device_index(dev)
     if same_dev and dt is t.dtype:
         return contiguous_copy(t) if copy else t
@@ -169,12 +171,16 @@ def copy_into(dst: Tensor, src: Tensor) -> None:
     dev = dst._dev()
     if src.device.type == "cpu" or src.dtype is not dst.dtype:
         src = src.to(device=dst.device, dtype=dst.dtype)
-    if not dst.is_contiguous():
-        raise unsupported("copy_ into a non-contiguous view", "cuda")
     n = dst.numel()
-    if n:
+    if n and dst.is_contiguous():
         _lib.check(_L().mthip_copy_strided(dev, dst.dtype.code, src.data_ptr(), src.dim(), _lib.int64_array(src.shape),
                                            _lib.int64_array(src.stride()), dst.data_ptr()))
+    elif n:
+        if src._storage is dst._storage:
+            src = contiguous_copy(src)  # an overlapping source is staged before the strided write
+        _lib.check(_L().mthip_copy_strided_to(dev, dst.dtype.code, src.data_ptr(), _lib.int64_array(src.stride()),
+                                              dst.dim(), _lib.int64_array(dst.shape), dst.data_ptr(),
+                                              _lib.int64_array(dst.stride())))
     dst._storage.version += 1
 
 
@@ -1058,8 +1064,13 @@ def softmax(x: Tensor, dim=-1, dtype=None) -> Tensor:
     out_dt = T._as_dtype(dtype, x.dtype)
     if not x.dtype.is_floating_point or not out_dt.is_floating_point:
         raise RuntimeError("softmax(): input dtype must be floating point")
-    src = x if out_dt is x.dtype else cast(x, out_dt)
     _float_dtype("softmax", out_dt)
+    # A dtype other than the input's takes the reference's generic path (tensor.cpp:15165-15207):
+    # the input is read at its own precision and only the results are narrowed.  So a wider
+    # output widens the input first (exact), a narrower one computes at the input's precision
+    # and narrows the probabilities.
+    narrowing = x.dtype is T.float32 and out_dt is T.float16
+    src = x if (out_dt is x.dtype or narrowing) else cast(x, out_dt)
     if rank == 0:
         src = src.reshape(1)
         d = 0
@@ -1075,8 +1086,10 @@ def softmax(x: Tensor, dim=-1, dtype=None) -> Tensor:
         for i, p in enumerate(perm):
             inv[p] = i
         out = res.permute(inv).contiguous()
-        return out.reshape(x.shape) if rank == 0 else out
-    out = _softmax_last(src.contiguous(), dev, divide)
+    else:
+        out = _softmax_last(src.contiguous(), dev, divide)
+    if narrowing:
+        out = cast(out, out_dt)
     return out.reshape(x.shape) if rank == 0 else out
 
 

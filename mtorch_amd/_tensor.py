@@ -102,9 +102,9 @@ def promote_types(a: dtype, b: dtype) -> dtype:
 class device(str):
     """Device spec: "cpu", "cuda[:i]" (the MI355X backend; "hip" is an alias).
 
-    The reference accepts only cpu/mps and rejects "cuda" (mtorch/__init__.py:33-55); this
-    backend adds the GPU type.  "mps"/"metal" keep raising NotImplementedError here because no
-    Apple GPU exists on this platform.
+    The reference accepts only cpu/mps and rejects "cuda" (mtorch/__init__.py:33-45); this
+    backend adds the GPU type.  "metal" parses to "mps" as in the reference, and, as there,
+    only creating storage on it raises NotImplementedError (no Apple GPU on this platform).
     """
 
     def __new__(cls, spec="cpu", index=None):
@@ -118,7 +118,7 @@ class device(str):
             kind = "cuda"
         if kind == "metal":
             kind = "mps"
-        if kind not in {"cpu", "cuda"}:
+        if kind not in {"cpu", "cuda", "mps"}:
             raise NotImplementedError(f"{kind!r} device is not implemented")
         if index is not None:
             idx = str(index)
@@ -247,6 +247,8 @@ class Storage:
         self.numel = numel
         self.version = 0
         self.packs = None
+        if dev.type == "mps":
+            raise NotImplementedError("'mps' device storage is not implemented")
         if dev.type == "cpu":
             self.host = host if host is not None else (np.zeros(numel, dtype=dt.np) if zero else np.empty(numel, dtype=dt.np))
             self.buf = None

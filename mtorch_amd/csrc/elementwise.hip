@@ -152,6 +152,22 @@ __global__ void copy_strided_kernel(const T* __restrict__ src, T* __restrict__ d
   }
 }
 
+// dst viewed through b_strides <- src viewed through a_strides (both in element units).
+template <typename T>
+__global__ void copy_strided_to_kernel(const T* __restrict__ src, T* __restrict__ dst, Shape s, int64_t n) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+    int64_t rem = i, so = 0, dof = 0;
+    for (int d = s.rank - 1; d >= 0; --d) {
+      const int64_t idx = rem % s.sizes[d];
+      rem /= s.sizes[d];
+      so += idx * s.a_strides[d];
+      dof += idx * s.b_strides[d];
+    }
+    dst[dof] = src[so];
+  }
+}
+
 // 2-D tiled transpose through LDS for views whose source is unit-stride along the second-last
 // collapsed dim (head split/merge [B,L,H,D] <-> [B,H,L,D], NCHW <-> NHWC):
 //   dst[b][r][c] (contiguous, c fastest) = src[b*sb + r + c*sc].
@@ -486,6 +502,35 @@ int mthip_copy_strided(int device, int dtype, const void* src, int rank, const i
     default: hipLaunchKernelGGL(copy_strided_kernel<uint64_t>, dim3(grid_for(n)), dim3(kThreads), 0, s, (const uint64_t*)src, (uint64_t*)dst, sh, n); break;
   }
   return check_launch("mthip_copy_strided");
+}
+
+int mthip_copy_strided_to(int device, int dtype, const void* src, const int64_t* src_strides, int rank,
+                          const int64_t* sizes, void* dst, const int64_t* dst_strides) {
+  const int es = elem_size(dtype);
+  MTHIP_REQUIRE(es != 0, "mthip_copy_strided_to: unknown dtype");
+  MTHIP_REQUIRE(rank >= 0 && rank <= kMaxRank, "mthip_copy_strided_to: rank must be <= 8");
+  int64_t n = 1;
+  for (int d = 0; d < rank; ++d) {
+    MTHIP_REQUIRE(sizes[d] >= 0, "mthip_copy_strided_to: negative size");
+    n *= sizes[d];
+  }
+  if (n == 0) return MTHIP_OK;
+  hipStream_t s = stream_for(device);
+  if (!s) return MTHIP_ERR_HIP;
+  if (int rc = use_device(device)) return rc;
+  Shape sh{};
+  int64_t* outs[2] = {sh.a_strides, sh.b_strides};
+  const int64_t* ins[2] = {src_strides, dst_strides};
+  sh.rank = collapse(rank, sizes, ins, 2, sh.sizes, outs);
+  if (sh.rank == 0) sh.rank = 1, sh.sizes[0] = 1, sh.a_strides[0] = 0, sh.b_strides[0] = 0;
+  const unsigned g = grid_for(n);
+  switch (es) {
+    case 1: hipLaunchKernelGGL(copy_strided_to_kernel<uint8_t>, dim3(g), dim3(kThreads), 0, s, (const uint8_t*)src, (uint8_t*)dst, sh, n); break;
+    case 2: hipLaunchKernelGGL(copy_strided_to_kernel<uint16_t>, dim3(g), dim3(kThreads), 0, s, (const uint16_t*)src, (uint16_t*)dst, sh, n); break;
+    case 4: hipLaunchKernelGGL(copy_strided_to_kernel<uint32_t>, dim3(g), dim3(kThreads), 0, s, (const uint32_t*)src, (uint32_t*)dst, sh, n); break;
+    default: hipLaunchKernelGGL(copy_strided_to_kernel<uint64_t>, dim3(g), dim3(kThreads), 0, s, (const uint64_t*)src, (uint64_t*)dst, sh, n); break;
+  }
+  return check_launch("mthip_copy_strided_to");
 }
 
 // The storage bits of `value` written as `dtype` (F16: float_to_half_bits((float)value),

@@ -3,6 +3,7 @@
 
 #include <algorithm>
 #include <cstdlib>
+#include <mutex>
 
 #include "gemm_core.h"
 #include "gemm_dtl.h"
@@ -293,7 +294,9 @@ __global__ void gelu_f16_table_kernel(uint16_t* tab) {
 
 const uint16_t* gelu_f16_table(int device, hipStream_t s) {
   static const uint16_t* ptr[64] = {nullptr};
+  static std::mutex init_mutex;  // first use from several host threads fills the table once
   if (device < 0 || device >= 64) return nullptr;
+  std::lock_guard<std::mutex> lock(init_mutex);
   if (!ptr[device]) {
     void* p = nullptr;
     if (hipGetSymbolAddress(&p, HIP_SYMBOL(g_gelu_f16_table)) != hipSuccess) return nullptr;
@@ -357,6 +360,10 @@ int mthip_linear(int device, int dtype, const void* x, int64_t lda, const void* 
   a.act = act;
   a.residual = residual;
   a.ld_res = ld_res;
+  if (dtype == MTHIP_F16 && act == MTHIP_ACT_GELU) {
+    a.gelu_tab = gelu_f16_table(device, s);
+    if (!a.gelu_tab) return fail(MTHIP_ERR_HIP, "mthip_linear: gelu table setup failed");
+  }
   const int vec = dtype == MTHIP_F16 ? 8 : 4;
   const int64_t es = dtype == MTHIP_F16 ? 2 : 4;
   const bool vec_ok = aligned16(x) && aligned16(w) && lda % vec == 0 && ldw % vec == 0 && K % vec == 0;

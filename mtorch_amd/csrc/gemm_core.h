@@ -211,15 +211,28 @@ __device__ __forceinline__ Raw4<T> load_raw4(const T* p) {
 // the row's bias in every slot (EPI_CONV, 0 without a bias), av the channel addend (EPI_CONV),
 // r the residual.  Values are narrowed once, except where a fused activation or residual needs
 // the narrowed intermediate that the unfused op sequence would have produced.
+// gtab: the fp16 gelu of every half value (ACT_GELU on fp16 only; unused otherwise): the
+// activation of the narrowed linear output is looked up by its bits -- the table holds exactly
+// what evaluating it gives -- instead of a double-precision erf per element.
 template <typename T, int EPI, int ACT>
 __device__ __forceinline__ void epi_math(float (&v)[4], const float (&b)[4], bool has_b, float av, bool has_av,
-                                         const float (&r)[4], bool has_r) {
+                                         const float (&r)[4], bool has_r, const uint16_t* gtab = nullptr) {
   if constexpr (EPI == EPI_LINEAR) {
     if (has_b) {
 #pragma unroll
       for (int t = 0; t < 4; ++t) v[t] += b[t];
     }
-    if (ACT != MTHIP_ACT_NONE || has_r) {
+    if constexpr (ACT == MTHIP_ACT_GELU && sizeof(T) == 2) {
+      uint32_t g[4];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) g[t] = gtab[f2h_fast(v[t])];  // every gather before the first use
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        float x = h2f_bits(g[t]);
+        if (has_r) x += r[t];
+        v[t] = x;
+      }
+    } else if (ACT != MTHIP_ACT_NONE || has_r) {
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
         float x = Elem<T>::round_trip(v[t]);
@@ -257,7 +270,7 @@ __device__ __forceinline__ void emit4(const GemmArgs& args, int64_t bz, int row,
     float b[4] = {0.0f, 0.0f, 0.0f, 0.0f}, r[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     if (bias) load_cols<T>(bias + col0, b, nv);
     if (res) load_cols<T>(res + col0, r, nv);
-    epi_math<T, EPI, ACT>(v, b, bias != nullptr, 0.0f, false, r, res != nullptr);
+    epi_math<T, EPI, ACT>(v, b, bias != nullptr, 0.0f, false, r, res != nullptr, args.gelu_tab);
     store_cols<T>(Cptr + (int64_t)row * args.ldc + col0, v, nv);
   } else if constexpr (EPI == EPI_GEMM) {
     const T* cin = reinterpret_cast<const T*>(args.c_in);
@@ -537,7 +550,7 @@ __device__ __forceinline__ void gemm_finish_unit(const GemmArgs& args, const Gem
                 b[t] = bz[j][g].at(t);
                 r[t] = rz[i][j][g].at(t);
               }
-              epi_math<T, EPI, ACT>(v, b, has_b, 0.0f, false, r, has_r);
+              epi_math<T, EPI, ACT>(v, b, has_b, 0.0f, false, r, has_r, args.gelu_tab);
               if (rows[i] < M) store_cols<T>(Cptr + (int64_t)rows[i] * args.ldc + col_base + j * 32 + 8 * g, v, 4);
             }
       } else {

@@ -10,6 +10,8 @@
 // form (tensor.cpp:18765-18767, 18822-18824) with fp32 tree sums.
 #include <hip/hip_runtime.h>
 
+#include <mutex>
+
 #include <algorithm>
 
 #include "activations.h"
@@ -346,7 +348,9 @@ __global__ void silu_f16_table_kernel(uint16_t* tab) {
 
 const uint16_t* silu_f16_table(int device, hipStream_t s) {
   static const uint16_t* ptr[64] = {nullptr};
+  static std::mutex init_mutex;  // first use from several host threads fills the table once
   if (device < 0 || device >= 64) return nullptr;
+  std::lock_guard<std::mutex> lock(init_mutex);
   if (!ptr[device]) {
     void* p = nullptr;
     if (hipGetSymbolAddress(&p, HIP_SYMBOL(g_silu_f16_table)) != hipSuccess) return nullptr;

@@ -310,29 +310,45 @@ int mthip_graph_end(int device, void** graph) {
   if (!s) return MTHIP_ERR_HIP;
   if (int rc = use_device(device)) return rc;
   auto* rec = new GraphRecord();
+  std::vector<std::pair<void*, size_t>> touched;
   hipError_t e = hipStreamEndCapture(s, &rec->graph);
   {
     std::lock_guard<std::mutex> lock(g_mutex);
     DeviceState& d = g_devices[device];
     d.capturing = false;
-    // Every block the capture handed out or freed is replayed into by the graph: keep it out
-    // of the shared cache until the graph is destroyed.
-    for (auto& kv : d.capture_touched) {
-      rec->owned.emplace_back(kv.first, kv.second);
-      d.graph_reserved[kv.first] += 1;
-    }
+    touched.assign(d.capture_touched.begin(), d.capture_touched.end());
     d.capture_touched.clear();
     d.capture_free.clear();
   }
+  std::string err;
   if (e != hipSuccess) {
-    delete rec;
-    return fail(MTHIP_ERR_HIP, std::string("hipStreamEndCapture: ") + hipGetErrorString(e));
+    err = std::string("hipStreamEndCapture: ") + hipGetErrorString(e);
+  } else {
+    e = hipGraphInstantiate(&rec->exec, rec->graph, nullptr, nullptr, 0);
+    if (e != hipSuccess) {
+      err = std::string("hipGraphInstantiate: ") + hipGetErrorString(e);
+      (void)hipGraphDestroy(rec->graph);
+    }
   }
-  e = hipGraphInstantiate(&rec->exec, rec->graph, nullptr, nullptr, 0);
-  if (e != hipSuccess) {
-    (void)hipGraphDestroy(rec->graph);
+  {
+    std::lock_guard<std::mutex> lock(g_mutex);
+    DeviceState& d = g_devices[device];
+    for (auto& kv : touched) {
+      if (err.empty()) {
+        // Every block the capture handed out or freed is replayed into by the graph: keep it
+        // out of the shared cache until the graph is destroyed.
+        rec->owned.emplace_back(kv.first, kv.second);
+        d.graph_reserved[kv.first] += 1;
+      } else if (d.live.find(kv.first) == d.live.end() && d.graph_reserved.count(kv.first) == 0) {
+        // No graph exists to replay into a block freed during the failed capture: it goes
+        // back to the shared cache.
+        d.free_blocks.emplace(kv.second, kv.first);
+      }
+    }
+  }
+  if (!err.empty()) {
     delete rec;
-    return fail(MTHIP_ERR_HIP, std::string("hipGraphInstantiate: ") + hipGetErrorString(e));
+    return fail(MTHIP_ERR_HIP, err);
   }
   *graph = rec;
   return MTHIP_OK;

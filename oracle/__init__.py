@@ -62,6 +62,7 @@ def lib():
         L.orc_group_norm.argtypes = [i32, vp, vp, vp, vp, i64, i64, i64, i64, dbl]
         L.orc_layer_norm.argtypes = [i32, vp, vp, vp, vp, i64, i64, dbl]
         L.orc_softmax_lastdim.argtypes = [i32, vp, vp, i64, i64, i32]
+        L.orc_softmax_generic.argtypes = [i32, vp, i32, vp, i64, i64]
         L.orc_gelu.argtypes = [i32, vp, vp, i64, i32]
         L.orc_fast_erf_float.restype = ctypes.c_float
         L.orc_fast_erf_float.argtypes = [ctypes.c_float]
@@ -70,7 +71,7 @@ def lib():
         L.orc_silu.argtypes = [i32, vp, vp, i64]
         L.orc_binary.argtypes = [i32, i32, vp, vp, vp, i64]
         for fn in ("orc_linear", "orc_matmul", "orc_addmm", "orc_conv2d", "orc_sdpa", "orc_group_norm",
-                   "orc_layer_norm", "orc_softmax_lastdim", "orc_gelu", "orc_silu", "orc_binary"):
+                   "orc_layer_norm", "orc_softmax_lastdim", "orc_softmax_generic", "orc_gelu", "orc_silu", "orc_binary"):
             getattr(L, fn).restype = i32
         _lib = L
     return _lib
@@ -258,6 +259,16 @@ def softmax_lastdim(x):
     cols = x.shape[-1]
     y = np.empty_like(x)
     lib().orc_softmax_lastdim(_dt(x), _p(x), _p(y), x.size // cols, cols, x.ndim)
+    return y
+
+
+def softmax_generic(x, out_dtype):
+    """softmax over the last dim with the output dtype ("float16"/"float32") differing from the
+    input's: the reference's generic double path."""
+    x = _c(x)
+    cols = x.shape[-1]
+    y = np.empty(x.shape, np.uint16 if out_dtype == "float16" else np.float32)
+    lib().orc_softmax_generic(_dt(x), _p(x), 0 if out_dtype == "float16" else 1, _p(y), x.size // cols, cols)
     return y
 
 

@@ -540,6 +540,39 @@ int orc_softmax_lastdim(int dtype, const void* x, void* y, int64_t rows, int64_t
   return 0;
 }
 
+/* softmax_impl's generic path (tensor.cpp:15165-15207), taken when the output dtype differs
+ * from the input's: the input read as double, e = exp(x - max) stored at the output dtype,
+ * the double total of the unstored e, then each stored e read back and divided by the total. */
+int orc_softmax_generic(int in_dtype, const void* x, int out_dtype, void* y, int64_t rows, int64_t cols) {
+  double* row = (double*)malloc(sizeof(double) * (size_t)(cols > 0 ? cols : 1));
+  if (!row) return -1;
+  for (int64_t r = 0; r < rows; ++r) {
+    for (int64_t i = 0; i < cols; ++i) {
+      const int64_t k = r * cols + i;
+      row[i] = in_dtype == ORC_F16 ? (double)orc_h2f(((const uint16_t*)x)[k]) : (double)((const float*)x)[k];
+    }
+    double mx = -INFINITY;
+    for (int64_t i = 0; i < cols; ++i) mx = row[i] > mx ? row[i] : mx;
+    double total = 0.0;
+    for (int64_t i = 0; i < cols; ++i) {
+      const double e = exp(row[i] - mx);
+      /* set_at_linear narrows double -> float (-> half) (tensor.cpp:593-614) */
+      row[i] = out_dtype == ORC_F16 ? (double)orc_h2f(orc_f2h((float)e)) : (double)(float)e;
+      total += e;
+    }
+    for (int64_t i = 0; i < cols; ++i) {
+      const float v = (float)(row[i] / total);
+      const int64_t k = r * cols + i;
+      if (out_dtype == ORC_F16)
+        ((uint16_t*)y)[k] = orc_f2h(v);
+      else
+        ((float*)y)[k] = v;
+    }
+  }
+  free(row);
+  return 0;
+}
+
 /* ------------------------------------------------------------------ activations */
 
 /* Abramowitz & Stegun 7.1.26 in float (tensor.cpp:17132-17144). */

@@ -98,6 +98,10 @@ int orc_layer_norm(int dtype, const void* x, const void* weight, const void* bia
  * rank 1 :7517-7539 (divide); fp16 :7743-7802 (multiply by 1/total). */
 int orc_softmax_lastdim(int dtype, const void* x, void* y, int64_t rows, int64_t cols, int rank);
 
+/* ---- softmax with an output dtype other than the input's: the generic double path,
+ * tensor.cpp:15165-15207 (e stored at the output dtype, divided by the double total). */
+int orc_softmax_generic(int in_dtype, const void* x, int out_dtype, void* y, int64_t rows, int64_t cols);
+
 /* ---- gelu: fp32 contiguous tensor.cpp:17254-17273 (+ :17132-17154); fp16 :17225-17235.
  * approximate: 0 = "none" (erf), 1 = "tanh". */
 int orc_gelu(int dtype, const void* x, void* y, int64_t n, int approximate);

@@ -697,6 +697,49 @@ def test_softmax(dt, shape):
     assert rel(val(got), val(orc.softmax_lastdim(x))) <= TOL[dt]
 
 
+@pytest.mark.parametrize("src,out", [("float32", "float16"), ("float16", "float32")])
+def test_softmax_with_another_output_dtype(src, out):
+    """softmax(x, dtype=...) reads x at its own precision and narrows only the results
+    (tensor.cpp:15165-15207), so large logits that one fp16 value cannot tell apart still get
+    their own probabilities."""
+    g = Gen(93)
+    x = g.randn((64, 77), src, 4.0)
+    if src == "float32":
+        x[0, :2] = [1000.0, 1000.3]
+        x[0, 2:] = -np.inf
+    got = host(F.softmax(dev(x), dim=-1, dtype=getattr(mt, out)))
+    ref = orc.softmax_generic(x, out)
+    assert rel(val(got), val(ref)) <= TOL[out]
+    if src == "float32":
+        assert abs(float(val(got)[0, 1]) - 0.5742) < 1e-3
+
+
+def test_copy_into_strided_views():
+    """copy_/item assignment of a tensor into a non-contiguous device view, with broadcasting
+    and an overlapping source (Tensor::copy_from, tensor.cpp:8292-8340)."""
+    g = Gen(94)
+    a = g.randn((6, 10), "float32")
+    d = dev(a)
+    src = g.randn((6, 4), "float32")
+    d[:, 3:7] = dev(src)
+    exp = a.copy()
+    exp[:, 3:7] = src
+    assert np.array_equal(host(d), exp)
+    row = g.randn((5,), "float32")
+    d[1:, ::2] = dev(row)  # broadcast over rows, every other column
+    exp[1:, ::2] = row
+    assert np.array_equal(host(d), exp)
+    d[:, 1:] = d[:, :-1]  # overlapping shift: staged, so every value is read before it is overwritten
+    exp[:, 1:] = exp[:, :-1].copy()
+    assert np.array_equal(host(d), exp)
+    h = dev(g.randn((4, 8), "float16"))
+    hx = host(h).copy()
+    v = g.randn((4, 3), "float32")
+    h[:, 2:8:2][:, :3] = dev(v)  # dtype conversion on the way in
+    hx[:, 2:8:2] = orc.f2h(v)
+    assert np.array_equal(host(h), hx)
+
+
 def test_softmax_other_dim():
     g = Gen(92)
     x = g.randn((5, 6, 7), "float32")

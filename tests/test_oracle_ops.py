@@ -211,6 +211,26 @@ def test_softmax_rows(orc, rng):
     assert ulps16(orc, orc.softmax_lastdim(h), orc.f2h(ref16)).max() <= 1
 
 
+def test_softmax_with_another_output_dtype(orc, rng):
+    """The generic path reads the input at its own precision and narrows only the results."""
+    # closed form: softmax([a, a + 0.3]) = (1/(1+e^0.3), 1/(1+e^-0.3)); rounding the logits to
+    # fp16 first would make both 1000.0 and give (0.5, 0.5)
+    got = orc.h2f(orc.softmax_generic(np.array([[1000.0, 1000.3]], np.float32), "float16"))
+    d = float(np.float32(1000.3)) - 1000.0
+    exp = orc.f2h(np.array([1 / (1 + math.exp(d)), 1 / (1 + math.exp(-d))], np.float32))
+    assert np.array_equal(orc.f2h(got[0]), exp)
+    x = rng.standard_normal((6, 77)).astype(np.float32) * 5
+    e = np.exp(x.astype(np.float64) - x.max(-1, keepdims=True))
+    ref = e / e.sum(-1, keepdims=True)
+    # e rounded to fp16, then the quotient rounded again: within one fp16 ulp of the exact value
+    assert ulps16(orc, orc.softmax_generic(x, "float16"), orc.f2h(ref.astype(np.float32))).max() <= 1
+    h = orc.f2h(x)
+    xr = orc.h2f(h).astype(np.float64)
+    e = np.exp(xr - xr.max(-1, keepdims=True))
+    ref = e / e.sum(-1, keepdims=True)
+    assert np.allclose(orc.softmax_generic(h, "float32"), ref, rtol=2e-7, atol=1e-12)
+
+
 # ------------------------------------------------------------------ activations
 
 
