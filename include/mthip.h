@@ -284,6 +284,16 @@ int mthip_sdpa(int device, int dtype, const void* q, const int64_t* qs, const vo
 int mthip_group_norm(int device, int dtype, const void* x, const void* weight, const void* bias,
                      void* y, int64_t B, int64_t C, int64_t inner, int64_t groups, double eps,
                      int fuse_silu, int param_dtype);
+/* mthip_group_norm without any device allocation.  No counterpart in the reference: it is for
+ * callers that cannot allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  Arguments and results are mthip_group_norm's, bit for bit;
+ * the statistics partials live in a static 1 MiB device array per GPU instead of a block from
+ * the caching allocator, so B * groups * ceil(group_size / chunk) must stay <= 131072 (at most
+ * 64 chunks of >= 2048 elements per group; an error status otherwise).  Calls that overlap on one
+ * GPU (other streams, other host threads) share the array and race. */
+int mthip_group_norm_noalloc(int device, int dtype, const void* x, const void* weight, const void* bias,
+                             void* y, int64_t B, int64_t C, int64_t inner, int64_t groups, double eps,
+                             int fuse_silu, int param_dtype);
 /* The same values written channels-last for mthip_conv2d_nhwc: y_nhwc[B][HW][Cp], Cp = C
  * rounded up to 8 (F16) or 4 (F32) channels, the padding channels zero.  x stays NCHW. */
 int mthip_group_norm_nhwc(int device, int dtype, const void* x, const void* weight, const void* bias,

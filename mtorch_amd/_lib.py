@@ -76,6 +76,8 @@ _SIGNATURES = {
                           _i64, _i64, _i64, _i64, _i64, _i64, _i64, _int, _int, _c_void_p, _i64p, _int, _dbl]),
     "mthip_group_norm": (_int, [_int, _int, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i64,
                                 _i64, _dbl, _int, _int]),
+    "mthip_group_norm_noalloc": (_int, [_int, _int, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i64,
+                                        _i64, _dbl, _int, _int]),
     "mthip_group_norm_nhwc": (_int, [_int, _int, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i64,
                                      _i64, _dbl, _int, _int]),
     "mthip_group_norm_nhwc_cat": (_int, [_int, _int, _c_void_p, _i64, _c_void_p, _i64, _c_void_p, _c_void_p, _c_void_p,

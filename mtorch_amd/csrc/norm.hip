@@ -776,10 +776,13 @@ __global__ __launch_bounds__(256) void softmax_long_kernel(const T* __restrict__
 // x1 (nullable): a second NCHW input of C - C0 channels concatenated after x's C0 channels
 // (channels-last fp16 output only); raw (nullable, channels-last only) receives the input
 // channels-last too.
+// ws_given (nullable): caller-owned room for ws_capacity float2 partials, used instead of a
+// block from the caching allocator (the no-allocation entry point passes its static scratch).
 template <typename T, typename P>
 int run_group_norm(int device, const void* x, const void* weight, const void* bias, void* y, int64_t B, int64_t C,
                    int64_t inner, int64_t groups, double eps, int fuse_silu, bool y_nhwc, int64_t Cp, hipStream_t s,
-                   const void* x1 = nullptr, int64_t C0 = -1, void* raw = nullptr) {
+                   const void* x1 = nullptr, int64_t C0 = -1, void* raw = nullptr, float2* ws_given = nullptr,
+                   int64_t ws_capacity = 0) {
   const int64_t group_size = (C / groups) * inner;
   if (C0 < 0) C0 = C;
   const GnSource<T> src{(const T*)x, (const T*)x1, C0, C - C0, C / groups, inner, groups};
@@ -797,8 +800,16 @@ int run_group_norm(int device, const void* x, const void* weight, const void* bi
   if (vect) chunk = ceil_div(chunk, V) * V;
   splits = ceil_div(group_size, chunk);
   void* ws = nullptr;
-  if (int rc = mthip_malloc(device, (size_t)(n_groups * splits) * sizeof(float2), &ws)) return rc;
-  float2* partial = static_cast<float2*>(ws);
+  float2* partial = ws_given;
+  if (ws_given) {
+    if (n_groups * splits > ws_capacity)
+      return fail(MTHIP_ERR_UNSUPPORTED, "mthip_group_norm_noalloc: batch*groups*chunks = " +
+                                             std::to_string(n_groups * splits) + " partial sums exceed the scratch of " +
+                                             std::to_string(ws_capacity));
+  } else {
+    if (int rc = mthip_malloc(device, (size_t)(n_groups * splits) * sizeof(float2), &ws)) return rc;
+    partial = static_cast<float2*>(ws);
+  }
   // The fp16 channels-last apply (the only one that reads two sources or writes `raw`).
   const bool nhwc_f16 = y_nhwc && sizeof(T) == 2 && ((uintptr_t)x % 16 == 0) && ((uintptr_t)y % 16 == 0) &&
                         inner % V == 0 && Cp % V == 0 && ((uintptr_t)x1 % 16 == 0) && ((uintptr_t)raw % 16 == 0) &&
@@ -959,6 +970,53 @@ int mthip_group_norm(int device, int dtype, const void* x, const void* weight, c
   if (param_dtype == MTHIP_F32)
     return run_group_norm<uint16_t, float>(device, x, weight, bias, y, B, C, inner, groups, eps, fuse_silu, false, C, s);
   return run_group_norm<uint16_t, uint16_t>(device, x, weight, bias, y, B, C, inner, groups, eps, fuse_silu, false, C, s);
+}
+
+// ---- the no-allocation entry point.  The statistics partials live in one file-scope device
+// array per GPU (each GPU that loads the library holds its own copy for the life of the
+// process); host code reaches it only through the per-device address hipGetSymbolAddress
+// returns.  Every (group, chunk) partial is written by the statistics pass before the apply pass
+// reads it, so nothing has to start at zero; concurrent calls on one GPU from different streams
+// or threads share the array and race.
+constexpr int64_t kGnScratchPartials = 131072;  // 1 MiB of float2
+static __device__ __align__(256) float2 scratch[kGnScratchPartials];
+
+static float2* gn_scratch_ptr(int device) {
+  static float2* ptrs[64] = {nullptr};
+  static std::mutex m;
+  if (device < 0 || device >= 64) return nullptr;
+  std::lock_guard<std::mutex> lock(m);
+  if (!ptrs[device]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) {
+      set_error(std::string("mthip_group_norm_noalloc: hipGetSymbolAddress: ") + hipGetErrorString(e));
+      return nullptr;
+    }
+    ptrs[device] = static_cast<float2*>(p);
+  }
+  return ptrs[device];
+}
+
+int mthip_group_norm_noalloc(int device, int dtype, const void* x, const void* weight, const void* bias, void* y,
+                             int64_t B, int64_t C, int64_t inner, int64_t groups, double eps, int fuse_silu,
+                             int param_dtype) {
+  MTHIP_REQUIRE(norm_dtypes_ok(dtype, param_dtype), "mthip_group_norm_noalloc: unsupported dtype / param_dtype pair");
+  MTHIP_REQUIRE(groups > 0 && C % groups == 0, "mthip_group_norm_noalloc: num_channels must be divisible by num_groups");
+  MTHIP_REQUIRE(B >= 0 && inner >= 0, "mthip_group_norm_noalloc: negative extent");
+  hipStream_t s = stream_for(device);
+  if (!s) return MTHIP_ERR_HIP;
+  if (int rc = use_device(device)) return rc;  // the symbol address below is the current device's
+  float2* ws = gn_scratch_ptr(device);
+  if (!ws) return MTHIP_ERR_HIP;
+  if (dtype == MTHIP_F32)
+    return run_group_norm<float, float>(device, x, weight, bias, y, B, C, inner, groups, eps, fuse_silu, false, C, s,
+                                        nullptr, -1, nullptr, ws, kGnScratchPartials);
+  if (param_dtype == MTHIP_F32)
+    return run_group_norm<uint16_t, float>(device, x, weight, bias, y, B, C, inner, groups, eps, fuse_silu, false, C,
+                                           s, nullptr, -1, nullptr, ws, kGnScratchPartials);
+  return run_group_norm<uint16_t, uint16_t>(device, x, weight, bias, y, B, C, inner, groups, eps, fuse_silu, false, C,
+                                            s, nullptr, -1, nullptr, ws, kGnScratchPartials);
 }
 
 int mthip_group_norm_nhwc(int device, int dtype, const void* x, const void* weight, const void* bias, void* y_nhwc,
