@@ -1,12 +1,17 @@
 """Benchmark of mtorch's SD-UNet hot path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload resnet|linear_gelu|unet|copy_calibration|suite] [--no-cpu]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload resnet|linear_gelu|unet|copy_calibration|suite]
+                    [--no-cpu] [--no-extras]
 
 Default workload (fp16 leg): the SD ResNet sub-block on a 64x64
 latent at batch 2 -- x[2,320,64,64] -> GroupNorm(32, eps 1e-5, affine) -> SiLU ->
 conv2d 3x3 s1 p1 320->320 (+bias) -> + x -- with inputs and parameters drawn from mtorch's
 generator (seed 0): x ~ N(0,1), gamma = 1 + 0.1 N(0,1), beta = 0.1 N(0,1), conv weight
 kaiming_uniform_(a=sqrt 5), bias U(+-1/sqrt(2880)); all drawn in fp32 and cast to fp16.
+
+The same line carries the rest of the headline metric: the configs[4] SD-1.5 UNet step at
+batch 2 (unet_ms_per_step, graph-replayed) and the configs[0]/[2]/[3] contractions (TFLOP/s and
+MFMA fraction per op, under "configs").
 
 One step = one pass of the block over the resident batch.  The timed region is K steps
 bracketed by device synchronisation; HIP events on the device stream time the whole step and,
@@ -164,7 +169,48 @@ def run_resnet(args):
     }
     if args.cpu:
         out["cpu_baseline"] = cpu_baseline_resnet(x, gamma, beta, w, b)
+    if args.extras:
+        out.update(headline_extras(args))
     return out
+
+
+def headline_extras(args):
+    """The rest of BASELINE.json's metric on the same line: the configs[4] UNet step (ms at
+    batch 2, graph-replayed) and the configs[0], [2], [3] contractions (TFLOP/s and fraction of
+    the MFMA peak that bounds each), every op graph-replayed x20 at its SD shape."""
+    import mtorch_amd as mt
+    from mtorch_amd import sd_unet
+
+    unet = run_unet(argparse.Namespace(steps=max(args.steps // 2, 5), warmup=max(args.warmup, 2)))
+    extras = {"unet_ms_per_step": unet["ms_per_step"], "unet_tflops": unet["tflops"],
+              "unet_mfma_frac": unet["mfma_frac"], "unet_tflop_per_step": unet["unet_tflop_per_step"]}
+    del unet
+    F = mt.nn.functional
+    mt.manual_seed(0)
+    rows = {}
+
+    def rnd(*shape, dt=mt.float16, scale=1.0):
+        t = mt.randn(*shape).to("cuda")
+        return (t * scale if scale != 1.0 else t).to(dt)
+
+    def put(key, r):
+        rows[key] = {"us": r["us"], "tflops": r["tflops"], "frac": r["frac"]}
+
+    bound = 1.0 / math.sqrt(320)
+    x = mt.randn(8192, 320).to("cuda")
+    w = mt.empty(1280, 320).uniform_(-bound, bound).to("cuda")
+    b = mt.empty(1280).uniform_(-bound, bound).to("cuda")
+    put("c0_linear_gelu_fp32", _suite_row("c0", lambda: F.linear_gelu(x, w, b), 20, flops=2.0 * 8192 * 1280 * 320,
+                                          peak=PEAK["fp32_tflops"], quiet=True))
+    for L, E in ((4096, 40), (1024, 80), (256, 160)):
+        q, k, v = rnd(2, 8, L, E, scale=1.0 / math.sqrt(E)), rnd(2, 8, L, E), rnd(2, 8, L, E)
+        put(f"c2_self_{L}x{E}", _suite_row("c2", lambda: F.scaled_dot_product_attention(q, k, v), 20,
+                                           flops=4.0 * 2 * 8 * L * L * E, quiet=True))
+    st = sd_unet.SpatialTransformer(sd_unet._Init("cuda"), 640)
+    xt, ctx = rnd(2, 640, 32, 32), rnd(2, 77, 768)
+    put("c3_spatial_transformer", _suite_row("c3", lambda: st(xt, ctx), 5, flops=39.63e9, quiet=True))
+    extras["configs"] = rows
+    return extras
 
 
 def run_copy_calibration(args):
@@ -296,7 +342,7 @@ def run_unet(args):
     }
 
 
-def _suite_row(name, fn, reps, flops=None, nbytes=None, bound="mfma", peak=None, graph=True):
+def _suite_row(name, fn, reps, flops=None, nbytes=None, bound="mfma", peak=None, graph=True, quiet=False):
     """Time one op: a HIP graph of `reps` back-to-back calls replayed once (so launch gaps do
     not count against short kernels), averaged per call; then price it against its roofline."""
     import mtorch_amd as mt
@@ -321,7 +367,8 @@ def _suite_row(name, fn, reps, flops=None, nbytes=None, bound="mfma", peak=None,
         row["frac"] = round(row["tflops"] / (peak or PEAK["fp16_mfma_tflops"]), 4)
     else:
         row["frac"] = round(row["gbs"] / PEAK["hbm_gbs"], 4)
-    print(json.dumps(row), file=sys.stderr, flush=True)
+    if not quiet:
+        print(json.dumps(row), file=sys.stderr, flush=True)
     return row
 
 
@@ -425,6 +472,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="resnet", choices=["resnet", "linear_gelu", "unet", "copy_calibration", "suite"])
     ap.add_argument("--no-cpu", dest="cpu", action="store_false")
+    ap.add_argument("--no-extras", dest="extras", action="store_false",
+                    help="resnet workload: skip the UNet step and per-config contraction keys")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this backend measures one MI355X; multi-GPU runs are not part of it",
