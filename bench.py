@@ -156,8 +156,9 @@ def run_resnet(args):
         "config": {"workload": "configs[1] ResNet sub-block fp16: x[2,320,64,64], GN(32), SiLU, conv3x3 320->320, residual",
                    "batch": 2, "channels": 320, "hw": [64, 64]},
         "roofline": {
-            "kernel": "conv3x3 launch: gemm_dtl_kernel<64x64, 3 LDS stages, MODE_CONV, EPI_CONV> "
-                      "(direct-to-LDS implicit GEMM, one K slice; bias and residual fused in the epilogue)",
+            "kernel": "conv3x3 launch: conv3x3_halo_kernel<80 channels x 2 rows x 64, 6-stage weight ring, "
+                      "4 waves> (input halo staged once per 64-channel block and reused by the 9 taps; "
+                      "bias and residual fused in the epilogue)",
             "bound": "mfma",
             "achieved": round(conv_tflops, 3),
             "peak": PEAK["fp16_mfma_tflops"],

@@ -9,6 +9,10 @@
 // NCHW store stays coalesced.  Bias and an optional residual are applied in the epilogue.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
+#include <cstdlib>
+
+#include "conv_halo.h"
 #include "gemm_core.h"
 
 namespace mthip {
@@ -99,6 +103,106 @@ int launch_pack_weight(const void* w, void* wp, int64_t O, int64_t C, int64_t KH
   return check_launch("pack_weight_kernel");
 }
 
+int halo_cu_count(int device) {
+  static int cached[64] = {0};
+  if (device < 0 || device >= 64) return 256;
+  if (cached[device] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess || n < 1) n = 256;
+    cached[device] = n;
+  }
+  return cached[device];
+}
+
+template <int BM, int TR, int TW>
+int launch_halo(int device, HaloArgs h, hipStream_t s) {
+  h.tiles_m = (int)ceil_div(h.O, BM);
+  h.row_blocks = (int)ceil_div(h.H, TR);
+  const int ncb = h.Cp / 64;
+  // Split the channel blocks when the units alone leave CUs idle (the 16x16 and 8x8 latents).
+  const int64_t base = (int64_t)h.tiles_m * h.row_blocks * h.B;
+  const int cus = halo_cu_count(device);
+  int ks = 1;
+  if (base * 4 < (int64_t)cus * 3) ks = (int)std::min<int64_t>(ncb, std::max<int64_t>(1, cus / base));
+  if (const char* f = std::getenv("MTHIP_CONV_HALO_KSPLIT")) ks = std::max(1, std::min(ncb, std::atoi(f)));
+  h.cb_per_split = (int)ceil_div(ncb, ks);
+  h.ksplit = (int)ceil_div(ncb, h.cb_per_split);
+  const int64_t units = base * h.ksplit;
+  MTHIP_REQUIRE(units < (int64_t(1) << 31), "conv: too many units");
+  h.units = (int)units;
+  void* ws = nullptr;
+  const int64_t N = (int64_t)h.B * h.H * h.W;
+  if (h.ksplit > 1) {
+    h.ld_partial = (int)(ceil_div(N, 4) * 4);
+    if (int rc = mthip_malloc(device, (size_t)((int64_t)h.ksplit * h.O * h.ld_partial) * sizeof(float), &ws)) return rc;
+    h.partial = static_cast<float*>(ws);
+  }
+  hipLaunchKernelGGL((conv3x3_halo_kernel<BM, TR, TW, 1, 6, 4>), dim3((unsigned)units), dim3(256), 0, s, h);
+  int rc = check_launch("conv3x3_halo_kernel");
+  if (rc == MTHIP_OK && h.ksplit > 1) {
+    GemmArgs a{};
+    a.M = h.O;
+    a.N = N;
+    a.c = h.y;
+    a.bias = h.bias;
+    a.residual = h.residual;
+    a.chan_add = h.chan_add;
+    a.chan_add_ld = h.chan_add_ld;
+    a.OH = h.H;
+    a.OW = h.W;
+    a.div_ohw = FastDiv((uint32_t)(h.H * h.W));
+    a.partial = h.partial;
+    a.ld_partial = h.ld_partial;
+    a.ksplit = h.ksplit;
+    const int64_t work = a.M * ceil_div(a.N, 4);
+    const unsigned rg = (unsigned)std::min<int64_t>(ceil_div(work, 256), 8192);
+    hipLaunchKernelGGL((gemm_splitk_reduce_kernel<uint16_t, EPI_CONV, MTHIP_ACT_NONE>), dim3(rg), dim3(256), 0, s, a);
+    rc = check_launch("gemm_splitk_reduce_kernel(conv)");
+  }
+  if (ws) mthip_free(device, ws);  // stream-ordered: reused only by later work
+  return rc;
+}
+
+// fp16 3x3 stride-1 pad-1 convs whose padded channel count is a whole number of 64-channel
+// blocks and whose width is one of the SD latent widths take the halo kernel; returns -1 for
+// the rest (MTHIP_CONV_HALO=0 sends every conv to the implicit GEMM).
+int try_conv_halo(int device, const void* xp, const void* wp, const void* b, void* y, int64_t B, int64_t H, int64_t W,
+                  int64_t Cp, int64_t O, int64_t KH, int64_t KW, int64_t sh, int64_t sw, int64_t ph, int64_t pw,
+                  int64_t dh, int64_t dw, const void* residual, const void* chan_add, int64_t chan_add_ld,
+                  hipStream_t s) {
+  static const bool enabled = [] {
+    const char* e = std::getenv("MTHIP_CONV_HALO");
+    return e == nullptr || std::atoi(e) != 0;
+  }();
+  if (!enabled || KH != 3 || KW != 3 || sh != 1 || sw != 1 || ph != 1 || pw != 1 || dh != 1 || dw != 1) return -1;
+  if (Cp % 64 != 0 || O < 64 || !(W == 64 || W == 32 || W == 16 || W == 8)) return -1;
+  if (((uintptr_t)b & 1) || ((uintptr_t)residual & 7) || ((uintptr_t)xp & 15) || ((uintptr_t)wp & 15)) return -1;
+  if (B * H * W * Cp * 2 >= (int64_t(1) << 31) || O * 9 * Cp * 2 >= (int64_t(1) << 31) ||
+      B * O * H * W * 2 >= (int64_t(1) << 31) || B * chan_add_ld * 2 >= (int64_t(1) << 31))
+    return -1;
+  HaloArgs h{};
+  h.x = xp;
+  h.w = wp;
+  h.y = y;
+  h.bias = b;
+  h.residual = residual;
+  h.chan_add = chan_add;
+  h.chan_add_ld = (int)chan_add_ld;
+  h.B = (int)B;
+  h.H = (int)H;
+  h.W = (int)W;
+  h.Cp = (int)Cp;
+  h.O = (int)O;
+  h.x_bytes = (int)(B * H * W * Cp * 2);
+  h.w_bytes = (int)(O * 9 * Cp * 2);
+  switch (W) {
+    case 64: return launch_halo<80, 2, 64>(device, h, s);
+    case 32: return launch_halo<80, 2, 32>(device, h, s);
+    case 16: return launch_halo<80, 4, 16>(device, h, s);
+    default: return launch_halo<80, 8, 8>(device, h, s);
+  }
+}
+
 // The implicit GEMM over an input already staged channels-last: xp[B][H][W][Cp].
 template <typename T>
 int run_conv_gemm_nhwc(int device, int dtype, const void* xp, const void* wp, const void* b, void* y, int64_t B,
@@ -112,6 +216,11 @@ int run_conv_gemm_nhwc(int device, int dtype, const void* xp, const void* wp, co
   const int64_t K = KH * KW * Cp;
   if (O * K * (int64_t)sizeof(T) >= (int64_t(1) << 31) || B * H * W * Cp * (int64_t)sizeof(T) >= (int64_t(1) << 31))
     return fail(MTHIP_ERR_UNSUPPORTED, "mthip_conv2d: operands above 2 GiB are not supported");
+  if constexpr (sizeof(T) == 2) {
+    const int rc = try_conv_halo(device, xp, wp, b, y, B, H, W, Cp, O, KH, KW, sh, sw, ph, pw, dh, dw, residual,
+                                 chan_add, chan_add_ld, s);
+    if (rc >= 0) return rc;
+  }
   GemmArgs a{};
   a.M = O;
   a.N = B * OH * OW;

@@ -566,6 +566,35 @@ def test_group_norm_silu_conv2d_channels_last_handoff(dt, B, C, H, W, O, G):
     assert rel(val(got), val(orc.conv2d(h, w, None, stride=2, padding=1))) <= TOL[dt]
 
 
+@pytest.mark.parametrize("B,C,H,W,O", [(2, 64, 64, 64, 80), (1, 128, 5, 64, 100), (2, 64, 32, 32, 160),
+                                         (2, 192, 16, 16, 96), (1, 320, 8, 8, 80), (2, 60, 9, 16, 64),
+                                         (1, 128, 3, 32, 240)])
+def test_conv3x3_halo_kernel_shapes(B, C, H, W, O):
+    """fp16 3x3 s1 p1 convs of 64-channel blocks take the halo kernel: every latent width (64,
+    32, 16, 8), a partial last row block, a partial last channel tile, padded input channels and
+    the channel-block split with its reduction; with bias, residual and the channel addend."""
+    g = Gen(B * 7000 + C * 13 + H * 3 + O)
+    x = g.randn((B, C, H, W), "float16")
+    w = g.randn((O, C, 3, 3), "float16", 1.0 / np.sqrt(9 * C))
+    b = g.randn((O,), "float16")
+    r = g.randn((B, O, H, W), "float16")
+    t = g.randn((B, O), "float16")
+    got = host(F.conv2d_residual(dev(x), dev(w), dev(b), dev(r), padding=1))
+    conv = orc.conv2d(x, w, b, padding=1)
+    assert rel(val(got), val(orc.binary(conv, r, "add"))) <= 1e-2
+    got = host(F.conv2d(dev(x), dev(w), None, padding=1))
+    assert rel(val(got), val(orc.conv2d(x, w, None, padding=1))) <= 1e-2
+    # through the channels-last hand-off, with the time-embedding addend fused
+    gamma = g.randn((C,), "float16")
+    beta = g.randn((C,), "float16")
+    groups = 4
+    fused = host(F.group_norm_silu_conv2d(dev(x), groups, dev(gamma), dev(beta), 1e-5, dev(w), dev(b), padding=1,
+                                          chan_add=dev(t), residual=dev(r)))
+    h = orc.silu(orc.group_norm(x, groups, gamma, beta, 1e-5))
+    ref = val(orc.conv2d(h, w, b, padding=1)).astype(np.float64) + val(t)[:, :, None, None] + val(r)
+    assert rel(val(fused), ref) <= 1e-2
+
+
 @pytest.mark.parametrize("dt", ["float32", "float16"])
 @pytest.mark.parametrize("B,C,H,W,O,G", [(2, 64, 16, 16, 48, 32), (2, 40, 9, 7, 40, 8), (1, 16, 8, 8, 24, 4)])
 def test_group_norm_silu_conv2d_channel_add_is_the_separate_add(dt, B, C, H, W, O, G):
