@@ -337,7 +337,7 @@ def _rows_view(x: Tensor):
     """x[..., K] as M rows of K with one row stride (lda), or None if not expressible."""
     K = x.shape[-1]
     if x.dim() == 1:
-        return 1, K if x.stride(0) == 1 else None
+        return (1, K) if x.stride(0) == 1 or K <= 1 else None
     if x.stride(-1) != 1 and K > 1:
         return None
     outer = list(x.shape[:-1])

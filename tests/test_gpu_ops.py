@@ -244,6 +244,18 @@ def test_linear(dt, M, N, K):
 
 
 @pytest.mark.parametrize("dt", ["float32", "float16"])
+def test_linear_strided_vector_input(dt):
+    """A 1-D input with a non-unit stride (x[::2]) is one row read after a dense copy."""
+    g = Gen(5)
+    x = g.randn((2 * 96,), dt)
+    w = g.randn((40, 96), dt, 0.1)
+    b = g.randn((40,), dt)
+    got = host(F.linear(dev(x)[::2], dev(w), dev(b)))
+    ref = orc.linear(np.ascontiguousarray(x[::2]).reshape(1, 96), w, b).reshape(40)
+    assert rel(val(got), val(ref)) <= TOL[dt]
+
+
+@pytest.mark.parametrize("dt", ["float32", "float16"])
 def test_linear_fused_epilogues(dt):
     g = Gen(21)
     x = g.randn((3, 50, 96), dt)
