@@ -348,8 +348,13 @@ void flash_fwd_f16_kernel(const FlashArgs a) {
 
   if (!qok) return;
   uint16_t* O = reinterpret_cast<uint16_t*>(a.o) + b * a.os[0] + head * a.os[1] + q * a.os[2];
+  // A fully masked row has l = 0 and, every P being 0, a zero accumulator: 0 * (1/0) = NaN, the
+  // reference's 0/0.
   const float inv_l = 1.0f / l_run;
-  const bool zero_l = l_run == 0.0f;  // fully masked row: 0/0 = NaN like the reference
+  // Under VEC, Ev and the output strides are multiples of 8 and the base is 16-byte aligned, so
+  // every 4-dim group below Ev is whole and 8-byte aligned: one straight store each.  (A generic
+  // per-element fallback here would multiply the epilogue's code several times over, and that
+  // straight-line code is fetched cold by every workgroup.)
 #pragma unroll
   for (int i = 0; i < DVB; ++i)
 #pragma unroll
@@ -358,14 +363,14 @@ void flash_fwd_f16_kernel(const FlashArgs a) {
       if (d0 >= Ev) continue;
       float v[4];
 #pragma unroll
-      for (int t = 0; t < 4; ++t) v[t] = zero_l ? acc[i][4 * g + t] / l_run : acc[i][4 * g + t] * inv_l;
-      if (d0 + 4 <= Ev && ((((uintptr_t)(O + d0)) & 7) == 0)) {
+      for (int t = 0; t < 4; ++t) v[t] = acc[i][4 * g + t] * inv_l;
+      if constexpr (VEC) {
         uint2 u;
-        u.x = (uint32_t)f2h_fast(v[0]) | ((uint32_t)f2h_fast(v[1]) << 16);
-        u.y = (uint32_t)f2h_fast(v[2]) | ((uint32_t)f2h_fast(v[3]) << 16);
+        u.x = (uint32_t)f2h_generic(v[0]) | ((uint32_t)f2h_generic(v[1]) << 16);
+        u.y = (uint32_t)f2h_generic(v[2]) | ((uint32_t)f2h_generic(v[3]) << 16);
         *reinterpret_cast<uint2*>(O + d0) = u;
       } else {
-        for (int t = 0; t < 4 && d0 + t < Ev; ++t) O[d0 + t] = f2h_fast(v[t]);
+        for (int t = 0; t < 4 && d0 + t < Ev; ++t) O[d0 + t] = f2h_generic(v[t]);
       }
     }
 }
@@ -518,7 +523,8 @@ extern "C" int mthip_sdpa(int device, int dtype, const void* q, const int64_t* q
   if (dtype == MTHIP_F16 && Lk > 0 && dmax <= 160 && small_heads) {
     const bool vec = E % 8 == 0 && Ev % 8 == 0 && qs[2] % 8 == 0 && ks[2] % 8 == 0 && vs[2] % 8 == 0 &&
                      qs[0] % 8 == 0 && qs[1] % 8 == 0 && ks[0] % 8 == 0 && ks[1] % 8 == 0 && vs[0] % 8 == 0 &&
-                     vs[1] % 8 == 0 && aligned16(q) && aligned16(k) && aligned16(v);
+                     vs[1] % 8 == 0 && a.os[0] % 8 == 0 && a.os[1] % 8 == 0 && a.os[2] % 8 == 0 &&
+                     aligned16(q) && aligned16(k) && aligned16(v) && aligned16(o);
     if (dmax <= 32)
       launch_flash<32>(a, bh, s, vec);
     else if (dmax <= 48)

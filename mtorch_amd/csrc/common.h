@@ -110,14 +110,20 @@ __device__ __forceinline__ uint16_t f2h_generic(float value) {
   return (uint16_t)((bits & 0x7fffffffu) > 0x7f800000u ? nan_bits : h);
 }
 
-// Same function with a short common path: for zero and |value| in [2^-14, 2^16) the result
-// is a normal half (or the overflow to inf), 13 significand bits are discarded, and the RNE
-// result needs the extra ulp exactly when those bits are 0x1000 with the kept LSB 0, i.e.
-// (bits & 0x3fff) == 0x1000 (inside [65520, 65536) the discarded bits are >= 0x3000, so inf
-// is never bumped).  Subnormal results, |value| >= 2^16, infinities and NaNs take
-// f2h_generic, on a branch the whole wave skips unless one of its lanes needs it.  Equal to
-// f2h_generic for all 2^32 inputs (tests/f2h_fast_model.c checks it exhaustively with a CPU
-// model of the hardware conversion).
+// f2h_generic with a short common path, for streaming kernels (one or a few values per lane
+// between loads, many waves per SIMD): for zero and |value| in [2^-14, 2^16) the result is a
+// normal half (or the overflow to inf), 13 significand bits are discarded, and the RNE result
+// needs the extra ulp exactly when those bits are 0x1000 with the kept LSB 0, i.e.
+// (bits & 0x3fff) == 0x1000 (inside [65520, 65536) the discarded bits are >= 0x3000, so inf is
+// never bumped).  Subnormal results, |value| >= 2^16, infinities and NaNs take f2h_generic, on a
+// branch the whole wave skips unless one of its lanes needs it.  Equal to f2h_generic for all
+// 2^32 inputs (tests/f2h_fast_model.c checks both exhaustively with a CPU model of the hardware
+// conversion).
+//
+// Epilogues that narrow dozens of values per lane at one or two waves per SIMD (GEMM, conv,
+// attention) call f2h_generic directly: about 21 VALU operations and no branch, so the
+// conversions interleave, where one scalar branch per value would serialise them and the
+// fallback, inlined at every call, would multiply the code each workgroup fetches cold.
 __device__ __forceinline__ uint16_t f2h_fast(float value) {
   const uint32_t bits = __float_as_uint(value);
   const uint32_t a = bits & 0x7fffffffu;

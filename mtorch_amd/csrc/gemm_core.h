@@ -125,6 +125,17 @@ struct GemmArgs {
   int64_t chan_add_ld;
 };
 
+// v as the unfused op sequence reads it back after storing it in T.  Epilogues narrow with the
+// branch-free f2h_generic (many values per lane at low occupancy).
+template <typename T>
+__device__ __forceinline__ float epi_round(float v) {
+  if constexpr (sizeof(T) == 2) {
+    return h2f_bits(f2h_generic(v));
+  } else {
+    return v;
+  }
+}
+
 // Stores the first nv (1..4) of 4 consecutive outputs, narrowed once each; one 8-byte (fp16)
 // or 16-byte (fp32) store when all four are valid and aligned.
 template <typename T>
@@ -132,7 +143,7 @@ __device__ __forceinline__ void store_cols(T* p, const float (&v)[4], int nv) {
   if constexpr (sizeof(T) == 2) {
     uint32_t h[4];
 #pragma unroll
-    for (int t = 0; t < 4; ++t) h[t] = f2h_fast(v[t]);
+    for (int t = 0; t < 4; ++t) h[t] = f2h_generic(v[t]);
     if (nv == 4 && ((uintptr_t)p & 7) == 0) {
       *reinterpret_cast<uint2*>(p) = make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
     } else {
@@ -225,7 +236,7 @@ __device__ __forceinline__ void epi_math(float (&v)[4], const float (&b)[4], boo
     if constexpr (ACT == MTHIP_ACT_GELU && sizeof(T) == 2) {
       uint32_t g[4];
 #pragma unroll
-      for (int t = 0; t < 4; ++t) g[t] = gtab[f2h_fast(v[t])];  // every gather before the first use
+      for (int t = 0; t < 4; ++t) g[t] = gtab[f2h_generic(v[t])];  // every gather before the first use
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
         float x = h2f_bits(g[t]);
@@ -235,9 +246,9 @@ __device__ __forceinline__ void epi_math(float (&v)[4], const float (&b)[4], boo
     } else if (ACT != MTHIP_ACT_NONE || has_r) {
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
-        float x = Elem<T>::round_trip(v[t]);
+        float x = epi_round<T>(v[t]);
         if constexpr (ACT != MTHIP_ACT_NONE) x = apply_act<T>(ACT, x);
-        if (has_r) x = Elem<T>::round_trip(x) + r[t];
+        if (has_r) x = epi_round<T>(x) + r[t];
         v[t] = x;
       }
     }
@@ -247,8 +258,8 @@ __device__ __forceinline__ void epi_math(float (&v)[4], const float (&b)[4], boo
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
       float x = v[t] + b[t];
-      if (has_av) x = Elem<T>::round_trip(x) + av;
-      if (has_r) x = Elem<T>::round_trip(x) + r[t];
+      if (has_av) x = epi_round<T>(x) + av;
+      if (has_r) x = epi_round<T>(x) + r[t];
       v[t] = x;
     }
   }
@@ -279,7 +290,7 @@ __device__ __forceinline__ void emit4(const GemmArgs& args, int64_t bz, int row,
     for (int t = 0; t < 4; ++t) {
       float x = v[t] * args.alpha;
       if (cinrow && t < nv)
-        x = Elem<T>::round_trip(args.beta * Elem<T>::load(cinrow, (int64_t)(col0 + t) * args.c_in_cs)) + x;
+        x = epi_round<T>(args.beta * Elem<T>::load(cinrow, (int64_t)(col0 + t) * args.c_in_cs)) + x;
       v[t] = x;
     }
     store_cols<T>(Cptr + bz * args.stride_c + (int64_t)row * args.ldc + col0, v, nv);
@@ -307,8 +318,8 @@ __device__ __forceinline__ void emit4(const GemmArgs& args, int64_t bz, int row,
         const int im = (int)args.div_ohw.div((uint32_t)c), px = c - im * OHW;
         const int64_t addr = ((int64_t)im * M + row) * OHW + px;
         float x = v[t] + bv;
-        if (cadd) x = Elem<T>::round_trip(x) + Elem<T>::load(cadd, im * args.chan_add_ld + row);
-        if (res) x = Elem<T>::round_trip(x) + Elem<T>::load(res, addr);
+        if (cadd) x = epi_round<T>(x) + Elem<T>::load(cadd, im * args.chan_add_ld + row);
+        if (res) x = epi_round<T>(x) + Elem<T>::load(res, addr);
         Elem<T>::store(Cptr, addr, x);
       }
     }
@@ -449,7 +460,7 @@ __device__ __forceinline__ void gemm_finish_unit(const GemmArgs& args, const Gem
           for (int t = 0; t < 4; ++t) {
             float gate = acc[i][1][4 * g + t];
             if (has_b) gate += bgate[g][t];
-            gh[g][t] = f2h_fast(gate);
+            gh[g][t] = f2h_generic(gate);
           }
 #pragma unroll
         for (int g = 0; g < 4; ++g)
@@ -476,7 +487,7 @@ __device__ __forceinline__ void gemm_finish_unit(const GemmArgs& args, const Gem
               float val = acc[i][0][4 * g + t];
               if (has_b) val += bval[g][t];
               if constexpr (sizeof(T) == 2) {
-                v[t] = h2f_bits(f2h_fast(val)) * gl[g][t];
+                v[t] = h2f_bits(f2h_generic(val)) * gl[g][t];
               } else {
                 v[t] = val * gl[g][t];
               }

@@ -87,7 +87,7 @@ struct GnSource {
   const T* x1;  // nullptr: one source (C1 == 0)
   int64_t C0, C1, gc, HW, groups;
   __device__ __forceinline__ void group(int64_t bg, const T*& lo, const T*& hi, int64_t& split) const {
-    const int64_t b = bg / groups, c = (bg - b * groups) * gc;
+    const int64_t b = (uint32_t)bg / (uint32_t)groups, c = (bg - b * groups) * gc;
     lo = x0 + (b * C0 + c) * HW;
     const int64_t n0 = c < C0 ? (C0 - c < gc ? C0 - c : gc) : 0;
     split = n0 * HW;
@@ -144,6 +144,13 @@ __global__ __launch_bounds__(256) void group_norm_stats_kernel(const GnSource<T>
     partial[bg * splits + split] = make_float2(red[0] + red[1] + red[2] + red[3], red[4] + red[5] + red[6] + red[7]);
 }
 
+// (mean, 1/sqrt(var + eps)) from a group's sum and sum of squares over n elements.
+__device__ __forceinline__ float2 gn_stats(float s, float ss, float n, float eps) {
+  const float mean = s / n;
+  const float var = fmaxf(0.0f, ss / n - mean * mean);
+  return make_float2(mean, 1.0f / sqrtf(var + eps));
+}
+
 // (mean, 1/sqrt(var + eps)) of one (sample, group) from its chunk partials, folded by one wave
 // (every lane returns the result).
 __device__ __forceinline__ float2 fold_group_stats(const float2* __restrict__ partial, int64_t bg, int splits,
@@ -156,10 +163,7 @@ __device__ __forceinline__ float2 fold_group_stats(const float2* __restrict__ pa
   }
   s = wave_sum(s);
   ss = wave_sum(ss);
-  const float n = (float)group_size;
-  const float mean = s / n;
-  const float var = fmaxf(0.0f, ss / n - mean * mean);
-  return make_float2(mean, 1.0f / sqrtf(var + eps));
+  return gn_stats(s, ss, (float)group_size, eps);
 }
 
 // Normalised value of one element in the reference's per-dtype form, with the optional SiLU
@@ -167,6 +171,36 @@ __device__ __forceinline__ float2 fold_group_stats(const float2* __restrict__ pa
 // P is the parameter (and computation) dtype: fp16 parameters take the fp16 path's form; fp32
 // parameters over fp16 data are the "upcast" pattern group_norm(x.float(), w32, b32).half(),
 // i.e. the fp32 path's form narrowed once.
+// Statistics of the groups [0, ng) starting at (sample, group) bg0, one group per wave at a
+// time, into st[k]; a wave takes groups k and k + 4 together so that both loads of partials are
+// in flight before either reduction (splits <= 64: one partial per lane).  The same sums, in the
+// same order, as fold_group_stats.
+__device__ __forceinline__ void fold_groups(const float2* __restrict__ partial, int64_t bg0, int ng, int splits,
+                                            int64_t group_size, float eps, int wave, int lane, float2* st) {
+  const float n = (float)group_size;
+  for (int k0 = wave; k0 < ng; k0 += 8) {
+    const int k1 = k0 + 4;
+    float2 p0 = make_float2(0.0f, 0.0f), p1 = make_float2(0.0f, 0.0f);
+    if (lane < splits) {
+      p0 = partial[(bg0 + k0) * splits + lane];
+      if (k1 < ng) p1 = partial[(bg0 + k1) * splits + lane];
+    }
+    float s0 = 0.0f, ss0 = 0.0f, s1 = 0.0f, ss1 = 0.0f;
+    s0 += p0.x;
+    ss0 += p0.y;
+    s1 += p1.x;
+    ss1 += p1.y;
+    s0 = wave_sum(s0);
+    ss0 = wave_sum(ss0);
+    s1 = wave_sum(s1);
+    ss1 = wave_sum(ss1);
+    if (lane == 0) {
+      st[k0] = gn_stats(s0, ss0, n, eps);
+      if (k1 < ng) st[k1] = gn_stats(s1, ss1, n, eps);
+    }
+  }
+}
+
 template <typename T, typename P>
 __device__ __forceinline__ float gn_value(float v, float mean, float inv, float gm, float bt, int fuse_silu) {
   float out;
@@ -199,8 +233,8 @@ __global__ __launch_bounds__(256) void group_norm_apply_kernel(const T* __restri
   }
   __syncthreads();
   const float mean = st_s.x, inv = st_s.y;
-  const int64_t g = bg % groups;
-  const int64_t gc = C / groups;
+  const int64_t g = (uint32_t)bg % (uint32_t)groups;
+  const int64_t gc = (uint32_t)C / (uint32_t)groups;
   const int64_t begin = (int64_t)split * chunk;
   const int64_t end = min(begin + chunk, group_size);
   const T* xb = x + bg * group_size;
@@ -209,7 +243,7 @@ __global__ __launch_bounds__(256) void group_norm_apply_kernel(const T* __restri
     // inner % V == 0, so a vector never straddles two channels.
     constexpr int V = Vec16<T>::N;
     for (int64_t i = begin + (int64_t)threadIdx.x * V; i < end; i += 256 * V) {
-      const int64_t c = g * gc + i / inner;
+      const int64_t c = g * gc + (uint32_t)i / (uint32_t)inner;
       const float gm = gamma ? Elem<P>::load(gamma, c) : 1.0f;
       const float bt = beta ? Elem<P>::load(beta, c) : 0.0f;
       float f[V];
@@ -235,7 +269,7 @@ __global__ __launch_bounds__(256) void group_norm_apply_kernel(const T* __restri
     }
   } else {
     for (int64_t i = begin + threadIdx.x; i < end; i += 256) {
-      const int64_t c = g * gc + i / inner;
+      const int64_t c = g * gc + (uint32_t)i / (uint32_t)inner;
       const float gm = gamma ? Elem<P>::load(gamma, c) : 1.0f;
       const float bt = beta ? Elem<P>::load(beta, c) : 0.0f;
       Elem<T>::store(yb, i, gn_value<T, P>(Elem<T>::load(xb, i), mean, inv, gm, bt, fuse_silu));
@@ -260,8 +294,8 @@ __global__ __launch_bounds__(256) void group_norm_apply_nhwc_kernel(const T* __r
   const int64_t b = blockIdx.z;
   const int64_t p0 = (int64_t)blockIdx.x * 64, c0 = (int64_t)blockIdx.y * 64;
   const int t = threadIdx.x;
-  const int64_t gc = C / groups;
-  const int64_t g_first = c0 / gc;
+  const uint32_t gc = (uint32_t)C / (uint32_t)groups;
+  const int64_t g_first = (uint32_t)c0 / gc;
   const int cl = t >> 2, pl0 = (t & 3) * 16;
   const int64_t c = c0 + cl;
   // The tile's input and affine parameters are requested first; the group statistics are
@@ -288,16 +322,13 @@ __global__ __launch_bounds__(256) void group_norm_apply_nhwc_kernel(const T* __r
   {
     // statistics of the (at most 64) groups this tile's channels belong to, one wave each
     const int64_t c_last = (c0 + 64 < C ? c0 + 64 : C) - 1;
-    const int ng = c0 < C ? (int)(c_last / gc - g_first + 1) : 0;
-    for (int k = t >> 6; k < ng; k += 4) {
-      const float2 st = fold_group_stats(partial, b * groups + g_first + k, splits, gc * HW, eps, t & 63);
-      if ((t & 63) == 0) st_s[k] = st;
-    }
+    const int ng = c0 < C ? (int)((uint32_t)c_last / gc - g_first + 1) : 0;
+    fold_groups(partial, b * groups + g_first, ng, splits, (int64_t)gc * HW, eps, t >> 6, t & 63, st_s);
   }
   __syncthreads();
   {
     if (c < C) {
-      const float2 st = st_s[c / gc - g_first];
+      const float2 st = st_s[(uint32_t)c / gc - g_first];
 #pragma unroll
       for (int j = 0; j < 16; ++j) f[j] = gn_value<T, P>(f[j], st.x, st.y, gm, bt, fuse_silu);
     } else {
@@ -389,8 +420,8 @@ __global__ __launch_bounds__(256) void group_norm_apply_nhwc_f16_kernel(
   const int cp = t & 31, po = t >> 5;  // channel pair, pixel octet
   const int64_t ca = c0 + 2 * cp;
   const int64_t pix = p0 + po * 8;
-  const int64_t gc = C / groups;
-  const int64_t g_first = c0 / gc;
+  const uint32_t gc = (uint32_t)C / (uint32_t)groups;
+  const int64_t g_first = (uint32_t)c0 / gc;
   float fa[8], fb[8];
   float ga = 1.0f, ba = 0.0f, gb = 1.0f, bb = 0.0f;
   auto load_row = [&](int64_t c, float (&f)[8]) {
@@ -415,16 +446,13 @@ __global__ __launch_bounds__(256) void group_norm_apply_nhwc_f16_kernel(
   {
     // statistics of the (at most 64) groups this tile's channels belong to, one wave each
     const int64_t c_last = (c0 + 64 < C ? c0 + 64 : C) - 1;
-    const int ng = c0 < C ? (int)(c_last / gc - g_first + 1) : 0;
-    for (int k = t >> 6; k < ng; k += 4) {
-      const float2 st = fold_group_stats(partial, b * groups + g_first + k, splits, gc * HW, eps, t & 63);
-      if ((t & 63) == 0) st_s[k] = st;
-    }
+    const int ng = c0 < C ? (int)((uint32_t)c_last / gc - g_first + 1) : 0;
+    fold_groups(partial, b * groups + g_first, ng, splits, (int64_t)gc * HW, eps, t >> 6, t & 63, st_s);
   }
   __syncthreads();
   {
-    const float2 sa = ca < C ? st_s[ca / gc - g_first] : make_float2(0.0f, 0.0f);
-    const float2 sb = ca + 1 < C ? st_s[(ca + 1) / gc - g_first] : make_float2(0.0f, 0.0f);
+    const float2 sa = ca < C ? st_s[(uint32_t)ca / gc - g_first] : make_float2(0.0f, 0.0f);
+    const float2 sb = ca + 1 < C ? st_s[(uint32_t)(ca + 1) / gc - g_first] : make_float2(0.0f, 0.0f);
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       uint32_t ha = ca < C ? f2h_fast(gn_value<uint16_t, P>(fa[j], sa.x, sa.y, ga, ba, 0)) : 0u;
@@ -789,6 +817,9 @@ int run_group_norm(int device, const void* x, const void* weight, const void* bi
   const int64_t n_groups = B * groups;
   if (n_groups == 0 || group_size == 0) return MTHIP_OK;
   MTHIP_REQUIRE(n_groups <= 65535, "mthip_group_norm: batch*groups must be <= 65535");
+  // channel and in-group indices are divided in 32-bit arithmetic
+  MTHIP_REQUIRE(group_size < (int64_t(1) << 31) && C < (int64_t(1) << 31) && inner < (int64_t(1) << 31),
+                "mthip_group_norm: a group, the channel count and the spatial size must stay below 2^31 elements");
   constexpr int V = Vec16<T>::N;
   const bool vect = ((uintptr_t)x % 16 == 0) && ((uintptr_t)y % 16 == 0) && inner % V == 0 &&
                     ((uintptr_t)x1 % 16 == 0);
