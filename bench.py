@@ -1,6 +1,6 @@
 """Benchmark of mtorch's SD-UNet hot path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload resnet|linear_gelu|unet|copy_calibration|suite]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload resnet|linear_gelu|unet|copy_calibration|suite|vendor]
                     [--no-cpu] [--no-extras]
 
 Default workload (fp16 leg): the SD ResNet sub-block on a 64x64
@@ -135,7 +135,19 @@ def run_resnet(args):
     mt.cuda.synchronize()
     wall_ms = (time.perf_counter() - t0) * 1e3 / args.steps
     ms_step = start.elapsed_time(end) / args.steps
-    conv_ms = sum(a.elapsed_time(b_) for a, b_ in ev) / args.steps
+    # In a step the conv's event pair also spans its dispatch after the GroupNorm (the event
+    # between them waits for the GroupNorm to finish); the roofline uses the average of `steps`
+    # back-to-back conv launches between two events on the library's stream, which is the
+    # kernel's own duration as rocprofv3's kernel trace reports it.
+    conv_in_step_ms = sum(a.elapsed_time(b_) for a, b_ in ev) / args.steps
+    burst0, burst1 = mt.cuda.Event(), mt.cuda.Event()
+    burst0.record()
+    for _ in range(args.steps):
+        _lib.check(L.mthip_conv2d_nhwc(0, _lib.F16, xn.ptr, wp, bbd.data_ptr(), y.data_ptr(), B, C, H, W, O, 3, 3,
+                                       1, 1, 1, 1, 1, 1, xd.data_ptr(), None, 0))
+    burst1.record()
+    mt.cuda.synchronize()
+    conv_ms = burst0.elapsed_time(burst1) / args.steps
     flops = 2.0 * B * H * W * O * C * 9  # 15.10 GFLOP per step (the conv; GN/SiLU/add are not counted)
     value = flops / (ms_step * 1e-3) / 1e12
     conv_tflops = flops / (conv_ms * 1e-3) / 1e12
@@ -164,8 +176,9 @@ def run_resnet(args):
             "peak": PEAK["fp16_mfma_tflops"],
             "unit": "TFLOP/s",
             "frac": round(conv_tflops / PEAK["fp16_mfma_tflops"], 4),
-            "traffic": _traffic("conv_gemm_resnet_fp16"),
+            "traffic": _traffic("conv_halo_resnet_fp16"),
             "kernel_ms": round(conv_ms, 5),
+            "kernel_ms_in_step": round(conv_in_step_ms, 5),
         },
     }
     if args.cpu:
@@ -466,16 +479,145 @@ def run_suite(args):
     }
 
 
+VENDOR_CONV = ((320, 64), (640, 32), (1280, 16), (1280, 8))
+VENDOR_LINEAR = ((8192, 320, 320), (2048, 640, 640), (512, 1280, 1280), (2048, 640, 2560), (8192, 1280, 320))
+
+
+def _vendor_torch_rows(reps):
+    """torch's F.conv2d (MIOpen, NCHW and channels-last) and F.linear (hipBLASLt) in fp16 on the
+    vendor comparison shapes.  Runs in a child process that never loads libmthip (torch brings its
+    own HIP runtime)."""
+    import torch
+    import torch.nn.functional as TF
+
+    def timed(fn):
+        """(µs per call, how): a CUDA graph of 20 calls replayed `reps` times, or eager calls
+        when the library call cannot be captured."""
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        try:
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                for _ in range(20):
+                    fn()
+            g.replay()
+            torch.cuda.synchronize()
+            s.record()
+            for _ in range(reps):
+                g.replay()
+            e.record()
+            torch.cuda.synchronize()
+            return s.elapsed_time(e) * 1e3 / (reps * 20), "graph"
+        except Exception:  # capture refused: time eager back-to-back calls instead
+            torch.cuda.synchronize()
+            s.record()
+            for _ in range(reps):
+                fn()
+            e.record()
+            torch.cuda.synchronize()
+            return s.elapsed_time(e) * 1e3 / reps, "eager"
+
+    torch.manual_seed(0)
+    out = {"torch": torch.__version__, "conv": [], "linear": []}
+    for C, hw in VENDOR_CONV:
+        tx = torch.randn(2, C, hw, hw, device="cuda", dtype=torch.float16)
+        tw = torch.randn(C, C, 3, 3, device="cuda", dtype=torch.float16) * 0.02
+        tb = torch.randn(C, device="cuda", dtype=torch.float16) * 0.02
+        txc, twc = tx.to(memory_format=torch.channels_last), tw.to(memory_format=torch.channels_last)
+        out["conv"].append((timed(lambda: TF.conv2d(tx, tw, tb, padding=1)),
+                            timed(lambda: TF.conv2d(txc, twc, tb, padding=1))))
+    for M, N, K in VENDOR_LINEAR:
+        tx = torch.randn(M, K, device="cuda", dtype=torch.float16) * 0.5
+        tw = torch.randn(N, K, device="cuda", dtype=torch.float16) * 0.05
+        tb = torch.randn(N, device="cuda", dtype=torch.float16) * 0.05
+        out["linear"].append(timed(lambda: TF.linear(tx, tw, tb)))
+    return out
+
+
+def run_vendor(args):
+    """The contractions of the hot path against the vendor libraries PyTorch-ROCm calls on the same
+    box: F.conv2d (MIOpen, NCHW and channels-last) and F.linear (hipBLASLt) in fp16.  Each side is
+    timed as a graph of 20 calls replayed `steps` times between two events on its own library's
+    stream (the torch side falls back to eager calls where capture is refused, and says so); the
+    torch side runs in a child process.  A comparison, not the headline."""
+    import subprocess
+
+    import mtorch_amd as mt
+
+    F = mt.nn.functional
+    reps = args.steps
+    child = subprocess.run([sys.executable, os.path.abspath(__file__), "--workload", "vendor_torch", "--steps", str(reps)],
+                           capture_output=True, text=True, timeout=600)
+    if child.returncode != 0:
+        raise SystemExit("bench.py vendor: the torch child failed:\n" + child.stderr[-2000:])
+    theirs = json.loads(child.stdout.strip().splitlines()[-1])
+
+    def ours(fn):
+        """µs per call: a HIP graph of 20 calls replayed `reps` times."""
+        for _ in range(3):
+            fn()
+        mt.cuda.synchronize()
+        g = mt.cuda.CUDAGraph()
+        with mt.cuda.graph(g):
+            for _ in range(20):
+                fn()
+        g.replay()
+        mt.cuda.synchronize()
+        s, e = mt.cuda.Event(), mt.cuda.Event()
+        s.record()
+        for _ in range(reps):
+            g.replay()
+        e.record()
+        mt.cuda.synchronize()
+        return s.elapsed_time(e) * 1e3 / (reps * 20)
+
+    rows = []
+    mt.manual_seed(0)
+    for (C, hw), ((nchw, how_a), (nhwc, how_b)) in zip(VENDOR_CONV, theirs["conv"]):
+        flop = 2.0 * 2 * hw * hw * C * C * 9
+        x = (mt.randn(2, C, hw, hw).to("cuda")).half()
+        w = (mt.randn(C, C, 3, 3).to("cuda") * 0.02).half()
+        b = (mt.randn(C).to("cuda") * 0.02).half()
+        us = ours(lambda: F.conv2d(x, w, b, padding=1))
+        rows.append({"op": f"conv3x3 fp16 [2,{C},{hw},{hw}] {C}->{C}", "libmthip_us": round(us, 2),
+                     "libmthip_tflops": round(flop / us / 1e6, 1), "miopen_nchw_us": round(nchw, 2),
+                     "miopen_nchw_tflops": round(flop / nchw / 1e6, 1), "miopen_nhwc_us": round(nhwc, 2),
+                     "miopen_nhwc_tflops": round(flop / nhwc / 1e6, 1), "miopen_timing": [how_a, how_b]})
+        print(json.dumps(rows[-1]), file=sys.stderr, flush=True)
+        del x, w, b
+    for (M, N, K), (th, how) in zip(VENDOR_LINEAR, theirs["linear"]):
+        flop = 2.0 * M * N * K
+        x = (mt.randn(M, K).to("cuda") * 0.5).half()
+        w = (mt.randn(N, K).to("cuda") * 0.05).half()
+        b = (mt.randn(N).to("cuda") * 0.05).half()
+        us = ours(lambda: F.linear(x, w, b))
+        rows.append({"op": f"linear fp16 [{M},{K}]x[{N},{K}]^T + b", "libmthip_us": round(us, 2),
+                     "libmthip_tflops": round(flop / us / 1e6, 1), "hipblaslt_us": round(th, 2),
+                     "hipblaslt_tflops": round(flop / th / 1e6, 1), "hipblaslt_timing": how})
+        print(json.dumps(rows[-1]), file=sys.stderr, flush=True)
+        del x, w, b
+    return {"metric": "fp16 conv3x3 / linear TFLOP/s against MIOpen / hipBLASLt (torch " + theirs["torch"] + ")",
+            "value": None, "unit": "TFLOP/s", "n_gpus": 1, "steps": reps, "warmup": 3, "higher_is_better": True,
+            "scaling": "weak", "vs_baseline": None, "dtype": "fp16", "data": "synthetic",
+            "config": {"workload": "SD-1.5 conv and linear shapes, graph-replayed x20 per side"}, "rows": rows}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", default="resnet", choices=["resnet", "linear_gelu", "unet", "copy_calibration", "suite"])
+    ap.add_argument("--workload", default="resnet", choices=["resnet", "linear_gelu", "unet", "copy_calibration", "suite", "vendor",
+                                                                 "vendor_torch"])
     ap.add_argument("--no-cpu", dest="cpu", action="store_false")
     ap.add_argument("--no-extras", dest="extras", action="store_false",
                     help="resnet workload: skip the UNet step and per-config contraction keys")
     args = ap.parse_args()
+    if args.workload == "vendor_torch":  # child of --workload vendor: torch only, libmthip never loaded
+        print(json.dumps(_vendor_torch_rows(args.steps)), flush=True)
+        return
     if args.gpus != 1:
         print(json.dumps({"error": "this backend measures one MI355X; multi-GPU runs are not part of it",
                           "n_gpus": args.gpus}))
@@ -486,7 +628,7 @@ def main():
         raise SystemExit("bench.py: no GPU visible to libmthip")
     with mt.no_grad():
         run = {"resnet": run_resnet, "linear_gelu": run_linear_gelu, "unet": run_unet,
-               "copy_calibration": run_copy_calibration, "suite": run_suite}
+               "copy_calibration": run_copy_calibration, "suite": run_suite, "vendor": run_vendor}
         out = run[args.workload](args)
     out["device"] = mt.cuda.get_device_name(0)
     print(json.dumps(out), flush=True)
