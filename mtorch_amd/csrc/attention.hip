@@ -72,13 +72,15 @@ __device__ __forceinline__ halfx4 tr_read16(const uint16_t* p) {
 // DVB = ceil(DK/32) 32-row blocks.  VEC: E and Ev are multiples of 8 and every row stride a
 // multiple of 8 elements with 16-byte aligned bases, so K/V/Q move in 16-byte chunks.
 // MASK: the mask kind (MTHIP_MASK_*) fixed at compile time, or -1 to read it at run time.
-// WAVES: query waves per workgroup (32 queries each).  KG: key groups -- KG sets of WAVES
+// WAVES: waves per key group; with DS dim parts they serve WAVES/DS blocks of 32 queries, DS
+// waves per block, each computing the block's scores and 1/DS of its output dims (DS = 1: a
+// wave is a query block).  KG: key groups -- KG sets of WAVES
 // waves take the same queries and alternate 64-key tiles (group g the tiles g, g+KG, ...),
 // each with its own LDS tile and online softmax; at the end group 0 folds in the others'
 // (max, sum, accumulator).  KG = 2 doubles the waves per SIMD on the large self-attentions,
 // where one wave's chain (score MFMAs -> softmax VALU -> PV MFMAs) would otherwise leave the
 // MFMA and VALU pipes idle.
-template <int DK, bool VEC, int MASK, int WAVES, int KG = 1>
+template <int DK, bool VEC, int MASK, int WAVES, int KG = 1, int DS = 1>
 __global__ __launch_bounds__(64 * WAVES * KG) __attribute__((amdgpu_waves_per_eu(KG > 1 ? 4 : 1)))
 void flash_fwd_f16_kernel(const FlashArgs a) {
   constexpr int NT = 64 * WAVES;  // threads of one key group
@@ -92,6 +94,8 @@ void flash_fwd_f16_kernel(const FlashArgs a) {
   constexpr int KCH = (BKV * KCHR + NT - 1) / NT;
   constexpr int VCH = (BKV * VCHR + NT - 1) / NT;
   static_assert(KG == 1 || KG == 2, "one or two key groups");
+  static_assert(DS == 1 || (KG == 1 && WAVES % DS == 0), "dim parts need one key group");
+  constexpr int DVBP = (DVB + DS - 1) / DS;  // 32-dim output blocks per dim part
   // One K/V tile per key group; after the key loop the same memory holds the group merge (one
   // lane's (max, sum) or 16 accumulator values, pitch 17 floats).
   constexpr int TILE = BKV * KP + BKV * VRP;  // halves of one K tile + V tile (16-byte multiple)
@@ -106,7 +110,10 @@ void flash_fwd_f16_kernel(const FlashArgs a) {
   const int64_t bh = blockIdx.y;
   const int64_t b = bh / a.H, head = bh - b * a.H;
   const int64_t kvh = head / (a.H / a.Hk);
-  const int64_t q = (int64_t)blockIdx.x * (32 * WAVES) + wave * 32 + col;
+  // DS dim parts: waves wave/DS own query block wave/DS and the output blocks [dp*DVBP,
+  // dp*DVBP + DVBP) of it, dp = wave % DS (each computes the block's scores itself).
+  const int dp = wave % DS;
+  const int64_t q = (int64_t)blockIdx.x * (32 * WAVES / DS) + (wave / DS) * 32 + col;
   const int Lk = (int)a.Lk, E = (int)a.E, Ev = (int)a.Ev;
   const uint16_t* Q = reinterpret_cast<const uint16_t*>(a.q) + b * a.qs[0] + head * a.qs[1];
   const uint16_t* K = reinterpret_cast<const uint16_t*>(a.k) + b * a.ks[0] + kvh * a.ks[1];
@@ -185,9 +192,9 @@ void flash_fwd_f16_kernel(const FlashArgs a) {
     }
   };
 
-  floatx16 acc[DVB];
+  floatx16 acc[DVBP];
 #pragma unroll
-  for (int i = 0; i < DVB; ++i)
+  for (int i = 0; i < DVBP; ++i)
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[i][r] = 0.0f;
   float m_run = -INFINITY, l_run = 0.0f;
@@ -269,7 +276,7 @@ void flash_fwd_f16_kernel(const FlashArgs a) {
       const float alpha = __builtin_amdgcn_exp2f(m_run - m_cand);  // 0 when m_run = -inf
       l_run *= alpha;
 #pragma unroll
-      for (int i = 0; i < DVB; ++i)
+      for (int i = 0; i < DVBP; ++i)
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[i][r] *= alpha;
       m_run = m_cand;
@@ -295,7 +302,9 @@ void flash_fwd_f16_kernel(const FlashArgs a) {
 #pragma unroll
         for (int j = 0; j < 8; ++j) pf[j] = (_Float16)s[sb][st * 8 + j];
 #pragma unroll
-        for (int i = 0; i < DVB; ++i) {
+        for (int ii = 0; ii < DVBP; ++ii) {
+          const int i = dp * DVBP + ii;  // output block (wave-uniform)
+          if (DS > 1 && i >= DVB) break;
           // Lane l needs V[k][i*32 + l%32] for keys k = K0+0..3 and K0+8..11, K0 = sb*32 +
           // st*16 + 4*(l/32).  In each 16-lane group the transposing read hands lane j the
           // halves [j%4] of the rows read by lanes j/4, j/4+4, j/4+8, j/4+12; so lane r of
@@ -305,7 +314,7 @@ void flash_fwd_f16_kernel(const FlashArgs a) {
           const halfx4 lo = tr_read16(v0);
           const halfx4 hi = tr_read16(v0 + 8 * VRP);
           const halfx8 vf = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-          acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf, acc[i], 0, 0, 0);
+          acc[ii] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf, acc[ii], 0, 0, 0);
         }
       }
     }
@@ -351,28 +360,40 @@ void flash_fwd_f16_kernel(const FlashArgs a) {
   // A fully masked row has l = 0 and, every P being 0, a zero accumulator: 0 * (1/0) = NaN, the
   // reference's 0/0.
   const float inv_l = 1.0f / l_run;
-  // Under VEC, Ev and the output strides are multiples of 8 and the base is 16-byte aligned, so
-  // every 4-dim group below Ev is whole and 8-byte aligned: one straight store each.  (A generic
-  // per-element fallback here would multiply the epilogue's code several times over, and that
-  // straight-line code is fetched cold by every workgroup.)
+  if constexpr (VEC) {
+    // Under VEC, Ev and the output strides are multiples of 8 and the base is 16-byte aligned,
+    // so every 4-dim group below Ev is whole and 8-byte aligned.  All values are narrowed in one
+    // branch-free block, where the 16*DVB independent conversion chains interleave, and the
+    // stores follow, each behind its bounds test: converting inside the guarded store loop split
+    // the block at every group and left each ~21-instruction chain to run at full latency with
+    // one wave per SIMD (about 5 us of a 16x16-latent attention).
+    uint2 h[DVBP][4];
 #pragma unroll
-  for (int i = 0; i < DVB; ++i)
+    for (int i = 0; i < DVBP; ++i)
 #pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      const int d0 = i * 32 + 8 * g + 4 * hh;
-      if (d0 >= Ev) continue;
-      float v[4];
-#pragma unroll
-      for (int t = 0; t < 4; ++t) v[t] = acc[i][4 * g + t] * inv_l;
-      if constexpr (VEC) {
-        uint2 u;
-        u.x = (uint32_t)f2h_generic(v[0]) | ((uint32_t)f2h_generic(v[1]) << 16);
-        u.y = (uint32_t)f2h_generic(v[2]) | ((uint32_t)f2h_generic(v[3]) << 16);
-        *reinterpret_cast<uint2*>(O + d0) = u;
-      } else {
-        for (int t = 0; t < 4 && d0 + t < Ev; ++t) O[d0 + t] = f2h_generic(v[t]);
+      for (int g = 0; g < 4; ++g) {
+        h[i][g].x = (uint32_t)f2h_generic(acc[i][4 * g] * inv_l) |
+                    ((uint32_t)f2h_generic(acc[i][4 * g + 1] * inv_l) << 16);
+        h[i][g].y = (uint32_t)f2h_generic(acc[i][4 * g + 2] * inv_l) |
+                    ((uint32_t)f2h_generic(acc[i][4 * g + 3] * inv_l) << 16);
       }
-    }
+#pragma unroll
+    for (int i = 0; i < DVBP; ++i)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int d0 = (dp * DVBP + i) * 32 + 8 * g + 4 * hh;
+        if (d0 < Ev) *reinterpret_cast<uint2*>(O + d0) = h[i][g];
+      }
+  } else {
+#pragma unroll
+    for (int i = 0; i < DVBP; ++i)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int d0 = (dp * DVBP + i) * 32 + 8 * g + 4 * hh;
+        if (d0 >= Ev) continue;
+        for (int t = 0; t < 4 && d0 + t < Ev; ++t) O[d0 + t] = f2h_generic(acc[i][4 * g + t] * inv_l);
+      }
+  }
 }
 
 // One wave per query: lanes split the head dims; online softmax over keys in fp32 (scores and
@@ -427,18 +448,19 @@ __global__ __launch_bounds__(256) void attention_rowwise_kernel(const FlashArgs 
   }
 }
 
-template <int DK, int WAVES, int KG>
+template <int DK, int WAVES, int KG, int DS = 1>
 void launch_flash_w(const FlashArgs& a, int64_t bh, hipStream_t s, bool vec) {
-  const dim3 grid((unsigned)ceil_div(a.Lq, 32 * WAVES), (unsigned)bh);
+  const dim3 grid((unsigned)ceil_div(a.Lq, 32 * WAVES / DS), (unsigned)bh);
   const dim3 block(64 * WAVES * KG);
   if (!vec) {
-    hipLaunchKernelGGL((flash_fwd_f16_kernel<DK, false, -1, WAVES, KG>), grid, block, 0, s, a);
+    hipLaunchKernelGGL((flash_fwd_f16_kernel<DK, false, -1, WAVES, KG>), dim3((unsigned)ceil_div(a.Lq, 32 * WAVES),
+                       (unsigned)bh), block, 0, s, a);
   } else if (a.mask_kind == MTHIP_MASK_NONE) {
-    hipLaunchKernelGGL((flash_fwd_f16_kernel<DK, true, MTHIP_MASK_NONE, WAVES, KG>), grid, block, 0, s, a);
+    hipLaunchKernelGGL((flash_fwd_f16_kernel<DK, true, MTHIP_MASK_NONE, WAVES, KG, DS>), grid, block, 0, s, a);
   } else if (a.mask_kind == MTHIP_MASK_BOOL) {
-    hipLaunchKernelGGL((flash_fwd_f16_kernel<DK, true, MTHIP_MASK_BOOL, WAVES, KG>), grid, block, 0, s, a);
+    hipLaunchKernelGGL((flash_fwd_f16_kernel<DK, true, MTHIP_MASK_BOOL, WAVES, KG, DS>), grid, block, 0, s, a);
   } else {
-    hipLaunchKernelGGL((flash_fwd_f16_kernel<DK, true, MTHIP_MASK_ADD, WAVES, KG>), grid, block, 0, s, a);
+    hipLaunchKernelGGL((flash_fwd_f16_kernel<DK, true, MTHIP_MASK_ADD, WAVES, KG, DS>), grid, block, 0, s, a);
   }
 }
 
@@ -456,6 +478,17 @@ void launch_flash(const FlashArgs& a, int64_t bh, hipStream_t s, bool vec) {
                          dim3((unsigned)ceil_div(a.Lq, 128), (unsigned)bh), dim3(512), 0, s, a);
       return;
     }
+  }
+  // Head dims above 80 (SD's 160 at the 16x16 and 8x8 latents): four dim parts, so a workgroup
+  // serves 32 queries and each wave runs a quarter of the value product and of the epilogue.
+  // Those grids are 16-32 workgroups of one wave per SIMD, whose issue slots bound them; the
+  // parts quadruple the SIMDs in use at the cost of recomputing each block's scores (measured at
+  // 16x16: one key tile 9.9 -> 7.0 us, 77 keys 12.1 -> 9.5 us, 256 keys 14.6 -> 12.5 us).  At
+  // head dim 80 the recomputed scores cost as much as the parts save (32x32, 1024 keys: 25.5
+  // against 27.3 us with two parts).
+  if constexpr (DK > 80) {
+    launch_flash_w<DK, 4, 1, 4>(a, bh, s, vec);
+    return;
   }
   launch_flash_w<DK, 4, 1>(a, bh, s, vec);
 }

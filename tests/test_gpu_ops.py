@@ -513,6 +513,25 @@ def test_sdpa_masks_causal_scale(dt):
         assert rel(val(got), val(ref)) <= TOL[dt], c
 
 
+@pytest.mark.parametrize("Lq,Lk,E,Ev", [(70, 90, 136, 136), (33, 200, 96, 96), (64, 77, 160, 120), (130, 64, 160, 160)])
+def test_sdpa_dim_parts(Lq, Lk, E, Ev):
+    """Head dims above 80 run four dim parts per 32-query block (each wave: the block's scores, a
+    quarter of the output dims): parts with fewer or no 32-dim blocks (136, 96), a value dim
+    narrower than the key dim, ragged query blocks, masks and causal."""
+    g = Gen(Lq + Lk + E + Ev)
+    q = g.randn((2, 3, Lq, E), "float16")
+    k = g.randn((2, 3, Lk, E), "float16")
+    v = g.randn((2, 3, Lk, Ev), "float16")
+    rng = np.random.default_rng(Lq)
+    bmask = rng.random((2, 1, Lq, Lk)) > 0.3
+    bmask[..., 0] = True
+    amask = (rng.standard_normal((Lq, Lk)) * 2).astype(np.float32)
+    for m, causal in ((None, False), (bmask, False), (amask, False), (None, True), (bmask, True)):
+        md = None if m is None else mt.from_numpy(m).to("cuda")
+        got = host(F.scaled_dot_product_attention(dev(q), dev(k), dev(v), attn_mask=md, is_causal=causal))
+        assert rel(val(got), val(orc.sdpa(q, k, v, m, causal))) <= TOL["float16"], (m is None, causal)
+
+
 def test_sdpa_fully_masked_row_is_nan_and_gqa():
     g = Gen(62)
     q = g.randn((1, 4, 40, 40), "float16")
