@@ -40,6 +40,8 @@ int check_launch(const char* what);
 // 65536-entry fp16 table of erf-gelu indexed by the input's bits, bit-identical to evaluating
 // it; filled on first use per device (nullptr if that failed).
 const uint16_t* gelu_f16_lookup(int device, hipStream_t s);
+// The fp16 SiLU of every half value (silu_half), filled once per device (norm.hip).
+const uint16_t* silu_f16_lookup(int device, hipStream_t s);
 
 __host__ __device__ inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 

@@ -347,6 +347,39 @@ __global__ void unary_vec_kernel(const uint4* __restrict__ x, uint4* __restrict_
   }
 }
 
+// fp16 SiLU / erf-GELU over large buffers: one 1024-thread workgroup per CU copies the op's
+// 64 K-entry result table (128 KB, exactly what evaluating the op gives for each half) into LDS,
+// then streams 16-byte chunks, four per thread in flight, each half looked up in LDS: about four
+// vector instructions per element where evaluating SiLU costs ~30 (two of them quarter-rate
+// transcendentals) and the GELU table gathers from L2.
+constexpr int kLutThreads = 1024;
+__global__ __launch_bounds__(1024) void unary_lut_f16_kernel(const uint4* __restrict__ x, uint4* __restrict__ y,
+                                                             int64_t nvec, const uint4* __restrict__ tab) {
+  __shared__ uint4 lut[65536 * 2 / 16];
+  for (int i = threadIdx.x; i < 65536 * 2 / 16; i += kLutThreads) lut[i] = tab[i];
+  __syncthreads();
+  const uint16_t* L = reinterpret_cast<const uint16_t*>(lut);
+  constexpr int U = 4;
+  const int64_t stride = (int64_t)gridDim.x * kLutThreads;
+  for (int64_t i0 = (int64_t)blockIdx.x * kLutThreads + threadIdx.x; i0 < nvec; i0 += stride * U) {
+    uint4 r[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      if (i0 + u * stride < nvec) r[u] = x[i0 + u * stride];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (i0 + u * stride >= nvec) break;
+      uint32_t w[4] = {r[u].x, r[u].y, r[u].z, r[u].w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) w[j] = (uint32_t)L[w[j] & 0xffffu] | ((uint32_t)L[w[j] >> 16] << 16);
+      y[i0 + u * stride] = make_uint4(w[0], w[1], w[2], w[3]);
+    }
+  }
+}
+
+// Chunks from which the LDS-table kernel pays for its 128 KB table fill per CU.
+constexpr int64_t kLutMinVec = 1 << 18;
+
 template <typename T>
 void launch_unary_vec(int op, const void* x, void* y, int64_t nvec, const uint16_t* tab, hipStream_t s) {
   const dim3 grid(grid_for(nvec, 2)), block(kThreads);
@@ -777,7 +810,16 @@ int mthip_unary(int device, int op, int dtype, const void* x, void* y, int64_t n
   int64_t done = 0;
   if ((((uintptr_t)x | (uintptr_t)y) & 15) == 0 && n * esz >= 16) {
     const int64_t nvec = n * esz / 16;
-    if (dtype == MTHIP_F16)
+    const bool lut = dtype == MTHIP_F16 && (op == MTHIP_UNARY_SILU || op == MTHIP_UNARY_GELU) && nvec >= kLutMinVec;
+    if (lut) {
+      const uint16_t* tab = op == MTHIP_UNARY_GELU ? gelu_f16_lookup(device, s) : silu_f16_lookup(device, s);
+      if (!tab) return fail(MTHIP_ERR_HIP, "mthip_unary: table setup failed");
+      int cus = 0;
+      if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess || cus < 1) cus = 256;
+      const int64_t grid = std::min<int64_t>(cus, ceil_div(nvec, kLutThreads));
+      hipLaunchKernelGGL(unary_lut_f16_kernel, dim3((unsigned)grid), dim3(kLutThreads), 0, s, (const uint4*)x,
+                         (uint4*)y, nvec, (const uint4*)tab);
+    } else if (dtype == MTHIP_F16)
       launch_unary_vec<uint16_t>(op, x, y, nvec, op == MTHIP_UNARY_GELU ? gelu_f16_lookup(device, s) : nullptr, s);
     else
       launch_unary_vec<float>(op, x, y, nvec, nullptr, s);

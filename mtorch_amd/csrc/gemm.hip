@@ -285,7 +285,7 @@ constexpr int64_t kMaxBufferBytes = (int64_t(1) << 31) - 1;
 // fp16 gelu of every half value, as mtorch's fp16 path computes it (tensor.cpp:17225-17235):
 // a GEGLU gate is always an fp16 value, so the fused epilogue looks its gelu up instead of
 // evaluating a double-precision erf per element.  Filled once per device.
-__device__ uint16_t g_gelu_f16_table[65536];
+__device__ __align__(16) uint16_t g_gelu_f16_table[65536];
 
 __global__ void gelu_f16_table_kernel(uint16_t* tab) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;

@@ -370,7 +370,7 @@ __global__ __launch_bounds__(256) void group_norm_apply_nhwc_kernel(const T* __r
 // channels-last apply kernel looks the activation of each narrowed normalised value up by its
 // bits, one gather where evaluating it costs ~20 vector instructions per element.  Filled once
 // per device.
-__device__ uint16_t g_silu_f16_table[65536];
+__device__ __align__(16) uint16_t g_silu_f16_table[65536];
 
 __global__ void silu_f16_table_kernel(uint16_t* tab) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
@@ -975,6 +975,8 @@ int run_softmax(const void* x, void* y, int64_t rows, int64_t cols, int divide, 
 }
 
 }  // namespace
+
+const uint16_t* silu_f16_lookup(int device, hipStream_t s) { return silu_f16_table(device, s); }
 
 }  // namespace mthip
 

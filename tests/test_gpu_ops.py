@@ -149,6 +149,24 @@ def test_silu_fp16_every_half_is_bit_exact():
     assert bad.size == 0, [(hex(i), hex(got[i]), hex(ref[i])) for i in bad[:8]]
 
 
+def test_silu_gelu_fp16_lds_table_path_is_bit_exact():
+    """Buffers of >= 2^21 halves take the kernel that looks SiLU / erf-GELU up in an LDS copy of
+    the 64 K-entry table: every half input, repeated past that size with a ragged 16-byte tail,
+    gives the same bits as the scalar kernel on the same halves and, for SiLU, as the oracle."""
+    allh = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    big = np.tile(allh, 40)[: 40 * 65536 - 3]  # 2,621,437 halves: table kernel + scalar tail
+    t = dev(big)
+    for name, fn in [("silu", F.silu), ("gelu", F.gelu)]:
+        got = host(fn(t))
+        ref = host(fn(dev(allh)[1:]))  # one element in: the unaligned scalar kernel
+        ref = np.concatenate([host(fn(dev(allh[:1]))), ref])
+        exp = np.tile(ref, 40)[: big.size]
+        bad = np.nonzero(got != exp)[0]
+        assert bad.size == 0, (name, [(int(big[i]), hex(got[i]), hex(exp[i])) for i in bad[:8]])
+    got = host(F.silu(t))
+    assert np.array_equal(got, np.tile(orc.silu(allh), 40)[: big.size])
+
+
 @pytest.mark.parametrize("dt", ["float32", "float16"])
 def test_unary_vector_path_equals_scalar_path(dt):
     """Aligned inputs go through the 16-byte-per-lane kernel (fp16 silu and erf-gelu as table
