@@ -26,6 +26,53 @@ inline unsigned grid_for(int64_t work_items, int per_thread = 1) {
   return (unsigned)std::min<int64_t>(blocks, 256 * 32);
 }
 
+// Streaming kernels (same-shape elementwise ops over 16-byte chunks): U chunks per thread in
+// flight and at most two 256-thread workgroups per CU -- the shape at which a plain copy of a
+// 640 MB read+write stream ran fastest on MI355X (6.1 TB/s with non-temporal accesses, 5.8
+// without; four or more workgroups per CU, or one chunk per thread, stayed at 4.6-5.4 TB/s).
+// Buffers above kStreamNTBytes are read and written non-temporally (not kept in the caches):
+// their data would not fit the caches anyway, while the smaller intermediates of a model step
+// are read back by the next kernel from L2 or the Infinity Cache.
+constexpr int kStreamU = 4;
+constexpr int64_t kStreamNTBytes = int64_t(64) << 20;
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+template <bool NT>
+__device__ __forceinline__ uint4 ld16(const uint4* p) {
+  if constexpr (NT) {
+    const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+  } else {
+    return *p;
+  }
+}
+
+template <bool NT>
+__device__ __forceinline__ void st16(uint4* p, const uint4 v) {
+  if constexpr (NT) {
+    const u32x4 w = {v.x, v.y, v.z, v.w};
+    __builtin_nontemporal_store(w, reinterpret_cast<u32x4*>(p));
+  } else {
+    *p = v;
+  }
+}
+
+int cu_count_dev(int device) {
+  static int cached[64] = {0};
+  if (device < 0 || device >= 64) return 256;
+  if (cached[device] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess || n < 1) n = 256;
+    cached[device] = n;
+  }
+  return cached[device];
+}
+
+inline unsigned stream_grid(int device, int64_t nvec) {
+  return (unsigned)std::max<int64_t>(1, std::min<int64_t>(ceil_div(nvec, (int64_t)kThreads * kStreamU),
+                                                          2 * (int64_t)cu_count_dev(device)));
+}
+
 struct Shape {
   int rank;
   int64_t sizes[kMaxRank];
@@ -214,21 +261,37 @@ __global__ void binary_contig_kernel(int op, const T* __restrict__ a, const T* _
     Elem<T>::store(out, i, apply_bin(op, Elem<T>::load(a, i), Elem<T>::load(b, i)));
 }
 
-// fp16 same-shape add/mul with 8 lanes-elements per 16-byte access.
-__global__ void binary_contig_h8_kernel(int op, const uint4* __restrict__ a, const uint4* __restrict__ b,
-                                        uint4* __restrict__ out, int64_t nvec) {
+// Same-shape binary op over 16-byte chunks (8 halves or 4 floats), streamed.
+template <typename T, bool NT, int U>
+__global__ __launch_bounds__(256) void binary_contig_vec_kernel(int op, const uint4* __restrict__ a,
+                                                                const uint4* __restrict__ b, uint4* __restrict__ out,
+                                                                int64_t nvec) {
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-  for (int64_t v = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; v < nvec; v += stride) {
-    const uint4 x = a[v], y = b[v];
-    const uint32_t xs[4] = {x.x, x.y, x.z, x.w}, ys[4] = {y.x, y.y, y.z, y.w};
-    uint32_t r[4];
+  for (int64_t i0 = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i0 < nvec; i0 += stride * U) {
+    uint4 x[U], y[U];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const float lo = apply_bin(op, h2f_bits((uint16_t)(xs[j] & 0xffff)), h2f_bits((uint16_t)(ys[j] & 0xffff)));
-      const float hi = apply_bin(op, h2f_bits((uint16_t)(xs[j] >> 16)), h2f_bits((uint16_t)(ys[j] >> 16)));
-      r[j] = (uint32_t)f2h_bits(lo) | ((uint32_t)f2h_bits(hi) << 16);
+    for (int u = 0; u < U; ++u)
+      if (i0 + u * stride < nvec) {
+        x[u] = ld16<NT>(a + i0 + u * stride);
+        y[u] = ld16<NT>(b + i0 + u * stride);
+      }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (i0 + u * stride >= nvec) break;
+      const uint32_t xs[4] = {x[u].x, x[u].y, x[u].z, x[u].w}, ys[4] = {y[u].x, y[u].y, y[u].z, y[u].w};
+      uint32_t r[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        if constexpr (sizeof(T) == 2) {
+          const float lo = apply_bin(op, h2f_bits((uint16_t)(xs[j] & 0xffff)), h2f_bits((uint16_t)(ys[j] & 0xffff)));
+          const float hi = apply_bin(op, h2f_bits((uint16_t)(xs[j] >> 16)), h2f_bits((uint16_t)(ys[j] >> 16)));
+          r[j] = (uint32_t)f2h_fast(lo) | ((uint32_t)f2h_fast(hi) << 16);
+        } else {
+          r[j] = __float_as_uint(apply_bin(op, __uint_as_float(xs[j]), __uint_as_float(ys[j])));
+        }
+      }
+      st16<NT>(out + i0 + u * stride, make_uint4(r[0], r[1], r[2], r[3]));
     }
-    out[v] = make_uint4(r[0], r[1], r[2], r[3]);
   }
 }
 
@@ -317,12 +380,20 @@ __global__ void unary_kernel(int op, const T* __restrict__ x, T* __restrict__ y,
 // 16-byte chunks per lane (8 halves or 4 floats) over 16-byte aligned buffers, the op fixed at
 // compile time.  With `tab` (fp16 erf-gelu, whose evaluation needs a double-precision erf) each
 // half is looked up by its bits instead.
-template <typename T, int OP>
-__global__ void unary_vec_kernel(const uint4* __restrict__ x, uint4* __restrict__ y, int64_t nvec,
-                                 const uint16_t* __restrict__ tab) {
+template <typename T, int OP, bool NT, int U>
+__global__ __launch_bounds__(256) void unary_vec_kernel(const uint4* __restrict__ x, uint4* __restrict__ y,
+                                                        int64_t nvec, const uint16_t* __restrict__ tab) {
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < nvec; i += stride) {
-    uint4 r = x[i];
+  for (int64_t i0 = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i0 < nvec; i0 += stride * U) {
+  uint4 rr[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u)
+    if (i0 + u * stride < nvec) rr[u] = ld16<NT>(x + i0 + u * stride);
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int64_t i = i0 + u * stride;
+    if (i >= nvec) break;
+    const uint4 r = rr[u];
     uint32_t w[4] = {r.x, r.y, r.z, r.w};
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -343,36 +414,38 @@ __global__ void unary_vec_kernel(const uint4* __restrict__ x, uint4* __restrict_
         w[j] = __float_as_uint(apply_unary<T>(OP, __uint_as_float(w[j])));
       }
     }
-    y[i] = make_uint4(w[0], w[1], w[2], w[3]);
+    st16<NT>(y + i, make_uint4(w[0], w[1], w[2], w[3]));
+  }
   }
 }
 
-// fp16 SiLU / erf-GELU over large buffers: one 1024-thread workgroup per CU copies the op's
-// 64 K-entry result table (128 KB, exactly what evaluating the op gives for each half) into LDS,
-// then streams 16-byte chunks, four per thread in flight, each half looked up in LDS: about four
+// fp16 SiLU / erf-GELU over large buffers: one workgroup per CU copies the op's 64 K-entry
+// result table (128 KB, exactly what evaluating the op gives for each half) into LDS, then
+// streams 16-byte chunks, four per thread in flight, each half looked up in LDS: about four
 // vector instructions per element where evaluating SiLU costs ~30 (two of them quarter-rate
 // transcendentals) and the GELU table gathers from L2.
-constexpr int kLutThreads = 1024;
-__global__ __launch_bounds__(1024) void unary_lut_f16_kernel(const uint4* __restrict__ x, uint4* __restrict__ y,
-                                                             int64_t nvec, const uint4* __restrict__ tab) {
+// TH threads: 256 for buffers that stream from HBM (see kStreamU), 1024 below that, where
+// filling the table with more waves, and more waves per CU, matter more.
+template <bool NT, int TH>
+__global__ __launch_bounds__(TH) void unary_lut_f16_kernel(const uint4* __restrict__ x, uint4* __restrict__ y,
+                                                           int64_t nvec, const uint4* __restrict__ tab) {
   __shared__ uint4 lut[65536 * 2 / 16];
-  for (int i = threadIdx.x; i < 65536 * 2 / 16; i += kLutThreads) lut[i] = tab[i];
+  for (int i = threadIdx.x; i < 65536 * 2 / 16; i += TH) lut[i] = tab[i];
   __syncthreads();
   const uint16_t* L = reinterpret_cast<const uint16_t*>(lut);
-  constexpr int U = 4;
-  const int64_t stride = (int64_t)gridDim.x * kLutThreads;
-  for (int64_t i0 = (int64_t)blockIdx.x * kLutThreads + threadIdx.x; i0 < nvec; i0 += stride * U) {
-    uint4 r[U];
+  const int64_t stride = (int64_t)gridDim.x * TH;
+  for (int64_t i0 = (int64_t)blockIdx.x * TH + threadIdx.x; i0 < nvec; i0 += stride * kStreamU) {
+    uint4 r[kStreamU];
 #pragma unroll
-    for (int u = 0; u < U; ++u)
-      if (i0 + u * stride < nvec) r[u] = x[i0 + u * stride];
+    for (int u = 0; u < kStreamU; ++u)
+      if (i0 + u * stride < nvec) r[u] = ld16<NT>(x + i0 + u * stride);
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
+    for (int u = 0; u < kStreamU; ++u) {
       if (i0 + u * stride >= nvec) break;
       uint32_t w[4] = {r[u].x, r[u].y, r[u].z, r[u].w};
 #pragma unroll
       for (int j = 0; j < 4; ++j) w[j] = (uint32_t)L[w[j] & 0xffffu] | ((uint32_t)L[w[j] >> 16] << 16);
-      y[i0 + u * stride] = make_uint4(w[0], w[1], w[2], w[3]);
+      st16<NT>(y + i0 + u * stride, make_uint4(w[0], w[1], w[2], w[3]));
     }
   }
 }
@@ -380,14 +453,15 @@ __global__ __launch_bounds__(1024) void unary_lut_f16_kernel(const uint4* __rest
 // Chunks from which the LDS-table kernel pays for its 128 KB table fill per CU.
 constexpr int64_t kLutMinVec = 1 << 18;
 
-template <typename T>
-void launch_unary_vec(int op, const void* x, void* y, int64_t nvec, const uint16_t* tab, hipStream_t s) {
-  const dim3 grid(grid_for(nvec, 2)), block(kThreads);
+template <typename T, bool NT, int U>
+void launch_unary_vec_nt(int device, int op, const void* x, void* y, int64_t nvec, const uint16_t* tab,
+                         hipStream_t s) {
+  const dim3 grid(U > 1 ? stream_grid(device, nvec) : grid_for(nvec, 2)), block(kThreads);
   const uint4* xv = (const uint4*)x;
   uint4* yv = (uint4*)y;
   switch (op) {
 #define MTHIP_UNARY_CASE(K) \
-    case K: hipLaunchKernelGGL((unary_vec_kernel<T, K>), grid, block, 0, s, xv, yv, nvec, tab); break;
+    case K: hipLaunchKernelGGL((unary_vec_kernel<T, K, NT, U>), grid, block, 0, s, xv, yv, nvec, tab); break;
     MTHIP_UNARY_CASE(MTHIP_UNARY_SILU)
     MTHIP_UNARY_CASE(MTHIP_UNARY_GELU)
     MTHIP_UNARY_CASE(MTHIP_UNARY_GELU_TANH)
@@ -399,6 +473,21 @@ void launch_unary_vec(int op, const void* x, void* y, int64_t nvec, const uint16
     default: MTHIP_UNARY_CASE(MTHIP_UNARY_RELU)
 #undef MTHIP_UNARY_CASE
   }
+}
+
+// Large fp32 buffers of the cheap ops stream (see kStreamU); the evaluated fp16 forms, the erf
+// and tanh GELUs and the double-precision exp/sin/cos keep one chunk per thread with more waves
+// per CU, which hides their vector work better.
+template <typename T>
+void launch_unary_vec(int device, int op, const void* x, void* y, int64_t nvec, const uint16_t* tab, hipStream_t s) {
+  const bool big = 2 * nvec * 16 > kStreamNTBytes;
+  const bool cheap = sizeof(T) == 4 && (op == MTHIP_UNARY_SILU || op == MTHIP_UNARY_NEG || op == MTHIP_UNARY_RELU);
+  if (big && cheap)
+    launch_unary_vec_nt<T, true, kStreamU>(device, op, x, y, nvec, tab, s);
+  else if (big)
+    launch_unary_vec_nt<T, true, 1>(device, op, x, y, nvec, tab, s);
+  else
+    launch_unary_vec_nt<T, false, 1>(device, op, x, y, nvec, tab, s);
 }
 
 template <typename T>
@@ -767,10 +856,25 @@ int mthip_binary(int device, int op, int dtype, const void* a, const int64_t* a_
   sh.rank = collapse(rank, out_sizes, ins, 3, sh.sizes, outs);
   const bool contig = sh.rank <= 1 && (sh.rank == 0 || (sh.a_strides[0] == 1 && sh.b_strides[0] == 1));
   const unsigned g = grid_for(n);
-  if (contig) {
-    if (dtype == MTHIP_F16 && n % 8 == 0 && (uintptr_t)a % 16 == 0 && (uintptr_t)b % 16 == 0 && (uintptr_t)out % 16 == 0)
-      hipLaunchKernelGGL(binary_contig_h8_kernel, dim3(grid_for(n / 8)), dim3(kThreads), 0, s, op, (const uint4*)a, (const uint4*)b, (uint4*)out, n / 8);
-    else if (dtype == MTHIP_F16)
+  const int esz = dtype == MTHIP_F16 ? 2 : 4;
+  if (contig && (n * esz) % 16 == 0 && (((uintptr_t)a | (uintptr_t)b | (uintptr_t)out) & 15) == 0) {
+    const int64_t nvec = n * esz / 16;
+    const uint4 *av = (const uint4*)a, *bv = (const uint4*)b;
+    uint4* ov = (uint4*)out;
+    // Large fp32 buffers stream (see kStreamU); the narrowing in fp16 ops keeps one chunk per
+    // thread, more waves per CU and cached accesses (64x batch: 202 us against 212 us non-temporal
+    // and 263 us streamed).
+    if (3 * n * esz > kStreamNTBytes && dtype == MTHIP_F32)
+      hipLaunchKernelGGL((binary_contig_vec_kernel<float, true, kStreamU>), dim3(stream_grid(device, nvec)),
+                         dim3(kThreads), 0, s, op, av, bv, ov, nvec);
+    else if (dtype == MTHIP_F32)
+      hipLaunchKernelGGL((binary_contig_vec_kernel<float, false, 1>), dim3(grid_for(nvec)), dim3(kThreads), 0, s, op,
+                         av, bv, ov, nvec);
+    else
+      hipLaunchKernelGGL((binary_contig_vec_kernel<uint16_t, false, 1>), dim3(grid_for(nvec)), dim3(kThreads), 0, s,
+                         op, av, bv, ov, nvec);
+  } else if (contig) {
+    if (dtype == MTHIP_F16)
       hipLaunchKernelGGL(binary_contig_kernel<uint16_t>, dim3(g), dim3(kThreads), 0, s, op, (const uint16_t*)a, (const uint16_t*)b, (uint16_t*)out, n);
     else
       hipLaunchKernelGGL(binary_contig_kernel<float>, dim3(g), dim3(kThreads), 0, s, op, (const float*)a, (const float*)b, (float*)out, n);
@@ -814,15 +918,20 @@ int mthip_unary(int device, int op, int dtype, const void* x, void* y, int64_t n
     if (lut) {
       const uint16_t* tab = op == MTHIP_UNARY_GELU ? gelu_f16_lookup(device, s) : silu_f16_lookup(device, s);
       if (!tab) return fail(MTHIP_ERR_HIP, "mthip_unary: table setup failed");
-      int cus = 0;
-      if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess || cus < 1) cus = 256;
-      const int64_t grid = std::min<int64_t>(cus, ceil_div(nvec, kLutThreads));
-      hipLaunchKernelGGL(unary_lut_f16_kernel, dim3((unsigned)grid), dim3(kLutThreads), 0, s, (const uint4*)x,
-                         (uint4*)y, nvec, (const uint4*)tab);
+      // one workgroup per CU (the table fills the LDS)
+      if (2 * nvec * 16 > kStreamNTBytes)
+        hipLaunchKernelGGL((unary_lut_f16_kernel<true, 256>), dim3((unsigned)std::min<int64_t>(cu_count_dev(device),
+                                                                                              ceil_div(nvec, 256))),
+                           dim3(256), 0, s, (const uint4*)x, (uint4*)y, nvec, (const uint4*)tab);
+      else
+        hipLaunchKernelGGL((unary_lut_f16_kernel<false, 1024>), dim3((unsigned)std::min<int64_t>(cu_count_dev(device),
+                                                                                                 ceil_div(nvec, 1024))),
+                           dim3(1024), 0, s, (const uint4*)x, (uint4*)y, nvec, (const uint4*)tab);
     } else if (dtype == MTHIP_F16)
-      launch_unary_vec<uint16_t>(op, x, y, nvec, op == MTHIP_UNARY_GELU ? gelu_f16_lookup(device, s) : nullptr, s);
+      launch_unary_vec<uint16_t>(device, op, x, y, nvec, op == MTHIP_UNARY_GELU ? gelu_f16_lookup(device, s) : nullptr,
+                                 s);
     else
-      launch_unary_vec<float>(op, x, y, nvec, nullptr, s);
+      launch_unary_vec<float>(device, op, x, y, nvec, nullptr, s);
     done = nvec * 16 / esz;
   }
   if (done < n) {
