@@ -139,6 +139,26 @@ __device__ __forceinline__ uint16_t f2h_fast(float value) {
   return (uint16_t)h;
 }
 
+// mtorch's fp16 narrowing for every value except NaN (which gives an infinity), branch-free and
+// without the hardware conversion: about 10 VALU operations against f2h_generic's ~20.
+//  * |value| >= 2^-14 (normal halves, overflow): adding 0x1000 to the bit pattern rounds the 13
+//    discarded significand bits half-up in magnitude (a carry moves into the exponent);
+//    subtracting (127 - 15) << 23 at the same time rebiases the exponent, and results from
+//    65520 up (and inf) clamp to 0x7c00.
+//  * |value| < 2^-14 (subnormal halves): the result counts units of 2^-24, floor(|v| * 2^24 +
+//    0.5).  fma(|v|, 2^24, 0.5 - 2^-25) produces that floor exactly under round-to-nearest-even
+//    (the sum of 0.5 itself and the float just below 2^-25, scaled, would round up to 1).
+// Epilogues narrow with it, record whether any lane met a NaN, and redo their values with
+// f2h_generic in the rare wave that did.  Equal to f2h_generic for every non-NaN float, with or
+// without fp32 denormal flushing (tests/f2h_fast_model.c checks all 2^32 patterns).
+__device__ __forceinline__ uint32_t f2h_nonnan(float value) {
+  const uint32_t bits = __float_as_uint(value);
+  const uint32_t hn = min(((bits - 0x37fff000u) >> 13) & 0x3ffffu, 0x7c00u);
+  const float av = __builtin_fabsf(value);
+  const uint32_t hs = (uint32_t)__builtin_fmaf(av, 16777216.0f, 0x1.fffffep-2f);
+  return (av < 0x1p-14f ? hs : hn) | ((bits >> 16) & 0x8000u);
+}
+
 // Exact widening; finite values and infinities match tensor.cpp:317-344 bit for bit.
 __device__ __forceinline__ float h2f_bits(uint16_t h) {
   return (float)__builtin_bit_cast(_Float16, h);

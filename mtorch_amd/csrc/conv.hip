@@ -137,7 +137,15 @@ int launch_halo(int device, HaloArgs h, hipStream_t s) {
     if (int rc = mthip_malloc(device, (size_t)((int64_t)h.ksplit * h.O * h.ld_partial) * sizeof(float), &ws)) return rc;
     h.partial = static_cast<float*>(ws);
   }
-  hipLaunchKernelGGL((conv3x3_halo_kernel<BM, TR, TW, 1, 6>), dim3((unsigned)units), dim3(320), 0, s, h);
+  const bool ha = h.ksplit == 1 && h.chan_add != nullptr, hr = h.ksplit == 1 && h.residual != nullptr;
+  if (ha && hr)
+    hipLaunchKernelGGL((conv3x3_halo_kernel<BM, TR, TW, 1, 6, true, true>), dim3((unsigned)units), dim3(320), 0, s, h);
+  else if (ha)
+    hipLaunchKernelGGL((conv3x3_halo_kernel<BM, TR, TW, 1, 6, true, false>), dim3((unsigned)units), dim3(320), 0, s, h);
+  else if (hr)
+    hipLaunchKernelGGL((conv3x3_halo_kernel<BM, TR, TW, 1, 6, false, true>), dim3((unsigned)units), dim3(320), 0, s, h);
+  else
+    hipLaunchKernelGGL((conv3x3_halo_kernel<BM, TR, TW, 1, 6, false, false>), dim3((unsigned)units), dim3(320), 0, s, h);
   int rc = check_launch("conv3x3_halo_kernel");
   if (rc == MTHIP_OK && h.ksplit > 1) {
     GemmArgs a{};

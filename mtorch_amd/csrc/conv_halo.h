@@ -93,7 +93,9 @@ struct HaloSchedule {
   }
 };
 
-template <int BM, int TR, int TW, int WGM, int SW>
+// HAS_A / HAS_R: the epilogue adds chan_add / residual (fixed at compile time so that the
+// epilogue is one straight-line block; a K-split launch writes fp32 partials and uses neither).
+template <int BM, int TR, int TW, int WGM, int SW, bool HAS_A, bool HAS_R>
 __global__ __launch_bounds__(320) void conv3x3_halo_kernel(const HaloArgs args) {
   constexpr int NW = 4;                 // compute waves (the fifth wave is the producer)
   constexpr int WGN = NW / WGM;
@@ -260,11 +262,11 @@ __global__ __launch_bounds__(320) void conv3x3_halo_kernel(const HaloArgs args) 
     oc[fc] = o0 + wm * WMO + fc * 16 + (lane & 15);
     const int orr = oc[fc] < O ? oc[fc] : O - 1;
     bh[fc] = __builtin_amdgcn_raw_buffer_load_b16(b_rsrc, orr * 2, 0, 0);
-    ah[fc] = __builtin_amdgcn_raw_buffer_load_b16(c_rsrc, (img * args.chan_add_ld + orr) * 2, 0, 0);
+    ah[fc] = HAS_A ? __builtin_amdgcn_raw_buffer_load_b16(c_rsrc, (img * args.chan_add_ld + orr) * 2, 0, 0) : 0;
   }
   Raw4<T> rz[FP][FC];
 #pragma unroll
-  for (int fp = 0; fp < FP; ++fp) {
+  for (int fp = 0; fp < FP && HAS_R; ++fp) {
     const int qq = wn * WNP + fp * 16 + 4 * (lane >> 4);
     const int oy = min(y0 + qq / TW, H - 1), ox = qq % TW;
 #pragma unroll
@@ -396,21 +398,52 @@ __global__ __launch_bounds__(320) void conv3x3_halo_kernel(const HaloArgs args) 
     bv[fc] = h2f_bits(bh[fc]);
     av[fc] = h2f_bits(ah[fc]);
   }
+  // conv + bias, then (+ chan_add), then (+ residual), each add narrowed as the unfused op
+  // sequence narrows it.  Every value is narrowed with f2h_nonnan first; a wave in which some
+  // lane met a NaN redoes all of them with f2h_generic (NaN payloads as mtorch keeps them).
+  uint2 out[FP][FC];
+  auto epilogue = [&](auto narrow) {
+#pragma unroll
+    for (int fp = 0; fp < FP; ++fp)
+#pragma unroll
+      for (int fc = 0; fc < FC; ++fc) {
+        uint32_t h[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          float x = acc[fp][fc][t] + bv[fc];
+          if constexpr (HAS_A) x = h2f_bits((uint16_t)narrow(x)) + av[fc];
+          if constexpr (HAS_R) x = h2f_bits((uint16_t)narrow(x)) + rz[fp][fc].at(t);
+          h[t] = narrow(x);
+        }
+        out[fp][fc] = make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
+      }
+  };
+  bool nan_seen = false;
+  epilogue([&](float x) {
+    nan_seen |= x != x;
+    return f2h_nonnan(x);
+  });
+  if (__builtin_amdgcn_ballot_w64(nan_seen)) epilogue([](float x) { return (uint32_t)f2h_generic(x); });
+  // lane l of fragment (fp, fc) holds channel oc[fc] at the four pixels wn*WNP + fp*16 + 4*(l/16)
+  // .. +3 of one output row (TW % 4 == 0): one 8-byte store when Y is 8-byte aligned
+  const bool y_al = ((uintptr_t)Y & 7) == 0;
 #pragma unroll
   for (int fp = 0; fp < FP; ++fp) {
     const int qq = wn * WNP + fp * 16 + 4 * (lane >> 4);
     const int oy = y0 + qq / TW, ox = qq % TW;
 #pragma unroll
     for (int fc = 0; fc < FC; ++fc) {
-      float v[4], r[4];
-      const float b[4] = {bv[fc], bv[fc], bv[fc], bv[fc]};
-#pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        v[t] = acc[fp][fc][t];
-        r[t] = rz[fp][fc].at(t);
+      if (oy < H && oc[fc] < O) {
+        T* dst = Y + ((int64_t)img * O + oc[fc]) * HW + oy * W + ox;
+        if (y_al) {
+          *reinterpret_cast<uint2*>(dst) = out[fp][fc];
+        } else {
+          dst[0] = (T)(out[fp][fc].x & 0xffffu);
+          dst[1] = (T)(out[fp][fc].x >> 16);
+          dst[2] = (T)(out[fp][fc].y & 0xffffu);
+          dst[3] = (T)(out[fp][fc].y >> 16);
+        }
       }
-      epi_math<T, EPI_CONV, MTHIP_ACT_NONE>(v, b, true, av[fc], cadd != nullptr, r, res != nullptr);
-      if (oy < H && oc[fc] < O) store_cols<T>(Y + ((int64_t)img * O + oc[fc]) * HW + oy * W + ox, v, 4);
     }
   }
 }

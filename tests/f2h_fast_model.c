@@ -2,9 +2,13 @@
  * float bit patterns: f2h_fast (short common path + generic fallback) must equal f2h_generic,
  * and f2h_generic must equal mtorch's rounding (round to nearest, ties away from zero, overflow
  * to inf, NaN keeping the top payload bits; tensor.cpp:276-315, restated in oracle/oracle.c).
+ * f2h_nonnan (integer and fma steps, no hardware conversion) must equal f2h_generic on every
+ * non-NaN pattern, with fp32 denormal inputs kept or flushed to zero.
  * The hardware conversion v_cvt_f16_f32 rounds to nearest-even; F16C's _cvtss_sh with
- * round-to-nearest is the same IEEE operation. */
+ * round-to-nearest is the same IEEE operation.  fmaf is the correctly rounded fused multiply-add
+ * that v_fma_f32 computes. */
 #include <immintrin.h>
+#include <math.h>
 #include <stdint.h>
 #include <stdio.h>
 #include <string.h>
@@ -35,6 +39,17 @@ static uint32_t f2h_fast(uint32_t bits) {
   return (rne(bits) + ((bits & 0x3fffu) == 0x1000u ? 1u : 0u)) & 0xffffu;
 }
 
+static uint32_t f2h_nonnan(uint32_t bits, int flush) {
+  float v;
+  memcpy(&v, &bits, 4);
+  const uint32_t t = ((bits - 0x37fff000u) >> 13) & 0x3ffffu;
+  const uint32_t hn = t < 0x7c00u ? t : 0x7c00u;
+  float av = fabsf(v);
+  if (flush && (bits & 0x7f800000u) == 0u) av = 0.0f;
+  const uint32_t hs = (uint32_t)fmaf(av, 16777216.0f, 0x1.fffffep-2f);
+  return (av < 0x1p-14f ? hs : hn) | ((bits >> 16) & 0x8000u);
+}
+
 /* mtorch's scalar rule, written independently of the hardware conversion */
 static uint32_t f2h_reference(uint32_t bits) {
   const uint32_t sign = (bits >> 16) & 0x8000u;
@@ -60,13 +75,16 @@ static uint32_t f2h_reference(uint32_t bits) {
 }
 
 int main(void) {
-  uint64_t bad_fast = 0, bad_ref = 0;
+  uint64_t bad_fast = 0, bad_ref = 0, bad_nonnan = 0;
   for (uint64_t i = 0; i <= 0xffffffffull; ++i) {
     const uint32_t b = (uint32_t)i;
     const uint32_t g = f2h_generic(b);
     if (f2h_fast(b) != g && bad_fast++ < 5) printf("fast %08x: %04x vs %04x\n", b, f2h_fast(b), g);
     if (f2h_reference(b) != g && bad_ref++ < 5) printf("ref %08x: %04x vs %04x\n", b, f2h_reference(b), g);
+    if ((b & 0x7fffffffu) <= 0x7f800000u && (f2h_nonnan(b, 0) != g || f2h_nonnan(b, 1) != g) && bad_nonnan++ < 5)
+      printf("nonnan %08x: %04x / %04x vs %04x\n", b, f2h_nonnan(b, 0), f2h_nonnan(b, 1), g);
   }
-  printf("fast!=generic %llu, reference!=generic %llu\n", (unsigned long long)bad_fast, (unsigned long long)bad_ref);
-  return (bad_fast || bad_ref) ? 1 : 0;
+  printf("fast!=generic %llu, reference!=generic %llu, nonnan!=generic %llu\n", (unsigned long long)bad_fast,
+         (unsigned long long)bad_ref, (unsigned long long)bad_nonnan);
+  return (bad_fast || bad_ref || bad_nonnan) ? 1 : 0;
 }
