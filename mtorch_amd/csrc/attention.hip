@@ -366,17 +366,24 @@ void flash_fwd_f16_kernel(const FlashArgs a) {
     // branch-free block, where the 16*DVB independent conversion chains interleave, and the
     // stores follow, each behind its bounds test: converting inside the guarded store loop split
     // the block at every group and left each ~21-instruction chain to run at full latency with
-    // one wave per SIMD (about 5 us of a 16x16-latent attention).
+    // one wave per SIMD (about 5 us of a 16x16-latent attention).  The narrowing is f2h_nonnan;
+    // a wave in which some lane met a NaN (a fully masked row) converts again with f2h_generic.
     uint2 h[DVBP][4];
+    auto convert = [&](auto narrow) {
 #pragma unroll
-    for (int i = 0; i < DVBP; ++i)
+      for (int i = 0; i < DVBP; ++i)
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        h[i][g].x = (uint32_t)f2h_generic(acc[i][4 * g] * inv_l) |
-                    ((uint32_t)f2h_generic(acc[i][4 * g + 1] * inv_l) << 16);
-        h[i][g].y = (uint32_t)f2h_generic(acc[i][4 * g + 2] * inv_l) |
-                    ((uint32_t)f2h_generic(acc[i][4 * g + 3] * inv_l) << 16);
-      }
+        for (int g = 0; g < 4; ++g) {
+          h[i][g].x = narrow(acc[i][4 * g] * inv_l) | (narrow(acc[i][4 * g + 1] * inv_l) << 16);
+          h[i][g].y = narrow(acc[i][4 * g + 2] * inv_l) | (narrow(acc[i][4 * g + 3] * inv_l) << 16);
+        }
+    };
+    bool nan_seen = false;
+    convert([&](float x) {
+      nan_seen |= x != x;
+      return f2h_nonnan(x);
+    });
+    if (__builtin_amdgcn_ballot_w64(nan_seen)) convert([](float x) { return (uint32_t)f2h_generic(x); });
 #pragma unroll
     for (int i = 0; i < DVBP; ++i)
 #pragma unroll

@@ -91,9 +91,18 @@ __device__ __forceinline__ uint16_t f2h_bits(float value) {
   return (uint16_t)(sign | (rounded >= 0x7c00u ? 0x7c00u : rounded));
 }
 
-// Bit-identical to f2h_bits for every input, and branch-free.  mtorch's rule is round-to-nearest with ties away from zero, overflowing to
-// inf; the hardware conversion (v_cvt_f16_f32, with fp16 subnormals) rounds to nearest-even
-// and overflows the same way.  The two differ only on exact ties whose kept LSB is 0, where
+// The hardware conversion (v_cvt_f16_f32, round to nearest-even) of exactly `value`.  The empty
+// asm hides where the value came from: given a product of two widened halves, the compiler
+// otherwise folds the multiply and this conversion into v_fma_mix(a, b, +0), whose +0 addend
+// turns a -0 product into +0.
+__device__ __forceinline__ uint32_t cvt_f16_rne(float value) {
+  asm("" : "+v"(value));
+  return __builtin_bit_cast(uint16_t, (_Float16)value);
+}
+
+// Bit-identical to f2h_bits for every input, and branch-free.  mtorch's rule is round-to-nearest
+// with ties away from zero, overflowing to inf; the hardware conversion (v_cvt_f16_f32, with
+// fp16 subnormals) rounds to nearest-even and overflows the same way.  The two differ only on exact ties whose kept LSB is 0, where
 // RNE keeps the smaller magnitude: with sh discarded significand bits (13 for normal halves,
 // up to 24 for the smallest subnormal, biased float exponent 102..142), such a tie has
 // significand & (2^(sh+1) - 1) == 2^(sh-1), and one ulp is added to the magnitude.  NaNs keep
@@ -101,7 +110,7 @@ __device__ __forceinline__ uint16_t f2h_bits(float value) {
 __device__ __forceinline__ uint16_t f2h_generic(float value) {
   const uint32_t bits = __float_as_uint(value);
   const uint32_t raw = (bits >> 23) & 0xffu;
-  uint32_t h = __builtin_bit_cast(uint16_t, (_Float16)value);
+  uint32_t h = cvt_f16_rne(value);
   const int d = 126 - (int)raw;
   const uint32_t sh = (uint32_t)(d < 13 ? 13 : (d > 24 ? 24 : d));
   const uint32_t sig = (bits & 0x7fffffu) | 0x800000u;
@@ -123,14 +132,13 @@ __device__ __forceinline__ uint16_t f2h_generic(float value) {
 // conversion).
 //
 // Epilogues that narrow dozens of values per lane at one or two waves per SIMD (GEMM, conv,
-// attention) call f2h_generic directly: about 21 VALU operations and no branch, so the
-// conversions interleave, where one scalar branch per value would serialise them and the
-// fallback, inlined at every call, would multiply the code each workgroup fetches cold.
+// attention) use f2h_nonnan below instead: no branch per value, so the conversions interleave,
+// where one scalar branch per value would serialise them.
 __device__ __forceinline__ uint16_t f2h_fast(float value) {
   const uint32_t bits = __float_as_uint(value);
   const uint32_t a = bits & 0x7fffffffu;
   const bool common = a == 0u || a - 0x38800000u < 0x0f000000u;
-  uint32_t h = __builtin_bit_cast(uint16_t, (_Float16)value);
+  uint32_t h = cvt_f16_rne(value);
   h += (bits & 0x3fffu) == 0x1000u ? 1u : 0u;
   if (__builtin_amdgcn_ballot_w64(!common)) {
     const uint32_t g = f2h_generic(value);

@@ -39,6 +39,8 @@
 
 #include <hip/hip_runtime.h>
 
+#include <type_traits>
+
 #include "activations.h"
 #include "common.h"
 
@@ -265,6 +267,41 @@ __device__ __forceinline__ void epi_math(float (&v)[4], const float (&b)[4], boo
   }
 }
 
+// fp16 narrowings of the straight-line epilogues.  NarrowFast is exact for every non-NaN value
+// (f2h_nonnan, ~10 VALU operations) and records whether a NaN went through it; a wave that met
+// one computes its values again with NarrowExact (f2h_generic: NaN payloads as mtorch keeps
+// them).
+struct NarrowFast {
+  bool nan = false;
+  __device__ __forceinline__ uint32_t operator()(float x) {
+    nan |= x != x;
+    return f2h_nonnan(x);
+  }
+};
+struct NarrowExact {
+  __device__ __forceinline__ uint32_t operator()(float x) const { return f2h_generic(x); }
+};
+
+// One fp16 output of EPI_LINEAR / EPI_CONV from its fp32 dot product x: + b (the bias, or -0.0,
+// which leaves every value as it is), then the activation (LINEAR) or the channel addend
+// (CONV, HA), then the residual (HR), each narrowed where the unfused op sequence stores it.
+template <int EPI, int ACT, bool HA, bool HR, typename N>
+__device__ __forceinline__ uint32_t epi_chain_h(float x, float b, float av, float r, const uint16_t* gtab, N& narrow) {
+  x += b;
+  if constexpr (EPI == EPI_LINEAR && ACT == MTHIP_ACT_GELU) {
+    const uint32_t g = gtab[narrow(x)];
+    if constexpr (!HR) return g;
+    x = h2f_bits((uint16_t)g) + r;
+  } else if constexpr (EPI == EPI_LINEAR && ACT != MTHIP_ACT_NONE) {
+    x = apply_act<uint16_t>(ACT, h2f_bits((uint16_t)narrow(x)));
+    if constexpr (HR) x = h2f_bits((uint16_t)narrow(x)) + r;
+  } else {
+    if constexpr (HA) x = h2f_bits((uint16_t)narrow(x)) + av;
+    if constexpr (HR) x = h2f_bits((uint16_t)narrow(x)) + r;
+  }
+  return narrow(x);
+}
+
 // Epilogue for C[row][col0 .. col0+3] of batch bz (row < M checked by the caller; columns
 // past N are skipped).  v holds the fp32 dot products.  Values are narrowed once, except where
 // a fused activation or residual needs the narrowed intermediate that the unfused op sequence
@@ -445,28 +482,61 @@ __device__ __forceinline__ void gemm_finish_unit(const GemmArgs& args, const Gem
 #pragma unroll
       for (int g = 0; g < 4; ++g)
 #pragma unroll
-        for (int t = 0; t < 4; ++t) bval[g][t] = bgate[g][t] = 0.0f;
+        for (int t = 0; t < 4; ++t) bval[g][t] = bgate[g][t] = -0.0f;  // adding -0.0 leaves every value as it is
+    }
+    if constexpr (sizeof(T) == 2) {
+      // out = value * gelu(gate): the gate narrowed and looked up, the value narrowed, their
+      // product narrowed; every gather of a row before the first use
+      uint2 out[FM][4];
+      auto chain = [&](auto& narrow) {
+#pragma unroll
+        for (int i = 0; i < FM; ++i) {
+          uint32_t gh[4][4];
+#pragma unroll
+          for (int g = 0; g < 4; ++g)
+#pragma unroll
+            for (int t = 0; t < 4; ++t) gh[g][t] = args.gelu_tab[narrow(acc[i][1][4 * g + t] + bgate[g][t])];
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            uint32_t h[4];
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+              h[t] = narrow(h2f_bits((uint16_t)narrow(acc[i][0][4 * g + t] + bval[g][t])) * h2f_bits((uint16_t)gh[g][t]));
+            out[i][g] = make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
+          }
+        }
+      };
+      NarrowFast fast;
+      chain(fast);
+      if (__builtin_amdgcn_ballot_w64(fast.nan)) {
+        NarrowExact exact;
+        chain(exact);
+      }
+#pragma unroll
+      for (int i = 0; i < FM; ++i) {
+        const int row = (int)un.m0 + wm * WM + i * 32 + (lane & 31);
+        if (row >= M) continue;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int col0 = (int)un.n0 / 2 + 8 * g + lane_col;
+          uint16_t* p = reinterpret_cast<uint16_t*>(Cp) + (int64_t)row * args.ldc + col0;
+          const uint32_t hv[4] = {out[i][g].x & 0xffffu, out[i][g].x >> 16, out[i][g].y & 0xffffu, out[i][g].y >> 16};
+          if (col0 + 4 <= Nout && ((uintptr_t)p & 7) == 0) {
+            *reinterpret_cast<uint2*>(p) = out[i][g];
+          } else {
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+              if (col0 + t < Nout) p[t] = (uint16_t)hv[t];
+          }
+        }
+      }
+      return;
     }
 #pragma unroll
     for (int i = 0; i < FM; ++i) {
       const int row = (int)un.m0 + wm * WM + i * 32 + (lane & 31);
       float gl[4][4];
-      if constexpr (sizeof(T) == 2) {
-        // the gates' fp16 values, then all 16 table reads, then the first use
-        uint32_t gh[4][4];
-#pragma unroll
-        for (int g = 0; g < 4; ++g)
-#pragma unroll
-          for (int t = 0; t < 4; ++t) {
-            float gate = acc[i][1][4 * g + t];
-            if (has_b) gate += bgate[g][t];
-            gh[g][t] = f2h_generic(gate);
-          }
-#pragma unroll
-        for (int g = 0; g < 4; ++g)
-#pragma unroll
-          for (int t = 0; t < 4; ++t) gl[g][t] = h2f_bits(args.gelu_tab[gh[g][t]]);
-      } else {
+      {
 #pragma unroll
         for (int g = 0; g < 4; ++g)
 #pragma unroll
@@ -486,11 +556,7 @@ __device__ __forceinline__ void gemm_finish_unit(const GemmArgs& args, const Gem
             for (int t = 0; t < 4; ++t) {
               float val = acc[i][0][4 * g + t];
               if (has_b) val += bval[g][t];
-              if constexpr (sizeof(T) == 2) {
-                v[t] = h2f_bits(f2h_generic(val)) * gl[g][t];
-              } else {
-                v[t] = val * gl[g][t];
-              }
+              v[t] = val * gl[g][t];
             }
             store_cols<T>(Cp + (int64_t)row * args.ldc + col0, v, Nout - col0 < 4 ? Nout - col0 : 4);
           }
@@ -516,6 +582,123 @@ __device__ __forceinline__ void gemm_finish_unit(const GemmArgs& args, const Gem
       }
     }
     return;
+  }
+  if constexpr ((EPI == EPI_LINEAR || EPI == EPI_CONV) && sizeof(T) == 2) {
+    if (epi_tile_fast<T, EPI, BN>(args, un)) {
+      // fp16, every column of the tile present: all values computed into registers (a lane holds
+      // 4 consecutive columns per (i, j, g)), then one 8-byte store each.
+      const uint16_t* bias = reinterpret_cast<const uint16_t*>(args.bias);
+      const uint16_t* res = reinterpret_cast<const uint16_t*>(args.residual);
+      const uint16_t* cadd = reinterpret_cast<const uint16_t*>(args.chan_add);
+      uint16_t* Cptr = reinterpret_cast<uint16_t*>(args.c);
+      const int col_base = (int)un.n0 + wn * WN + lane_col;  // + j*32 + 8*g
+      int rows[FM], rrows[FM];
+#pragma unroll
+      for (int i = 0; i < FM; ++i) {
+        rows[i] = (int)un.m0 + wm * WM + i * 32 + (lane & 31);
+        rrows[i] = rows[i] < M ? rows[i] : M - 1;
+      }
+      const int OHW = (int)(args.OH * args.OW);
+      const int img = EPI == EPI_CONV ? (int)args.div_ohw.div((uint32_t)un.n0) : 0;
+      const int pix_base = col_base - img * OHW;
+      // output element offset of (i, j, g)
+      auto out_off = [&](int i, int j, int g) -> int64_t {
+        if constexpr (EPI == EPI_CONV) return ((int64_t)img * M + rows[i]) * OHW + pix_base + j * 32 + 8 * g;
+        return (int64_t)rows[i] * args.ldc + col_base + j * 32 + 8 * g;
+      };
+      // bias: per column (LINEAR) or per row (CONV); fp16 -0 without one
+      Raw4<uint16_t> bz[EPI == EPI_LINEAR ? FN : 1][4];
+      float bv[FM], av[FM];
+      if constexpr (EPI == EPI_LINEAR) {
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+          for (int g = 0; g < 4; ++g)
+            bz[j][g].u = bias ? load_raw4<uint16_t>(bias + col_base + j * 32 + 8 * g).u : make_uint2(0x80008000u, 0x80008000u);
+      } else {
+#pragma unroll
+        for (int i = 0; i < FM; ++i) {
+          bv[i] = bias ? h2f_bits(bias[rrows[i]]) : -0.0f;
+          av[i] = cadd ? h2f_bits(cadd[img * args.chan_add_ld + rrows[i]]) : 0.0f;
+        }
+      }
+      auto run = [&](auto ha_c, auto hr_c) {
+        constexpr bool HA = decltype(ha_c)::value, HR = decltype(hr_c)::value;
+        Raw4<uint16_t> rz[FM][FN][4];
+        if constexpr (HR) {
+#pragma unroll
+          for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int j = 0; j < FN; ++j)
+#pragma unroll
+              for (int g = 0; g < 4; ++g) {
+                const int64_t o = EPI == EPI_CONV ? ((int64_t)img * M + rrows[i]) * OHW + pix_base + j * 32 + 8 * g
+                                                  : (int64_t)rrows[i] * args.ld_res + col_base + j * 32 + 8 * g;
+                rz[i][j][g] = load_raw4<uint16_t>(res + o);
+              }
+        }
+        uint2 out[FM][FN][4];
+        auto chain = [&](auto& narrow) {
+#pragma unroll
+          for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int j = 0; j < FN; ++j)
+#pragma unroll
+              for (int g = 0; g < 4; ++g) {
+                uint32_t h[4];
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                  float b, a = 0.0f, r = 0.0f;
+                  if constexpr (EPI == EPI_LINEAR) {
+                    b = bz[j][g].at(t);
+                  } else {
+                    b = bv[i];
+                    a = av[i];
+                  }
+                  if constexpr (HR) r = rz[i][j][g].at(t);
+                  h[t] = epi_chain_h<EPI, ACT, HA, HR>(acc[i][j][4 * g + t], b, a, r, args.gelu_tab, narrow);
+                }
+                out[i][j][g] = make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
+              }
+        };
+        NarrowFast fast;
+        chain(fast);
+        if (__builtin_amdgcn_ballot_w64(fast.nan)) {
+          NarrowExact exact;
+          chain(exact);
+        }
+        const bool al = ((uintptr_t)Cptr & 7) == 0 && (EPI == EPI_CONV || (args.ldc & 3) == 0);
+#pragma unroll
+        for (int i = 0; i < FM; ++i) {
+          if (rows[i] >= M) continue;
+#pragma unroll
+          for (int j = 0; j < FN; ++j)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+              uint16_t* p = Cptr + out_off(i, j, g);
+              if (al) {
+                *reinterpret_cast<uint2*>(p) = out[i][j][g];
+              } else {
+                p[0] = (uint16_t)(out[i][j][g].x & 0xffffu);
+                p[1] = (uint16_t)(out[i][j][g].x >> 16);
+                p[2] = (uint16_t)(out[i][j][g].y & 0xffffu);
+                p[3] = (uint16_t)(out[i][j][g].y >> 16);
+              }
+            }
+        }
+      };
+      const bool ha = EPI == EPI_CONV && cadd != nullptr, hr = res != nullptr;
+      if constexpr (EPI == EPI_CONV) {
+        if (ha && hr) run(std::true_type{}, std::true_type{});
+        else if (ha) run(std::true_type{}, std::false_type{});
+        else if (hr) run(std::false_type{}, std::true_type{});
+        else run(std::false_type{}, std::false_type{});
+      } else {
+        if (hr) run(std::false_type{}, std::true_type{});
+        else run(std::false_type{}, std::false_type{});
+      }
+      return;
+    }
   }
   if constexpr (EPI == EPI_LINEAR || EPI == EPI_CONV) {
     if (epi_tile_fast<T, EPI, BN>(args, un)) {

@@ -237,6 +237,38 @@ def test_geglu_matches_chunk_gelu_mul():
     assert rel(val(got), val(ref)) <= 1e-3
 
 
+def _finite_halves():
+    h = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    return h[(h & 0x7C00) != 0x7C00]
+
+
+def test_fp16_mul_keeps_the_sign_of_zero_products():
+    """fp16 products narrowed on the device keep mtorch's signed zeros (a -0 product stays 0x8000,
+    tiny products flush to a zero of their sign), bit for bit against the oracle for every finite
+    half times a set of multipliers, the zeros included."""
+    a = _finite_halves()
+    for bm in [0x3C00, 0xBC00, 0x0000, 0x8000, 0x0001, 0x8001, 0x7BFF, 0x3555]:
+        b = np.full(a.shape, bm, np.uint16)
+        got = host(dev(a) * dev(b))
+        ref = orc.binary(a, b, "mul")
+        bad = np.nonzero(got != ref)[0]
+        assert bad.size == 0, (hex(bm), [(hex(a[i]), hex(got[i]), hex(ref[i])) for i in bad[:6]])
+
+
+def test_geglu_bit_exact_over_every_gate():
+    """geglu(value, gate) = value * gelu(gate) in fp16 equals the oracle's chunk -> gelu -> mul
+    bit for bit for every finite gate half (large negative gates give -0 gelus, whose products
+    keep the sign), with positive and negative values."""
+    gate = _finite_halves()
+    for vm in [0x3C00, 0xBC00, 0x2CAA, 0x0000]:
+        value = np.full(gate.shape, vm, np.uint16)
+        x = np.concatenate([value, gate]).reshape(1, 2 * gate.size)
+        got = host(F.geglu(dev(x))).reshape(-1)
+        ref = orc.binary(value, orc.gelu(gate), "mul")
+        bad = np.nonzero(got != ref)[0]
+        assert bad.size == 0, (hex(vm), [(hex(gate[i]), hex(got[i]), hex(ref[i])) for i in bad[:6]])
+
+
 def test_scalar_ops_and_unary_math():
     g = Gen(14)
     x = g.randn((1000,), "float32")
