@@ -204,7 +204,7 @@ __global__ __launch_bounds__(320) void conv3x3_halo_kernel(const HaloArgs args) 
     // opens step s, then slot s
     auto slot = [&](int j, auto jp_c, auto t_c) {
       constexpr int JP = decltype(jp_c)::value, T = decltype(t_c)::value;
-      constexpr int STAGE = (3 * JP + T + SW - 1) % SW;  // ring stage of step s + SW - 1 (SW | 18)
+      constexpr int STAGE = (9 * JP + T + SW - 1) % SW;  // ring stage of step s + SW - 1 (SW | 18)
       constexpr int WC = (T + SW - 1) / 9, WT = (T + SW - 1) % 9;
       constexpr int PPS = Sched::PPS;
       __builtin_amdgcn_s_waitcnt(vmcnt_only(Sched::pending(T)));
@@ -332,7 +332,7 @@ __global__ __launch_bounds__(320) void conv3x3_halo_kernel(const HaloArgs args) 
     constexpr int set = (JP + T) & 1;
     constexpr int T1 = (T + 1) % 9;                // tap of step s + 1
     constexpr int BUF1 = T == 8 ? 1 - JP : JP;     // its patch buffer
-    constexpr int STAGE1 = (3 * JP + T + 1) % SW;  // its ring stage (SW | 18)
+    constexpr int STAGE1 = (9 * JP + T + 1) % SW;  // its ring stage (SW | 18)
     __builtin_amdgcn_s_waitcnt(0xc07f);            // lgkmcnt(0)
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
