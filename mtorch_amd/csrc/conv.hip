@@ -206,7 +206,18 @@ int try_conv_halo(int device, const void* xp, const void* wp, const void* b, voi
   switch (W) {
     case 64: return launch_halo<80, 2, 64>(device, h, s);
     case 32: return launch_halo<80, 2, 32>(device, h, s);
-    case 16: return launch_halo<80, 4, 16>(device, h, s);
+    case 16: {
+      // 48 channels x a whole 16x16 image per unit (four pixel fragments per wave: a weight
+      // tile feeds 4x the MFMAs of the 80 x 4x16 unit) when its units, split over K, still
+      // fill three quarters of the CUs -- the 1280-channel convs of SD's 16x16 latent
+      // (1280->1280: 39.6 -> 24.8 us with the split-K reduction); smaller convs keep 80 x 4x16.
+      const int64_t base = ceil_div(O, 48) * ceil_div(H, 16) * B;
+      const int64_t cus = halo_cu_count(device);
+      const int64_t ks = std::min<int64_t>(Cp / 64, std::max<int64_t>(1, cus / base));
+      const int64_t units = base * ceil_div(Cp / 64, ceil_div(Cp / 64, ks));
+      if (units * 4 >= cus * 3) return launch_halo<48, 16, 16>(device, h, s);
+      return launch_halo<80, 4, 16>(device, h, s);
+    }
     default: return launch_halo<80, 8, 8>(device, h, s);
   }
 }

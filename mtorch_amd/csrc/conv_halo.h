@@ -264,18 +264,24 @@ __global__ __launch_bounds__(320) void conv3x3_halo_kernel(const HaloArgs args) 
     bh[fc] = __builtin_amdgcn_raw_buffer_load_b16(b_rsrc, orr * 2, 0, 0);
     ah[fc] = HAS_A ? __builtin_amdgcn_raw_buffer_load_b16(c_rsrc, (img * args.chan_add_ld + orr) * 2, 0, 0) : 0;
   }
+  // The residual is read here, under the K loop, when its registers fit beside the wave's tile
+  // (FP * FC <= 10); a wider tile reads it at the epilogue instead of spilling.
+  constexpr bool R_EARLY = FP * FC <= 10;
   Raw4<T> rz[FP][FC];
+  auto load_residual = [&]() {
 #pragma unroll
-  for (int fp = 0; fp < FP && HAS_R; ++fp) {
-    const int qq = wn * WNP + fp * 16 + 4 * (lane >> 4);
-    const int oy = min(y0 + qq / TW, H - 1), ox = qq % TW;
+    for (int fp = 0; fp < FP; ++fp) {
+      const int qq = wn * WNP + fp * 16 + 4 * (lane >> 4);
+      const int oy = min(y0 + qq / TW, H - 1), ox = qq % TW;
 #pragma unroll
-    for (int fc = 0; fc < FC; ++fc) {
-      const int orr = oc[fc] < O ? oc[fc] : O - 1;
-      const auto u = __builtin_amdgcn_raw_buffer_load_b64(r_rsrc, (((img * O + orr) * HW) + oy * W + ox) * 2, 0, 0);
-      rz[fp][fc].u = make_uint2(u[0], u[1]);
+      for (int fc = 0; fc < FC; ++fc) {
+        const int orr = oc[fc] < O ? oc[fc] : O - 1;
+        const auto u = __builtin_amdgcn_raw_buffer_load_b64(r_rsrc, (((img * O + orr) * HW) + oy * W + ox) * 2, 0, 0);
+        rz[fp][fc].u = make_uint2(u[0], u[1]);
+      }
     }
-  }
+  };
+  if constexpr (HAS_R && R_EARLY) load_residual();
 
   // ---- LDS read addresses, fixed for the unit: pixel fragment fp at tap t in patch buffer 0
   //      (buffer 1 is + PBUF), weight fragment fc in stage 0 (stage k is + k * WSTAGE); the
@@ -392,6 +398,7 @@ __global__ __launch_bounds__(320) void conv3x3_halo_kernel(const HaloArgs args) 
     }
     return;
   }
+  if constexpr (HAS_R && !R_EARLY) load_residual();
   float bv[FC], av[FC];
 #pragma unroll
   for (int fc = 0; fc < FC; ++fc) {

@@ -676,6 +676,35 @@ def test_conv3x3_halo_kernel_shapes(B, C, H, W, O):
     assert rel(val(fused), ref) <= 1e-2
 
 
+@pytest.mark.parametrize("C,H", [(640, 16), (1280, 16), (1280, 13)])
+def test_conv3x3_halo_whole_image_tiles(C, H):
+    """Wide convs at width 16 (SD's 1280-channel 16x16 latent) run 48-channel units over a whole
+    16-row image with the channel blocks split over K and reduced: checked against the oracle on
+    a strided subset of output channels that includes the partial last 48-channel tile, with
+    bias and residual, and with the time-embedding addend through the fused GroupNorm path."""
+    B, W, O = 2, 16, 1280
+    g = Gen(C + H + 77)
+    x = g.randn((B, C, H, W), "float16")
+    w = g.randn((O, C, 3, 3), "float16", 1.0 / np.sqrt(9 * C))
+    b = g.randn((O,), "float16")
+    r = g.randn((B, O, H, W), "float16")
+    t = g.randn((B, O), "float16")
+    sel = np.r_[np.arange(0, O, 37), np.arange(O - 40, O)]
+    ws, bs = np.ascontiguousarray(w[sel]), np.ascontiguousarray(b[sel])
+    got = host(F.conv2d_residual(dev(x), dev(w), dev(b), dev(r), padding=1))[:, sel]
+    ref = orc.binary(orc.conv2d(x, ws, bs, padding=1), np.ascontiguousarray(r[:, sel]), "add")
+    assert rel(val(got), val(ref)) <= 1e-2
+    got = host(F.conv2d(dev(x), dev(w), None, padding=1))[:, sel]
+    assert rel(val(got), val(orc.conv2d(x, ws, None, padding=1))) <= 1e-2
+    gamma = g.randn((C,), "float16")
+    beta = g.randn((C,), "float16")
+    fused = host(F.group_norm_silu_conv2d(dev(x), 32, dev(gamma), dev(beta), 1e-5, dev(w), dev(b), padding=1,
+                                          chan_add=dev(t)))[:, sel]
+    h = orc.silu(orc.group_norm(x, 32, gamma, beta, 1e-5))
+    ref = val(orc.conv2d(h, ws, bs, padding=1)).astype(np.float64) + val(t)[:, sel, None, None]
+    assert rel(val(fused), ref) <= 1e-2
+
+
 @pytest.mark.parametrize("dt", ["float32", "float16"])
 @pytest.mark.parametrize("B,C,H,W,O,G", [(2, 64, 16, 16, 48, 32), (2, 40, 9, 7, 40, 8), (1, 16, 8, 8, 24, 4)])
 def test_group_norm_silu_conv2d_channel_add_is_the_separate_add(dt, B, C, H, W, O, G):
