@@ -224,6 +224,15 @@ def test_norm_upcast_pattern():
     got = host(_ops.layer_norm(dev(t), [320], dev(lw), dev(lb), 1e-5, allow_upcast=True))
     ref = orc.f2h(orc.layer_norm(orc.h2f(t), 320, lw, lb, 1e-5))
     assert rel(val(got), val(ref)) <= 2e-3
+    # the SpatialTransformer shapes (8192 tokens x 320, 2048 x 640, 512 x 1280): rows of five
+    # 16-byte chunks per lane over 8/16/32 lanes
+    for rows, n in [(8192, 320), (2048, 640), (2050, 1280)]:
+        t2 = g.randn((rows, n), "float16", 2.0)
+        w2 = g.randn((n,), "float32")
+        b2 = g.randn((n,), "float32")
+        got = host(_ops.layer_norm(dev(t2), [n], dev(w2), dev(b2), 1e-5, allow_upcast=True))
+        ref = orc.f2h(orc.layer_norm(orc.h2f(t2), n, w2, b2, 1e-5))
+        assert rel(val(got), val(ref)) <= 2e-3, (rows, n)
     with pytest.raises(RuntimeError, match="same dtype"):
         F.layer_norm(dev(t), [320], dev(lw), dev(lb))  # the public op keeps the same-dtype rule
 
@@ -817,7 +826,8 @@ def test_sd_group_norm_scenario_fixture():
 
 
 @pytest.mark.parametrize("dt", ["float32", "float16"])
-@pytest.mark.parametrize("rows,n", [(2048, 320), (2049, 320), (1000, 640), (77, 768), (50, 1280), (13, 3000), (9, 100)])
+@pytest.mark.parametrize("rows,n", [(2048, 320), (2049, 320), (1000, 640), (77, 768), (50, 1280), (13, 3000), (9, 100),
+                                    (4096, 640), (2050, 1280)])
 def test_layer_norm(dt, rows, n):
     g = Gen(81 + n)
     x = g.randn((rows, n), dt, 2.0)
