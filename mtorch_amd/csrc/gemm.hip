@@ -7,6 +7,7 @@
 
 #include "gemm_core.h"
 #include "gemm_dtl.h"
+#include "gemm_stream.h"
 
 namespace mthip {
 namespace {
@@ -335,6 +336,97 @@ using namespace mthip;
 
 extern "C" {
 
+namespace {
+
+// fp16 linears without an activation whose K is a multiple of 320 (units of whole 5-step ring
+// cycles) can take the streamed kernel (gemm_stream.h); MTHIP_GEMM_STREAM=0 turns it off.  The
+// K split comes from a makespan model: a persistent workgroup per CU runs ceil(units / CUs)
+// units of `steps` K steps each plus an epilogue, and a split adds the fp32 slices' write and
+// read and the reduction launch.  (128-token units need more than the 256 VGPRs a wave of a
+// five-wave workgroup can hold.)  Returns -1 when it does not apply.
+int try_stream_linear(int device, const GemmArgs& a, hipStream_t s) {
+  const int mode = env_flag("MTHIP_GEMM_STREAM", 1);
+  if (!mode) return -1;
+  const int64_t M = a.M, N = a.N, K = a.K;
+  // Where it wins (SD projections, graph-replayed): few tokens with long K -- 512x1280x1280
+  // 13.8 -> 10.3 us, 2048x640x2560 20.4 -> 16.4, 512x1280x5120 22.3 -> 20.2, 2048x640x640
+  // 9.3 -> 8.7; the wide or token-heavy ones stay on the DTL GEMM (8192x960x320 22.0 against
+  // 25.2, 512x3840x1280 13.6 against 18.2).  MTHIP_GEMM_STREAM=2 takes it wherever it applies.
+  if (mode == 1 && !(M <= 2048 && N <= 1280 && K >= 640)) return -1;
+  if (K == 0 || K % 320 != 0 || N % 16 != 0 || a.ldc % 4 != 0 || ((uintptr_t)a.c & 7) || ((uintptr_t)a.bias & 7))
+    return -1;
+  if (a.residual && (a.ld_res % 4 != 0 || ((uintptr_t)a.residual & 7))) return -1;
+  if (!aligned16(a.a) || !aligned16(a.b) || a.lda % 8 != 0 || a.ldb % 8 != 0) return -1;
+  if (M * a.ldc >= (int64_t(1) << 31) || (a.residual && M * a.ld_res >= (int64_t(1) << 31)) ||
+      M * a.lda >= (int64_t(1) << 30) || N * a.ldb >= (int64_t(1) << 30))
+    return -1;
+  const int64_t nk = K / 64, groups = nk / 5;
+  const int64_t cus = cu_count(device);
+  const double step_us = 0.17, epi_us = 0.4;
+  const int best_bt = 64;
+  int64_t best_ks = 1;
+  double best = 0.0;
+  for (int64_t ks = 1; ks <= std::min<int64_t>(8, groups); ++ks) {
+    if (groups % ks) continue;
+    const int64_t units = ceil_div(M, best_bt) * ceil_div(N, 80) * ks;
+    double t = (double)ceil_div(units, cus) * ((double)(nk / ks) * step_us + epi_us);
+    if (ks > 1) t += 3.0 + (double)((ks + 1) * M * N * 4) / 3.0e6;
+    if (best == 0.0 || t < best) {
+      best = t;
+      best_ks = ks;
+    }
+  }
+  StreamArgs sa{};
+  sa.a = a.a;
+  sa.b = a.b;
+  sa.c = a.c;
+  sa.bias = a.bias;
+  sa.residual = a.residual;
+  sa.M = (int)M;
+  sa.N = (int)N;
+  sa.lda = (int)a.lda;
+  sa.ldb = (int)a.ldb;
+  sa.ldc = (int)a.ldc;
+  sa.ld_res = (int)a.ld_res;
+  sa.tiles_m = (int)ceil_div(M, best_bt);
+  sa.tiles_n = (int)ceil_div(N, 80);
+  sa.ksplit = (int)best_ks;
+  sa.steps = (int)(nk / best_ks);
+  sa.units = sa.tiles_m * sa.tiles_n * sa.ksplit;
+  sa.a_bytes = (int)a.a_bytes;
+  sa.b_bytes = (int)a.b_bytes;
+  // consecutive units share the operand with fewer tiles (held in the XCD's L2)
+  sa.m_fast = sa.tiles_m <= sa.tiles_n ? 1 : 0;
+  void* ws = nullptr;
+  GemmArgs r = a;
+  if (best_ks > 1) {
+    r.ld_partial = ceil_div(N, 4) * 4;
+    r.ksplit = best_ks;
+    if (int rc = mthip_malloc(device, (size_t)(best_ks * M * r.ld_partial) * sizeof(float), &ws)) return rc;
+    r.partial = static_cast<float*>(ws);
+    sa.partial = r.partial;
+    sa.ld_partial = (int)r.ld_partial;
+  }
+  int64_t g = std::min<int64_t>(sa.units, cus);
+  if (g > 8) g = g / 8 * 8;
+  const bool hr = a.residual != nullptr && best_ks == 1;
+  if (hr)
+    hipLaunchKernelGGL((gemm_stream_kernel<64, true>), dim3((unsigned)g), dim3(320), 0, s, sa);
+  else
+    hipLaunchKernelGGL((gemm_stream_kernel<64, false>), dim3((unsigned)g), dim3(320), 0, s, sa);
+  int rc = check_launch("gemm_stream_kernel");
+  if (rc == MTHIP_OK && best_ks > 1) {
+    const int64_t work = M * ceil_div(N, 4);
+    const unsigned rg = (unsigned)std::min<int64_t>(ceil_div(work, 256), 8192);
+    hipLaunchKernelGGL((gemm_splitk_reduce_kernel<uint16_t, EPI_LINEAR, MTHIP_ACT_NONE>), dim3(rg), dim3(256), 0, s, r);
+    rc = check_launch("gemm_splitk_reduce_kernel(stream)");
+  }
+  if (ws) mthip_free(device, ws);  // stream-ordered: reused only by later work
+  return rc;
+}
+
+}  // namespace
+
 int mthip_linear(int device, int dtype, const void* x, int64_t lda, const void* w, int64_t ldw, const void* b,
                  void* y, int64_t ldy, int64_t M, int64_t N, int64_t K, int act, const void* residual,
                  int64_t ld_res) {
@@ -391,10 +483,12 @@ int mthip_linear(int device, int dtype, const void* x, int64_t lda, const void* 
   int rc;
   if (a.a_bytes > kMaxBufferBytes || a.b_bytes > kMaxBufferBytes)
     rc = fail(MTHIP_ERR_UNSUPPORTED, "mthip_linear: operands above 2 GiB are not supported");
-  else if (dtype == MTHIP_F16)
-    rc = launch_gemm<uint16_t, MODE_NT, EPI_LINEAR>(device, a, 1, s);
-  else
+  else if (dtype == MTHIP_F16) {
+    rc = act == MTHIP_ACT_NONE ? try_stream_linear(device, a, s) : -1;
+    if (rc < 0) rc = launch_gemm<uint16_t, MODE_NT, EPI_LINEAR>(device, a, 1, s);
+  } else {
     rc = launch_gemm<float, MODE_NT, EPI_LINEAR>(device, a, 1, s);
+  }
   mthip_free(device, xp);  // stream-ordered: reused only by later work
   mthip_free(device, wp);
   return rc;

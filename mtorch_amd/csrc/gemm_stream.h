@@ -1,0 +1,337 @@
+// Streamed fp16 linear layer (gfx950): C[m, n] = sum_k A[m, k] * B[n, k] + bias[n] (+ R[m, n]),
+// A the activations (tokens x K), B the weight (N x K), both k-contiguous, fp32 accumulate,
+// mtorch's fp16 narrowing of every stored value.
+//
+// A unit is 80 output channels x BT tokens over a run of K (one slice of the K split); a
+// persistent workgroup takes a contiguous run of units (XCD-contiguous numbering) and streams
+// their K steps (64 k each) back to back through one LDS ring.  Five wave64s: four compute waves
+// (each owns all 80 channels x BT/4 tokens: FC = 5 channel fragments x FP token fragments of
+// v_mfma_f32_16x16x32_f16) and a producer wave that issues every direct-to-LDS load.  The
+// producer runs SW - 1 steps ahead of the compute waves across unit boundaries, so the next
+// unit's first K steps arrive while the compute waves run the previous unit's epilogue -- the
+// DTL GEMM instead starts every unit's pipeline from its own loads, which at K = 320 (five
+// steps) is most of a unit.
+//
+// Step protocol (as in conv_halo.h): before the barrier that opens step s the producer waits
+// (a fixed vmcnt) until step s's operands have landed and the compute waves until their LDS
+// reads of step s are in registers; after it the producer refills the ring stage of step s - 1
+// with step s + SW - 1, and each compute wave reads step s + 1's fragments into its other
+// register set, interleaved one-to-one with step s's MFMAs.  Units hold a multiple of SW steps
+// (the launcher requires K / 64 to be a multiple of 5), so every unit starts at ring stage 0
+// and a group of SW steps has compile-time stages; the register set of step s is s & 1.
+//
+// LDS stage layout: the 80 weight rows, then the BT token rows, each row 64 halves (128 bytes)
+// with 16-byte chunk c at chunk c ^ ((row >> 1) & 7) (the ds_read_b128 passes of a fragment
+// cover all 64 banks).  Rows past M or N are fetched from an out-of-range offset and read as
+// zeros.
+#pragma once
+
+#include "gemm_core.h"
+#include "gemm_dtl.h"
+
+namespace mthip {
+
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+struct StreamArgs {
+  const void* a;  // [M][lda]
+  const void* b;  // [N][ldb]
+  void* c;        // [M][ldc]
+  const void* bias;      // [N] or null
+  const void* residual;  // [M][ld_res] or null
+  int M, N, lda, ldb, ldc, ld_res;
+  int tiles_m, tiles_n, ksplit;
+  int steps;   // K steps per unit (a multiple of 5)
+  int units;   // tiles_m * tiles_n * ksplit
+  int a_bytes, b_bytes;
+  float* partial;  // ksplit > 1: [ksplit][M][ld_partial] fp32
+  int ld_partial;
+  int m_fast;  // 1: consecutive units walk the token tiles of one channel tile
+};
+
+template <int BT, bool HAS_R>
+__global__ __launch_bounds__(320) void gemm_stream_kernel(const StreamArgs args) {
+  constexpr int BC = 80, NW = 4, SW = 5;
+  constexpr int WT = BT / NW;              // tokens per compute wave
+  constexpr int FC = BC / 16, FP = WT / 16;
+  constexpr int LW = BC / 8, LA = BT / 8;  // DMA instructions per step
+  constexpr int L = LW + LA;
+  constexpr uint32_t STAGE = (BC + BT) * 128;
+  constexpr int PEND = (SW - 2) * L > 63 ? 63 : (SW - 2) * L;
+  static_assert(BT % 64 == 0 && FP >= 1, "tokens per unit: a multiple of 64");
+  static_assert((size_t)SW * STAGE <= 160 * 1024, "LDS");
+  __shared__ __align__(16) uint8_t lds[SW * STAGE];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  constexpr uint32_t kOOB = 0x80000000u;
+
+  // ---- this workgroup's run of units: workgroups are dealt to the 8 XCDs round-robin, so
+  //      workgroup w takes chunk (w % 8) * (G / 8) + w / 8 of G equal runs (G a multiple of 8).
+  const uint32_t G = gridDim.x, w = blockIdx.x;
+  const uint32_t chunk = (G % 8 == 0) ? (w % 8) * (G / 8) + w / 8 : w;
+  const uint32_t U = (uint32_t)args.units;
+  const uint32_t u_begin = (uint32_t)(((uint64_t)U * chunk) / G), u_end = (uint32_t)(((uint64_t)U * (chunk + 1)) / G);
+  const int M = args.M, N = args.N, steps = args.steps;
+  struct Unit {
+    int m0, n0, split;
+  };
+  auto decode = [&](uint32_t u) {
+    Unit r;
+    const uint32_t tmn = (uint32_t)(args.tiles_m * args.tiles_n);
+    r.split = (int)(u / tmn);
+    const uint32_t t = u - (uint32_t)r.split * tmn;
+    uint32_t tm, tn;
+    if (args.m_fast) {
+      tm = t % (uint32_t)args.tiles_m;
+      tn = t / (uint32_t)args.tiles_m;
+    } else {
+      tn = t % (uint32_t)args.tiles_n;
+      tm = t / (uint32_t)args.tiles_n;
+    }
+    r.m0 = (int)tm * BT;
+    r.n0 = (int)tn * BC;
+    return r;
+  };
+
+  // =============================================================================== producer
+  if (wave == NW) {
+    const __amdgpu_buffer_rsrc_t a_rsrc =
+        __builtin_amdgcn_make_buffer_rsrc((void*)args.a, (short)0, args.a_bytes, 0x00020000);
+    const __amdgpu_buffer_rsrc_t b_rsrc =
+        __builtin_amdgcn_make_buffer_rsrc((void*)args.b, (short)0, args.b_bytes, 0x00020000);
+    const uint32_t base = lds_addr(lds);
+    uint32_t w_off[LW], a_off[LA];
+    uint32_t iu = u_begin;  // unit and step of the next load
+    int ij = 0, k0 = 0;
+    auto set_unit = [&]() {
+      const bool live = iu < u_end;
+      const Unit un = decode(live ? iu : u_begin);
+      k0 = un.split * steps;
+#pragma unroll
+      for (int gi = 0; gi < LW; ++gi) {
+        const int r = gi * 8 + (lane >> 3);
+        const int c = (lane & 7) ^ ((r >> 1) & 7);
+        const int n = un.n0 + r;
+        w_off[gi] = (live && n < N) ? ((uint32_t)n * (uint32_t)args.ldb + (uint32_t)c * 8u) * 2u : kOOB;
+      }
+#pragma unroll
+      for (int gi = 0; gi < LA; ++gi) {
+        const int r = BC + gi * 8 + (lane >> 3);
+        const int c = (lane & 7) ^ ((r >> 1) & 7);
+        const int m = un.m0 + gi * 8 + (lane >> 3);
+        a_off[gi] = (live && m < M) ? ((uint32_t)m * (uint32_t)args.lda + (uint32_t)c * 8u) * 2u : kOOB;
+      }
+    };
+    // one step's loads into ring stage `stage` (past the last unit: out-of-range, zeros)
+    auto issue = [&](uint32_t stage) {
+      const uint32_t dst = base + stage * STAGE;
+      const uint32_t soff = (uint32_t)(k0 + ij) * 128u;
+#pragma unroll
+      for (int gi = 0; gi < LW; ++gi) dma16(b_rsrc, dst + gi * 1024, w_off[gi], soff);
+#pragma unroll
+      for (int gi = 0; gi < LA; ++gi) dma16(a_rsrc, dst + (uint32_t)BC * 128u + gi * 1024, a_off[gi], soff);
+      if (++ij == steps) {
+        ij = 0;
+        ++iu;
+        set_unit();
+      }
+    };
+    set_unit();
+    issue(0);
+    issue(1);
+    issue(2);
+    issue(3);
+    const uint32_t total = (u_end - u_begin) * (uint32_t)steps;
+    uint32_t stage = SW - 1;
+    for (uint32_t s = 0; s < total; ++s) {
+      __builtin_amdgcn_s_waitcnt(vmcnt_only(PEND));
+      __builtin_amdgcn_s_barrier();
+      issue(stage);
+      stage = stage == SW - 1 ? 0 : stage + 1;
+    }
+    // the barrier the compute waves pass at the end of their last step
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_s_waitcnt(0);
+    return;
+  }
+
+  // =========================================================================== compute waves
+  using T = uint16_t;
+  const T* bias = reinterpret_cast<const T*>(args.bias);
+  const T* res = reinterpret_cast<const T*>(args.residual);
+  T* C = reinterpret_cast<T*>(args.c);
+  const __amdgpu_buffer_rsrc_t bias_rsrc =
+      __builtin_amdgcn_make_buffer_rsrc((void*)bias, (short)0, bias ? N * 2 : 0, 0x00020000);
+  const __amdgpu_buffer_rsrc_t res_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)res, (short)0, (HAS_R && args.ksplit == 1) ? ((M - 1) * args.ld_res + N) * 2 : 0, 0x00020000);
+
+  // LDS read addresses in stage 0 (stage k is + k * STAGE; the second 32 k is ^ 64)
+  uint32_t wa[FC], pa[FP];
+#pragma unroll
+  for (int fc = 0; fc < FC; ++fc) {
+    const int r = fc * 16 + (lane & 15);
+    wa[fc] = (uint32_t)(r * 128 + ((((lane >> 4) ^ (r >> 1)) & 7) << 4));
+  }
+#pragma unroll
+  for (int fp = 0; fp < FP; ++fp) {
+    const int r = BC + wave * WT + fp * 16 + (lane & 15);
+    pa[fp] = (uint32_t)(r * 128 + ((((lane >> 4) ^ (r >> 1)) & 7) << 4));
+  }
+
+  floatx4 acc[FC][FP];
+  halfx8 wf[2][2][FC], pf[2][2][FP];  // [set][kk][fragment]
+  auto zero_acc = [&]() {
+#pragma unroll
+    for (int fc = 0; fc < FC; ++fc)
+#pragma unroll
+      for (int fp = 0; fp < FP; ++fp) acc[fc][fp] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+  };
+  auto read_frags = [&](auto set_c, auto stage_c) {
+    constexpr int set = decltype(set_c)::value;
+    constexpr uint32_t off = decltype(stage_c)::value * STAGE;
+#pragma unroll
+    for (int fp = 0; fp < FP; ++fp) {
+      pf[set][0][fp] = *reinterpret_cast<const halfx8*>(lds + pa[fp] + off);
+      pf[set][1][fp] = *reinterpret_cast<const halfx8*>(lds + (pa[fp] ^ 64) + off);
+    }
+#pragma unroll
+    for (int fc = 0; fc < FC; ++fc) {
+      wf[set][0][fc] = *reinterpret_cast<const halfx8*>(lds + wa[fc] + off);
+      wf[set][1][fc] = *reinterpret_cast<const halfx8*>(lds + (wa[fc] ^ 64) + off);
+    }
+  };
+
+  // The current unit's epilogue operands, read when the unit starts (they arrive under its K
+  // steps).  Lane l of fragment (fc, fp) holds channels n0 + fc*16 + 4*(l/16) .. +3 of token
+  // m0 + wave*WT + fp*16 + l%16.
+  Unit cur{};
+  uint2 bz[FC], rz[FC][FP];
+  auto begin_unit = [&](uint32_t u) {
+    cur = decode(u);
+#pragma unroll
+    for (int fc = 0; fc < FC; ++fc) {
+      const int n = cur.n0 + fc * 16 + 4 * (lane >> 4);
+      const auto v = __builtin_amdgcn_raw_buffer_load_b64(bias_rsrc, (n < N ? n : 0) * 2, 0, 0);
+      bz[fc] = make_uint2(v[0], v[1]);
+    }
+    if constexpr (HAS_R) {
+#pragma unroll
+      for (int fc = 0; fc < FC; ++fc)
+#pragma unroll
+        for (int fp = 0; fp < FP; ++fp) {
+          const int n = cur.n0 + fc * 16 + 4 * (lane >> 4);
+          const int m = cur.m0 + wave * WT + fp * 16 + (lane & 15);
+          const int o = (m < M && n < N) ? m * args.ld_res + n : 0;
+          const auto v = __builtin_amdgcn_raw_buffer_load_b64(res_rsrc, o * 2, 0, 0);
+          rz[fc][fp] = make_uint2(v[0], v[1]);
+        }
+    }
+    zero_acc();
+  };
+  auto end_unit = [&]() {
+    if (args.ksplit > 1) {
+#pragma unroll
+      for (int fc = 0; fc < FC; ++fc)
+#pragma unroll
+        for (int fp = 0; fp < FP; ++fp) {
+          const int n = cur.n0 + fc * 16 + 4 * (lane >> 4);
+          const int m = cur.m0 + wave * WT + fp * 16 + (lane & 15);
+          if (m < M && n < N)
+            *reinterpret_cast<float4*>(args.partial + ((int64_t)cur.split * M + m) * args.ld_partial + n) =
+                make_float4(acc[fc][fp][0], acc[fc][fp][1], acc[fc][fp][2], acc[fc][fp][3]);
+        }
+      return;
+    }
+    // + bias, (narrowed, + residual), narrowed: every value with f2h_nonnan, again with
+    // f2h_generic in a wave that met a NaN
+    uint2 out[FC][FP];
+    auto chain = [&](auto& narrow) {
+#pragma unroll
+      for (int fc = 0; fc < FC; ++fc)
+#pragma unroll
+        for (int fp = 0; fp < FP; ++fp) {
+          uint32_t h[4];
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            const uint32_t bw = t < 2 ? bz[fc].x : bz[fc].y;
+            float x = acc[fc][fp][t] + (bias ? h2f_bits((uint16_t)((t & 1) ? bw >> 16 : bw & 0xffffu)) : -0.0f);
+            if constexpr (HAS_R) {
+              const uint32_t rw = t < 2 ? rz[fc][fp].x : rz[fc][fp].y;
+              x = h2f_bits((uint16_t)narrow(x)) + h2f_bits((uint16_t)((t & 1) ? rw >> 16 : rw & 0xffffu));
+            }
+            h[t] = narrow(x);
+          }
+          out[fc][fp] = make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
+        }
+    };
+    NarrowFast fast;
+    chain(fast);
+    if (__builtin_amdgcn_ballot_w64(fast.nan)) {
+      NarrowExact exact;
+      chain(exact);
+    }
+#pragma unroll
+    for (int fc = 0; fc < FC; ++fc)
+#pragma unroll
+      for (int fp = 0; fp < FP; ++fp) {
+        const int n = cur.n0 + fc * 16 + 4 * (lane >> 4);
+        const int m = cur.m0 + wave * WT + fp * 16 + (lane & 15);
+        if (m < M && n < N) *reinterpret_cast<uint2*>(C + (int64_t)m * args.ldc + n) = out[fc][fp];
+      }
+  };
+
+  // one step: this step's fragments are in registers (set SET), the barrier that opens the next
+  // step, the next step's LDS reads (stage STAGE1, set 1 - SET) interleaved with this step's
+  // MFMAs
+  auto step = [&](auto set_c, auto stage1_c) {
+    constexpr int SET = decltype(set_c)::value;
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    read_frags(ic<1 - SET>{}, stage1_c);
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+      for (int fc = 0; fc < FC; ++fc)
+#pragma unroll
+        for (int fp = 0; fp < FP; ++fp)
+          acc[fc][fp] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wf[SET][kk][fc], pf[SET][kk][fp], acc[fc][fp], 0, 0, 0);
+    constexpr int NMF = 2 * FP * FC, NDS = 2 * (FP + FC);
+    constexpr int A = NDS < NMF ? NDS : NMF;
+#pragma unroll
+    for (int i = 0; i < A; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+    if constexpr (NDS > A) __builtin_amdgcn_sched_group_barrier(0x100, NDS - A, 0);
+    if constexpr (NMF > A) __builtin_amdgcn_sched_group_barrier(0x008, NMF - A, 0);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  // a group of SW steps starting at ring stage 0, the first with register set G
+  auto group = [&](auto g_c) {
+    constexpr int G0 = decltype(g_c)::value;
+    step(ic<(G0 + 0) & 1>{}, ic<1>{});
+    step(ic<(G0 + 1) & 1>{}, ic<2>{});
+    step(ic<(G0 + 2) & 1>{}, ic<3>{});
+    step(ic<(G0 + 3) & 1>{}, ic<4>{});
+    step(ic<(G0 + 4) & 1>{}, ic<0>{});
+  };
+
+  __builtin_amdgcn_s_barrier();
+  read_frags(ic<0>{}, ic<0>{});
+  const int groups_per_unit = steps / SW;
+  uint32_t g = 0;
+  for (uint32_t u = u_begin; u < u_end; ++u) {
+    begin_unit(u);
+    for (int gi = 0; gi < groups_per_unit; ++gi, ++g) {
+      if (g & 1)
+        group(ic<1>{});
+      else
+        group(ic<0>{});
+    }
+    end_unit();
+  }
+}
+
+}  // namespace mthip

@@ -302,6 +302,32 @@ def test_linear(dt, M, N, K):
     assert rel(val(got), val(orc.linear(x, w, b))) <= TOL[dt]
 
 
+@pytest.mark.parametrize("M,N,K,res", [(8192, 960, 320, False), (8192, 320, 320, True), (2048, 640, 2560, True),
+                                        (512, 3840, 1280, False), (512, 1280, 1280, True), (77, 96, 640, True),
+                                        (1000, 48, 320, False)])
+def test_linear_streamed_kernel(M, N, K, res, monkeypatch):
+    """fp16 linears with K a multiple of 320 can take the streamed kernel (persistent workgroups
+    over 80-channel x 64-token units, producer wave, K split and reduction where the model picks
+    it); MTHIP_GEMM_STREAM=2 sends every such shape there.  Checked against the oracle on a
+    strided subset of rows that includes the last, with bias and with the residual, including
+    partial channel and token tiles."""
+    monkeypatch.setenv("MTHIP_GEMM_STREAM", "2")
+    g = Gen(M + N + K)
+    x = g.randn((M, K), "float16")
+    w = g.randn((N, K), "float16", 1.0 / np.sqrt(K))
+    b = g.randn((N,), "float16")
+    r = g.randn((M, N), "float16") if res else None
+    if res:
+        got = host(F.linear_residual(dev(x), dev(w), dev(b), dev(r)))
+    else:
+        got = host(F.linear(dev(x), dev(w), dev(b)))
+    rows = np.unique(np.r_[np.arange(0, M, max(1, M // 60)), M - 1])
+    ref = orc.linear(np.ascontiguousarray(x[rows]), w, b)
+    if res:
+        ref = orc.binary(ref, np.ascontiguousarray(r[rows]), "add")
+    assert rel(val(got[rows]), val(ref)) <= TOL["float16"]
+
+
 @pytest.mark.parametrize("dt", ["float32", "float16"])
 def test_linear_strided_vector_input(dt):
     """A 1-D input with a non-unit stride (x[::2]) is one row read after a dense copy."""
