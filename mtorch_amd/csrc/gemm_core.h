@@ -127,8 +127,9 @@ struct GemmArgs {
   int64_t chan_add_ld;
 };
 
-// v as the unfused op sequence reads it back after storing it in T.  Epilogues narrow with the
-// branch-free f2h_generic (many values per lane at low occupancy).
+// v as the unfused op sequence reads it back after storing it in T, for the general epilogue
+// paths (partial tiles, the split-K reduction, fp32); the straight-line fp16 tile epilogues use
+// epi_chain_h with f2h_nonnan instead.
 template <typename T>
 __device__ __forceinline__ float epi_round(float v) {
   if constexpr (sizeof(T) == 2) {
