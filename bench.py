@@ -169,8 +169,8 @@ def run_resnet(args):
                    "batch": 2, "channels": 320, "hw": [64, 64]},
         "roofline": {
             "kernel": "conv3x3 launch: conv3x3_halo_kernel<80 channels x 2 rows x 64, 6-stage weight ring, "
-                      "4 waves> (input halo staged once per 64-channel block and reused by the 9 taps; "
-                      "bias and residual fused in the epilogue)",
+                      "4 compute + 2 producer waves> (input halo staged once per 64-channel block and reused "
+                      "by the 9 taps; bias and residual fused in the epilogue)",
             "bound": "mfma",
             "achieved": round(conv_tflops, 3),
             "peak": PEAK["fp16_mfma_tflops"],

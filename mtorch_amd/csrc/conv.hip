@@ -137,15 +137,16 @@ int launch_halo(int device, HaloArgs h, hipStream_t s) {
     if (int rc = mthip_malloc(device, (size_t)((int64_t)h.ksplit * h.O * h.ld_partial) * sizeof(float), &ws)) return rc;
     h.partial = static_cast<float*>(ws);
   }
+  // two producer waves (2 % over one at 64x64 and 32x32, bit-identical)
   const bool ha = h.ksplit == 1 && h.chan_add != nullptr, hr = h.ksplit == 1 && h.residual != nullptr;
   if (ha && hr)
-    hipLaunchKernelGGL((conv3x3_halo_kernel<BM, TR, TW, 1, 6, true, true>), dim3((unsigned)units), dim3(320), 0, s, h);
+    hipLaunchKernelGGL((conv3x3_halo_kernel<BM, TR, TW, 1, 6, true, true, 2>), dim3((unsigned)units), dim3(384), 0, s, h);
   else if (ha)
-    hipLaunchKernelGGL((conv3x3_halo_kernel<BM, TR, TW, 1, 6, true, false>), dim3((unsigned)units), dim3(320), 0, s, h);
+    hipLaunchKernelGGL((conv3x3_halo_kernel<BM, TR, TW, 1, 6, true, false, 2>), dim3((unsigned)units), dim3(384), 0, s, h);
   else if (hr)
-    hipLaunchKernelGGL((conv3x3_halo_kernel<BM, TR, TW, 1, 6, false, true>), dim3((unsigned)units), dim3(320), 0, s, h);
+    hipLaunchKernelGGL((conv3x3_halo_kernel<BM, TR, TW, 1, 6, false, true, 2>), dim3((unsigned)units), dim3(384), 0, s, h);
   else
-    hipLaunchKernelGGL((conv3x3_halo_kernel<BM, TR, TW, 1, 6, false, false>), dim3((unsigned)units), dim3(320), 0, s, h);
+    hipLaunchKernelGGL((conv3x3_halo_kernel<BM, TR, TW, 1, 6, false, false, 2>), dim3((unsigned)units), dim3(384), 0, s, h);
   int rc = check_launch("conv3x3_halo_kernel");
   if (rc == MTHIP_OK && h.ksplit > 1) {
     GemmArgs a{};

@@ -12,7 +12,7 @@
 // 9 / (1 + 2/TR): at TR = 2 a unit moves 126 KB per 64 channels for 11.8 MFLOP (94 FLOP/B)
 // where a 64x64 im2col tile moves 16 KB per 0.5 MFLOP (32 FLOP/B).
 //
-// Five wave64s: four compute waves, one per SIMD, and a producer wave that issues every load.
+// Four compute waves, one per SIMD, and one or two producer waves that issue every load.
 // Operands go global -> LDS with direct-to-LDS buffer loads (no staging registers, no
 // ds_write): an instruction moves 64 x 16 B, i.e. eight 128-byte rows (one row = one pixel's or
 // one output channel's 64 channels), with row r's 16-byte chunk c stored at chunk c ^ ((r >> 1)
@@ -60,17 +60,30 @@ struct HaloArgs {
   int ld_partial;
 };
 
-// Load bookkeeping of the producer, fixed at compile time.  LW weight instructions per slot; the
-// next block's LP patch instructions spread over the slots of taps 0..6 (PPS per slot), each
-// slot issuing its patch part ahead of its weights.
-template <int LW, int LP, int SW>
+// Load bookkeeping of producer wave P of NPW, fixed at compile time.  LW weight instructions per
+// slot; the next block's LP patch instructions spread over the slots of taps 0..6 (PPS per
+// slot), each slot issuing its patch part ahead of its weights.  Producer P issues the
+// instructions gi with gi % NPW == P of every slot, and waits only for its own.
+template <int LW, int LP, int SW, int NPW, int P>
 struct HaloSchedule {
   static constexpr int PPS = (LP + 6) / 7;
   static constexpr int patch_in(int tap) {
     return tap > 6 ? 0 : (LP - tap * PPS < 0 ? 0 : (LP - tap * PPS < PPS ? LP - tap * PPS : PPS));
   }
-  static constexpr int slot_loads(int tap) { return LW + patch_in(tap); }
-  static constexpr int last_patch_tap() { return (LP + PPS - 1) / PPS - 1; }
+  static constexpr int mine(int g0, int g1) {  // instructions gi in [g0, g1) with gi % NPW == P
+    int n = 0;
+    for (int gi = g0; gi < g1; ++gi) n += gi % NPW == P ? 1 : 0;
+    return n;
+  }
+  static constexpr int w_loads() { return mine(0, LW); }
+  static constexpr int p_loads(int tap) { return mine(tap * PPS, tap * PPS + patch_in(tap)); }
+  static constexpr int slot_loads(int tap) { return w_loads() + p_loads(tap); }
+  static constexpr int last_patch_tap() {
+    int t = 0;
+    for (int tap = 0; tap <= 6; ++tap)
+      if (p_loads(tap) > 0) t = tap;
+    return t;
+  }
   // Loads allowed in flight at the wait that precedes step s (tap T): the weights of step s were
   // the last load of the slot of step s - SW + 1, so every load of slots s - SW + 2 .. s - 1 may
   // still be in flight; at tap 0 the block's patch must have landed too, whose last part was
@@ -80,7 +93,7 @@ struct HaloSchedule {
     int n = 0;
     for (int d = 1; d <= SW - 2; ++d) n += slot_loads((T - d + 18) % 9);
     if (T == 0) {
-      int m = LW;
+      int m = w_loads();
       for (int t = last_patch_tap() + 1; t <= 8; ++t) m += slot_loads(t);
       n = n < m ? n : m;
     }
@@ -95,9 +108,12 @@ struct HaloSchedule {
 
 // HAS_A / HAS_R: the epilogue adds chan_add / residual (fixed at compile time so that the
 // epilogue is one straight-line block; a K-split launch writes fp32 partials and uses neither).
-template <int BM, int TR, int TW, int WGM, int SW, bool HAS_A, bool HAS_R>
-__global__ __launch_bounds__(320) void conv3x3_halo_kernel(const HaloArgs args) {
-  constexpr int NW = 4;                 // compute waves (the fifth wave is the producer)
+// NPW producer waves (waves NW .. NW + NPW - 1) share the loads: one wave keeps at most 63
+// loads in flight (the vmcnt range), which at the L2's latency under this load caps one
+// producer's direct-to-LDS stream at ~25 B/clk.
+template <int BM, int TR, int TW, int WGM, int SW, bool HAS_A, bool HAS_R, int NPW>
+__global__ __launch_bounds__(64 * (4 + NPW)) void conv3x3_halo_kernel(const HaloArgs args) {
+  constexpr int NW = 4;                 // compute waves (the others are producers)
   constexpr int WGN = NW / WGM;
   constexpr int NPX = TR * TW;          // output pixels per unit
   constexpr int PW = TW + 2, PH = TR + 2;
@@ -107,10 +123,11 @@ __global__ __launch_bounds__(320) void conv3x3_halo_kernel(const HaloArgs args) 
   constexpr int LW = BM / 8;            // weight DMA instructions per step
   constexpr int LP = (NP + 7) / 8;      // patch DMA instructions per channel block
   constexpr uint32_t WSTAGE = BM * 128, PBUF = LP * 8 * 128;
-  using Sched = HaloSchedule<LW, LP, SW>;
+  using Sched0 = HaloSchedule<LW, LP, SW, NPW, 0>;
   static_assert(WGM * WGN == NW && WMO % 16 == 0 && WNP % 16 == 0 && TW % 4 == 0 && BM % 8 == 0, "tile shape");
   static_assert(SW >= 3 && SW <= 9 && 18 % SW == 0, "weight ring depth: 3, 6 or 9");
-  static_assert(Sched::fits(), "vmcnt range");
+  static_assert(Sched0::fits() && HaloSchedule<LW, LP, SW, NPW, NPW - 1>::fits(), "vmcnt range");
+  static_assert(NPW >= 1 && NPW <= 2, "one or two producer waves");
   static_assert((size_t)(2 * PBUF + SW * WSTAGE) <= 160 * 1024, "LDS");
   static_assert(PBUF < 65536 && (SW - 1) * WSTAGE < 65536, "LDS read offsets are 16-bit immediates");
 
@@ -138,7 +155,9 @@ __global__ __launch_bounds__(320) void conv3x3_halo_kernel(const HaloArgs args) 
   const int HW = H * W;
 
   // =============================================================================== producer
-  if (wave == NW) {
+  auto producer = [&](auto p_c) {
+    constexpr int P = decltype(p_c)::value;
+    using Sched = HaloSchedule<LW, LP, SW, NPW, P>;
     const __amdgpu_buffer_rsrc_t x_rsrc =
         __builtin_amdgcn_make_buffer_rsrc((void*)args.x, (short)0, args.x_bytes, 0x00020000);
     const __amdgpu_buffer_rsrc_t w_rsrc =
@@ -171,7 +190,7 @@ __global__ __launch_bounds__(320) void conv3x3_halo_kernel(const HaloArgs args) 
       const uint32_t dst = base + 2 * PBUF + (uint32_t)stage * WSTAGE;
       const uint32_t soff = (uint32_t)((cb0 + min(j2, ncb - 1)) * 128 + t2 * Cp2);
 #pragma unroll
-      for (int gi = 0; gi < LW; ++gi) dma16(w_rsrc, dst + gi * 1024, w_off[gi], soff);
+      for (int gi = P; gi < LW; gi += NPW) dma16(w_rsrc, dst + gi * 1024, w_off[gi], soff);
     };
     // patch instructions [G0, G1) of block j2 into buffer `buf` (past the slice: the last block
     // again, into the buffer the last block does not use)
@@ -180,7 +199,8 @@ __global__ __launch_bounds__(320) void conv3x3_halo_kernel(const HaloArgs args) 
       const uint32_t dst = base + (uint32_t)buf * PBUF;
       const uint32_t soff = (uint32_t)(cb0 + min(j2, ncb - 1)) * 128u;
 #pragma unroll
-      for (int gi = G0; gi < G1; ++gi) dma16(x_rsrc, dst + gi * 1024, p_off[gi], soff);
+      for (int gi = G0; gi < G1; ++gi)
+        if (gi % NPW == P) dma16(x_rsrc, dst + gi * 1024, p_off[gi], soff);
     };
     // prologue: the nine slots of a block before the first, back to back -- block 0's patch in
     // the parts taps 0..6 issue, and the weights of steps 0 .. SW-2 in the slots of steps
@@ -235,6 +255,12 @@ __global__ __launch_bounds__(320) void conv3x3_halo_kernel(const HaloArgs args) 
     __builtin_amdgcn_s_barrier();
     // DMA writes still in flight target this workgroup's LDS: let them land before leaving.
     __builtin_amdgcn_s_waitcnt(0);
+  };
+  if (wave >= NW) {
+    if (NPW == 1 || wave == NW)
+      producer(ic<0>{});
+    else
+      producer(ic<NPW - 1>{});
     return;
   }
 

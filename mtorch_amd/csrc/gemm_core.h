@@ -1099,23 +1099,36 @@ __global__ __launch_bounds__(256) void gemm_kernel(const GemmArgs args) {
 }
 
 // Sums the K slices of a split GEMM in slice order and applies the epilogue; one thread per
-// 4 consecutive outputs of a row.
+// 4 consecutive outputs of a row.  The slices are read eight at a time, all loads of a group in
+// flight together (one memory round trip per group instead of one per slice).
 template <typename T, int EPI, int ACT>
 __global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(const GemmArgs args) {
   const int64_t n4 = ceil_div(args.N, 4);
   const int64_t total = args.M * n4;
   const int64_t slice = args.M * args.ld_partial;
+  const int ks = (int)args.ksplit;
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
     const int row = (int)(i / n4);
     const int col0 = (int)(i - (int64_t)row * n4) * 4;
     const float* p = args.partial + (int64_t)row * args.ld_partial + col0;
-    float4 s = *reinterpret_cast<const float4*>(p);
-    for (int64_t k = 1; k < args.ksplit; ++k) {
-      const float4 t = *reinterpret_cast<const float4*>(p + k * slice);
-      s.x += t.x;
-      s.y += t.y;
-      s.z += t.z;
-      s.w += t.w;
+    float4 s = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    for (int k0 = 0; k0 < ks; k0 += 8) {
+      float4 t[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k)
+        if (k0 + k < ks) t[k] = *reinterpret_cast<const float4*>(p + (int64_t)(k0 + k) * slice);
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        if (k0 + k >= ks) break;
+        if (k0 + k == 0) {
+          s = t[0];
+        } else {
+          s.x += t[k].x;
+          s.y += t[k].y;
+          s.z += t[k].z;
+          s.w += t[k].w;
+        }
+      }
     }
     float v[4] = {s.x, s.y, s.z, s.w};
     emit4<T, EPI, ACT>(args, 0, row, col0, v);
