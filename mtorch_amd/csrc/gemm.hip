@@ -342,17 +342,18 @@ namespace {
 // cycles) can take the streamed kernel (gemm_stream.h); MTHIP_GEMM_STREAM=0 turns it off.  The
 // K split comes from a makespan model: a persistent workgroup per CU runs ceil(units / CUs)
 // units of `steps` K steps each plus an epilogue, and a split adds the fp32 slices' write and
-// read and the reduction launch.  (128-token units need more than the 256 VGPRs a wave of a
-// five-wave workgroup can hold.)  Returns -1 when it does not apply.
+// read and the reduction launch; MTHIP_GEMM_STREAM_BT=64/128 forces the token tile.  Returns -1
+// when it does not apply.
 int try_stream_linear(int device, const GemmArgs& a, hipStream_t s) {
   const int mode = env_flag("MTHIP_GEMM_STREAM", 1);
   if (!mode) return -1;
   const int64_t M = a.M, N = a.N, K = a.K;
-  // Where it wins (SD projections, graph-replayed): few tokens with long K -- 512x1280x1280
-  // 13.8 -> 10.3 us, 2048x640x2560 20.4 -> 16.4, 512x1280x5120 22.3 -> 20.2, 2048x640x640
-  // 9.3 -> 8.7; the wide or token-heavy ones stay on the DTL GEMM (8192x960x320 22.0 against
-  // 25.2, 512x3840x1280 13.6 against 18.2).  MTHIP_GEMM_STREAM=2 takes it wherever it applies.
-  if (mode == 1 && !(M <= 2048 && N <= 1280 && K >= 640)) return -1;
+  // Where it wins (SD projections, graph-replayed): up to 1280 output channels with K >= 640 --
+  // 512x1280x1280 13.5 -> 9.7 us, 2048x640x2560 19.7 -> 15.4, 512x1280x5120 22.3 -> 20.0,
+  // 8192x320x1280 19.1 -> 17.7, 2048x640x640 8.9 -> 8.2; the wide or short-K ones stay on the
+  // DTL GEMM (8192x960x320 21.4 against 23.8, 512x3840x1280 13.3 against 17.1).
+  // MTHIP_GEMM_STREAM=2 takes it wherever it applies.
+  if (mode == 1 && !(N <= 1280 && K >= 640)) return -1;
   if (K == 0 || K % 320 != 0 || N % 16 != 0 || a.ldc % 4 != 0 || ((uintptr_t)a.c & 7) || ((uintptr_t)a.bias & 7))
     return -1;
   if (a.residual && (a.ld_res % 4 != 0 || ((uintptr_t)a.residual & 7))) return -1;
@@ -362,18 +363,27 @@ int try_stream_linear(int device, const GemmArgs& a, hipStream_t s) {
     return -1;
   const int64_t nk = K / 64, groups = nk / 5;
   const int64_t cus = cu_count(device);
-  const double step_us = 0.17, epi_us = 0.4;
-  const int best_bt = 64;
+  // per-step and per-unit costs (µs) of 64- and 128-token units, from graph-replayed sweeps;
+  // 128-token units lost on every SD shape (8192x960x320: 37.1 against 23.8 us), so they run
+  // only when forced
+  const double step_us[2] = {0.40, 0.55}, epi_us = 0.4;
+  const int force_bt = env_flag("MTHIP_GEMM_STREAM_BT", 64);
+  int best_bt = 64;
   int64_t best_ks = 1;
   double best = 0.0;
-  for (int64_t ks = 1; ks <= std::min<int64_t>(8, groups); ++ks) {
-    if (groups % ks) continue;
-    const int64_t units = ceil_div(M, best_bt) * ceil_div(N, 80) * ks;
-    double t = (double)ceil_div(units, cus) * ((double)(nk / ks) * step_us + epi_us);
-    if (ks > 1) t += 3.0 + (double)((ks + 1) * M * N * 4) / 3.0e6;
-    if (best == 0.0 || t < best) {
-      best = t;
-      best_ks = ks;
+  for (int bi = 0; bi < 2; ++bi) {
+    const int bt = bi ? 128 : 64;
+    if (force_bt && force_bt != bt) continue;
+    for (int64_t ks = 1; ks <= std::min<int64_t>(8, groups); ++ks) {
+      if (groups % ks) continue;
+      const int64_t units = ceil_div(M, bt) * ceil_div(N, 80) * ks;
+      double t = (double)ceil_div(units, cus) * ((double)(nk / ks) * step_us[bi] + epi_us);
+      if (ks > 1) t += 3.0 + (double)((ks + 1) * M * N * 4) / 3.0e6;
+      if (best == 0.0 || t < best) {
+        best = t;
+        best_bt = bt;
+        best_ks = ks;
+      }
     }
   }
   StreamArgs sa{};
@@ -410,10 +420,17 @@ int try_stream_linear(int device, const GemmArgs& a, hipStream_t s) {
   int64_t g = std::min<int64_t>(sa.units, cus);
   if (g > 8) g = g / 8 * 8;
   const bool hr = a.residual != nullptr && best_ks == 1;
-  if (hr)
-    hipLaunchKernelGGL((gemm_stream_kernel<64, true>), dim3((unsigned)g), dim3(320), 0, s, sa);
-  else
-    hipLaunchKernelGGL((gemm_stream_kernel<64, false>), dim3((unsigned)g), dim3(320), 0, s, sa);
+  if (best_bt == 128) {
+    if (hr)
+      hipLaunchKernelGGL((gemm_stream_kernel<128, true>), dim3((unsigned)g), dim3(320), 0, s, sa);
+    else
+      hipLaunchKernelGGL((gemm_stream_kernel<128, false>), dim3((unsigned)g), dim3(320), 0, s, sa);
+  } else {
+    if (hr)
+      hipLaunchKernelGGL((gemm_stream_kernel<64, true>), dim3((unsigned)g), dim3(320), 0, s, sa);
+    else
+      hipLaunchKernelGGL((gemm_stream_kernel<64, false>), dim3((unsigned)g), dim3(320), 0, s, sa);
+  }
   int rc = check_launch("gemm_stream_kernel");
   if (rc == MTHIP_OK && best_ks > 1) {
     const int64_t work = M * ceil_div(N, 4);

@@ -205,8 +205,23 @@ __global__ __launch_bounds__(320) void gemm_stream_kernel(const StreamArgs args)
   // The current unit's epilogue operands, read when the unit starts (they arrive under its K
   // steps).  Lane l of fragment (fc, fp) holds channels n0 + fc*16 + 4*(l/16) .. +3 of token
   // m0 + wave*WT + fp*16 + l%16.
+  // (A 128-token unit reads its residual at the epilogue: its registers would not fit beside
+  // the tile under the K steps.)
+  constexpr bool R_EARLY = FC * FP <= 5;
   Unit cur{};
   uint2 bz[FC], rz[FC][FP];
+  auto load_residual = [&]() {
+#pragma unroll
+    for (int fc = 0; fc < FC; ++fc)
+#pragma unroll
+      for (int fp = 0; fp < FP; ++fp) {
+        const int n = cur.n0 + fc * 16 + 4 * (lane >> 4);
+        const int m = cur.m0 + wave * WT + fp * 16 + (lane & 15);
+        const int o = (m < M && n < N) ? m * args.ld_res + n : 0;
+        const auto v = __builtin_amdgcn_raw_buffer_load_b64(res_rsrc, o * 2, 0, 0);
+        rz[fc][fp] = make_uint2(v[0], v[1]);
+      }
+  };
   auto begin_unit = [&](uint32_t u) {
     cur = decode(u);
 #pragma unroll
@@ -215,18 +230,7 @@ __global__ __launch_bounds__(320) void gemm_stream_kernel(const StreamArgs args)
       const auto v = __builtin_amdgcn_raw_buffer_load_b64(bias_rsrc, (n < N ? n : 0) * 2, 0, 0);
       bz[fc] = make_uint2(v[0], v[1]);
     }
-    if constexpr (HAS_R) {
-#pragma unroll
-      for (int fc = 0; fc < FC; ++fc)
-#pragma unroll
-        for (int fp = 0; fp < FP; ++fp) {
-          const int n = cur.n0 + fc * 16 + 4 * (lane >> 4);
-          const int m = cur.m0 + wave * WT + fp * 16 + (lane & 15);
-          const int o = (m < M && n < N) ? m * args.ld_res + n : 0;
-          const auto v = __builtin_amdgcn_raw_buffer_load_b64(res_rsrc, o * 2, 0, 0);
-          rz[fc][fp] = make_uint2(v[0], v[1]);
-        }
-    }
+    if constexpr (HAS_R && R_EARLY) load_residual();
     zero_acc();
   };
   auto end_unit = [&]() {
@@ -243,6 +247,7 @@ __global__ __launch_bounds__(320) void gemm_stream_kernel(const StreamArgs args)
         }
       return;
     }
+    if constexpr (HAS_R && !R_EARLY) load_residual();
     // + bias, (narrowed, + residual), narrowed: every value with f2h_nonnan, again with
     // f2h_generic in a wave that met a NaN
     uint2 out[FC][FP];
@@ -318,19 +323,29 @@ __global__ __launch_bounds__(320) void gemm_stream_kernel(const StreamArgs args)
     step(ic<(G0 + 4) & 1>{}, ic<0>{});
   };
 
+  // The steps run in blocks of two groups (ten steps, register sets fixed at compile time);
+  // units end on group boundaries, so the epilogue may follow either group.
   __builtin_amdgcn_s_barrier();
   read_frags(ic<0>{}, ic<0>{});
-  const int groups_per_unit = steps / SW;
-  uint32_t g = 0;
-  for (uint32_t u = u_begin; u < u_end; ++u) {
-    begin_unit(u);
-    for (int gi = 0; gi < groups_per_unit; ++gi, ++g) {
-      if (g & 1)
-        group(ic<1>{});
-      else
-        group(ic<0>{});
+  uint32_t u = u_begin;
+  int left = (int)(u_end - u_begin) * steps;  // steps still to run
+  int in_unit = 0;
+  if (u < u_end) begin_unit(u);
+  auto after_group = [&]() {
+    left -= SW;
+    in_unit += SW;
+    if (in_unit == steps) {
+      end_unit();
+      in_unit = 0;
+      if (++u < u_end) begin_unit(u);
     }
-    end_unit();
+  };
+  while (left > 0) {
+    group(ic<0>{});
+    after_group();
+    if (left == 0) break;
+    group(ic<1>{});
+    after_group();
   }
 }
 

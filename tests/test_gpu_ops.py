@@ -305,13 +305,15 @@ def test_linear(dt, M, N, K):
 @pytest.mark.parametrize("M,N,K,res", [(8192, 960, 320, False), (8192, 320, 320, True), (2048, 640, 2560, True),
                                         (512, 3840, 1280, False), (512, 1280, 1280, True), (77, 96, 640, True),
                                         (1000, 48, 320, False)])
-def test_linear_streamed_kernel(M, N, K, res, monkeypatch):
+@pytest.mark.parametrize("bt", ["64", "128"])
+def test_linear_streamed_kernel(M, N, K, res, bt, monkeypatch):
     """fp16 linears with K a multiple of 320 can take the streamed kernel (persistent workgroups
     over 80-channel x 64-token units, producer wave, K split and reduction where the model picks
     it); MTHIP_GEMM_STREAM=2 sends every such shape there.  Checked against the oracle on a
     strided subset of rows that includes the last, with bias and with the residual, including
-    partial channel and token tiles."""
+    partial channel and token tiles; 64- and 128-token units (MTHIP_GEMM_STREAM_BT)."""
     monkeypatch.setenv("MTHIP_GEMM_STREAM", "2")
+    monkeypatch.setenv("MTHIP_GEMM_STREAM_BT", bt)
     g = Gen(M + N + K)
     x = g.randn((M, K), "float16")
     w = g.randn((N, K), "float16", 1.0 / np.sqrt(K))
