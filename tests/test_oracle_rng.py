@@ -3,9 +3,14 @@ and checks the product generator (libmthip host code) against it bit for bit.
 
 Pins: splitmix64's published test vectors; the 53-bit scaling of the uniform from the pinned
 u64 stream; the polar pair's ordering/acceptance from the pinned uniforms; normality (KS);
-the spare-normal bookkeeping across fp32 pair fills and fp16 per-element fills."""
+the spare-normal bookkeeping across fp32 pair fills and fp16 per-element fills; and, where the
+reference tree is present, the reference's own generator compiled from module.cpp
+(oracle/_ref/libref_rng.so, built by `make -C oracle ref`) bit for bit over streams, odd and
+even fills and interleaved fp32/fp16 draws."""
 
+import ctypes
 import math
+import os
 
 import numpy as np
 import pytest
@@ -106,3 +111,83 @@ def test_kaiming_uniform_consumes_uniforms_with_default_bound(orc):
     mt.nn.init.kaiming_uniform_(w, a=math.sqrt(5))
     bound = math.sqrt(3.0) * math.sqrt(2.0 / 6.0) / math.sqrt(36.0)
     assert np.array_equal(w.numpy(), o.uniform((8, 4, 3, 3), -bound, bound))
+
+
+# ------------------------------------------------------------------ against the reference build
+
+_REF = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "oracle", "_ref", "libref_rng.so")
+
+
+@pytest.fixture(scope="module")
+def ref():
+    if not os.path.exists(_REF):
+        pytest.skip("oracle/_ref/libref_rng.so not built (needs the reference tree: make -C oracle ref)")
+    lib = ctypes.CDLL(_REF)
+    u64, dbl, vp, i64 = ctypes.c_uint64, ctypes.c_double, ctypes.c_void_p, ctypes.c_int64
+    lib.ref_rng_new.restype, lib.ref_rng_new.argtypes = vp, [u64]
+    lib.ref_rng_free.restype, lib.ref_rng_free.argtypes = None, [vp]
+    lib.ref_rng_next_u64.restype, lib.ref_rng_next_u64.argtypes = u64, [vp]
+    lib.ref_rng_next_uniform.restype, lib.ref_rng_next_uniform.argtypes = dbl, [vp]
+    lib.ref_rng_next_normal.restype, lib.ref_rng_next_normal.argtypes = dbl, [vp]
+    for name in ("ref_rng_fill_normal_f32", "ref_rng_fill_uniform_f32"):
+        fn = getattr(lib, name)
+        fn.restype, fn.argtypes = None, [vp, vp, i64, dbl, dbl]
+    return lib
+
+
+class _RefRng:
+    def __init__(self, lib, seed):
+        self.lib, self.p = lib, lib.ref_rng_new(seed)
+
+    def __del__(self):
+        self.lib.ref_rng_free(self.p)
+
+    def randn_f32(self, n, mean=0.0, std=1.0):
+        out = np.empty(n, np.float32)
+        self.lib.ref_rng_fill_normal_f32(self.p, out.ctypes.data, n, mean, std)
+        return out
+
+    def uniform_f32(self, n, a, b):
+        out = np.empty(n, np.float32)
+        self.lib.ref_rng_fill_uniform_f32(self.p, out.ctypes.data, n, a, b)
+        return out
+
+
+SEEDS = [0, 1, 42, 1234567, 2**63 + 5, 2**64 - 1]
+
+
+@pytest.mark.parametrize("seed", SEEDS)
+def test_oracle_streams_equal_the_reference_build(orc, ref, seed):
+    """u64, open-uniform and standard-normal streams (the last with the spare carried between
+    draws) from the reference's module.cpp equal the oracle's, draw for draw."""
+    r, o = _RefRng(ref, seed), orc.Rng(seed)
+    assert [ref.ref_rng_next_u64(r.p) for _ in range(1000)] == [o.next_u64() for _ in range(1000)]
+    got = [ref.ref_rng_next_uniform(r.p) for _ in range(1000)]
+    assert got == [o.uniform_open() for _ in range(1000)]
+    got = [ref.ref_rng_next_normal(r.p) for _ in range(1001)]
+    assert got == [o.next_normal() for _ in range(1001)]
+
+
+@pytest.mark.parametrize("seed", SEEDS)
+def test_oracle_fills_equal_the_reference_build(orc, ref, seed):
+    """A sequence of contiguous fp32 normal fills of odd and even lengths (a fill that ends on
+    the first of a pair leaves the second as the spare, and the next fill starts with it),
+    uniform fills, single draws and fp16 per-element draws in between: the oracle equals the
+    reference build bit for bit, array by array."""
+    r, o = _RefRng(ref, seed), orc.Rng(seed)
+    for kind, n, a, b in [("n", 5, 0.0, 1.0), ("n", 7, 0.5, 2.0), ("n", 1, 0.0, 1.0), ("n", 0, 0.0, 1.0),
+                          ("u", 11, -1.0, 1.0), ("n", 10, -3.0, 0.25), ("h", 7, 0.0, 1.0), ("n", 3, 0.0, 1.0),
+                          ("hu", 9, -0.5, 0.5), ("s", 1, 0.0, 1.0), ("n", 4096, 0.0, 1.0), ("u", 1000, 2.0, 5.0)]:
+        if kind == "n":
+            assert np.array_equal(o.randn((n,), "float32", a, b), r.randn_f32(n, a, b)), (kind, n)
+        elif kind == "u":
+            assert np.array_equal(o.uniform((n,), a, b, "float32"), r.uniform_f32(n, a, b)), (kind, n)
+        elif kind == "h":
+            # fp16 normal_: one standard normal per element, mean + std * z narrowed through float
+            z = np.array([ref.ref_rng_next_normal(r.p) for _ in range(n)])
+            assert np.array_equal(o.randn((n,), "float16", a, b), orc.f2h(np.float32(a + b * z))), (kind, n)
+        elif kind == "hu":
+            u = np.array([ref.ref_rng_next_uniform(r.p) for _ in range(n)])
+            assert np.array_equal(o.uniform((n,), a, b, "float16"), orc.f2h(np.float32(a + (b - a) * u))), (kind, n)
+        else:
+            assert o.next_normal() == ref.ref_rng_next_normal(r.p)
