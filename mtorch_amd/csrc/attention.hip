@@ -138,6 +138,16 @@ void flash_fwd_f16_kernel(const FlashArgs a) {
     }
   }
 
+  // Row sums by MFMA: where the value dims leave a padding row in the last 32-dim block (DK not
+  // a multiple of 32; Ev <= DK), V's dim Ev is staged as 1 for every key, so O^T row Ev
+  // accumulates sum_k P[q][k] -- the sum of the fp16 weights the PV product actually uses -- and
+  // the softmax loop skips its 32 adds and exchange per tile.  The lazy rescale scales that row
+  // with the rest.  Fixed at compile time: a run-time choice between the two loop bodies costs
+  // the two-key-group instance its register budget.  Dim parts (DS > 1) would put the row in
+  // another wave's blocks.
+  constexpr bool kOnes = DS == 1 && DK % 32 != 0;
+  constexpr bool ones = kOnes;
+
   // K/V staging: chunk c of this thread covers row (c / CHR) and dims 8*(c % CHR) of the tile.
   const __amdgpu_buffer_rsrc_t k_rsrc = __builtin_amdgcn_make_buffer_rsrc(
       (void*)K, (short)0, (int)(((int64_t)(Lk > 0 ? Lk - 1 : 0) * a.ks[2] + E) * 2), 0x00020000);
@@ -174,7 +184,12 @@ void flash_fwd_f16_kernel(const FlashArgs a) {
 #pragma unroll
       for (int i = 0; i < VCH; ++i) {
         const int c = tid + i * NT;
-        if (c < BKV * VCHR) *reinterpret_cast<uint4*>(&Vr[(c % BKV) * VRP + (c / BKV) * 8]) = vreg[i];
+        uint4 val = vreg[i];
+        // the sum column: value 1 at dim Ev of every existing key (Ev % 8 == 0 under VEC; the
+        // chunk was loaded as zeros)
+        if constexpr (kOnes)
+          if (ones && (c / BKV) * 8 == Ev && kv0 + c % BKV < Lk) val = make_uint4(0x3c00u, 0u, 0u, 0u);
+        if (c < BKV * VCHR) *reinterpret_cast<uint4*>(&Vr[(c % BKV) * VRP + (c / BKV) * 8]) = val;
       }
     } else {
       for (int idx = tid; idx < BKV * DK; idx += NT) {
@@ -187,6 +202,7 @@ void flash_fwd_f16_kernel(const FlashArgs a) {
         const int key = idx / (DVB * 32), d = idx - key * (DVB * 32);
         uint16_t bits = 0;
         if (kv0 + key < Lk && d < Ev) bits = V[(int64_t)(kv0 + key) * a.vs[2] + d];
+        if (kOnes && ones && kv0 + key < Lk && d == Ev) bits = 0x3c00u;  // the sum column
         Vr[key * VRP + d] = bits;
       }
     }
@@ -282,16 +298,23 @@ void flash_fwd_f16_kernel(const FlashArgs a) {
       m_run = m_cand;
     }
     const float m_use = m_run == -INFINITY ? 0.0f : m_run;
-    float psum = 0.0f;
+    if (kOnes && ones) {
 #pragma unroll
-    for (int sb = 0; sb < 2; ++sb)
+      for (int sb = 0; sb < 2; ++sb)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        s[sb][r] = __builtin_amdgcn_exp2f(fmaf(s[sb][r], sl2, -m_use));
-        psum += s[sb][r];
-      }
-    psum += __shfl_xor(psum, 32, 64);
-    l_run += psum;
+        for (int r = 0; r < 16; ++r) s[sb][r] = __builtin_amdgcn_exp2f(fmaf(s[sb][r], sl2, -m_use));
+    } else {
+      float psum = 0.0f;
+#pragma unroll
+      for (int sb = 0; sb < 2; ++sb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          s[sb][r] = __builtin_amdgcn_exp2f(fmaf(s[sb][r], sl2, -m_use));
+          psum += s[sb][r];
+        }
+      psum += __shfl_xor(psum, 32, 64);
+      l_run += psum;
+    }
 
     // O^T += V^T . P^T, four 16-key steps.
 #pragma unroll
@@ -318,6 +341,18 @@ void flash_fwd_f16_kernel(const FlashArgs a) {
         }
       }
     }
+  }
+
+  if (kOnes && ones) {
+    // O^T[Ev][q] sits in register 4*(o/8) + o%4 of block Ev/32 (o = Ev % 32) in the lanes of
+    // half (o/4) % 2; every lane takes its query's value from there.
+    const int ib = Ev >> 5, o = Ev & 31, rr = 4 * (o >> 3) + (o & 3), half = (o >> 2) & 1;
+    float v = 0.0f;
+#pragma unroll
+    for (int i = 0; i < DVBP; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) v = (i == ib && r == rr) ? acc[i][r] : v;
+    l_run = __shfl(v, col + 32 * half, 64);
   }
 
   if constexpr (KG > 1) {

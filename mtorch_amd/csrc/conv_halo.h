@@ -63,8 +63,10 @@ struct HaloArgs {
 // Load bookkeeping of producer wave P of NPW, fixed at compile time.  LW weight instructions per
 // slot; the next block's LP patch instructions spread over the slots of taps 0..6 (PPS per
 // slot), each slot issuing its patch part ahead of its weights.  Producer P issues the
-// instructions gi with gi % NPW == P of every slot, and waits only for its own.
-template <int LW, int LP, int SW, int NPW, int P>
+// instructions gi with gi % NPW == P of every slot, and waits only for its own.  TR, PW: output
+// rows and patch row width of the unit (patch instruction gi holds patch pixels 8gi .. 8gi+7,
+// row-major).
+template <int LW, int LP, int SW, int NPW, int P, int TR, int PW>
 struct HaloSchedule {
   static constexpr int PPS = (LP + 6) / 7;
   static constexpr int patch_in(int tap) {
@@ -99,9 +101,49 @@ struct HaloSchedule {
     }
     return n;
   }
+  // Patch instructions that tap t reads: the pixels of patch rows 0 .. t/3 + TR - 1.
+  static constexpr int need(int t) {
+    const int n = ((t / 3 + TR) * PW + 7) / 8;
+    return n < LP ? n : LP;
+  }
+  // The first channel block has no previous block to stream its patch under, so the prologue
+  // issues it in row order with each tap's rows ahead of that tap's weights (taps 0 .. SW-2),
+  // then the rest of the patch: step 0 waits for the top TR rows and its weights only, not for
+  // the whole patch.  Loads allowed in flight at the wait that precedes step T of that block:
+  // everything this producer issued after its last load that step T reads.
+  static constexpr int first_pending(int T) {
+    int pos = 0, req = 0, pi = 0;
+    const int nT = need(T);
+    for (int k = 0; k <= SW - 2; ++k) {
+      for (; pi < need(k); ++pi)
+        if (pi % NPW == P) {
+          ++pos;
+          if (pi < nT) req = pos;
+        }
+      for (int g = 0; g < LW; ++g)
+        if (g % NPW == P) {
+          ++pos;
+          if (k == T) req = pos;
+        }
+    }
+    for (; pi < LP; ++pi)
+      if (pi % NPW == P) {
+        ++pos;
+        if (pi < nT) req = pos;
+      }
+    for (int t = 0; t < T; ++t) {  // slots 0 .. T-1: block 1's patch part, then weights
+      pos += p_loads(t);
+      for (int g = 0; g < LW; ++g)
+        if (g % NPW == P) {
+          ++pos;
+          if (t + SW - 1 == T) req = pos;
+        }
+    }
+    return pos - req;
+  }
   static constexpr bool fits() {
     for (int t = 0; t < 9; ++t)
-      if (pending(t) > 63) return false;
+      if (pending(t) > 63 || first_pending(t) > 63) return false;
     return true;
   }
 };
@@ -123,10 +165,10 @@ __global__ __launch_bounds__(64 * (4 + NPW)) void conv3x3_halo_kernel(const Halo
   constexpr int LW = BM / 8;            // weight DMA instructions per step
   constexpr int LP = (NP + 7) / 8;      // patch DMA instructions per channel block
   constexpr uint32_t WSTAGE = BM * 128, PBUF = LP * 8 * 128;
-  using Sched0 = HaloSchedule<LW, LP, SW, NPW, 0>;
+  using Sched0 = HaloSchedule<LW, LP, SW, NPW, 0, TR, PW>;
   static_assert(WGM * WGN == NW && WMO % 16 == 0 && WNP % 16 == 0 && TW % 4 == 0 && BM % 8 == 0, "tile shape");
   static_assert(SW >= 3 && SW <= 9 && 18 % SW == 0, "weight ring depth: 3, 6 or 9");
-  static_assert(Sched0::fits() && HaloSchedule<LW, LP, SW, NPW, NPW - 1>::fits(), "vmcnt range");
+  static_assert(Sched0::fits() && HaloSchedule<LW, LP, SW, NPW, NPW - 1, TR, PW>::fits(), "vmcnt range");
   static_assert(NPW >= 1 && NPW <= 2, "one or two producer waves");
   static_assert((size_t)(2 * PBUF + SW * WSTAGE) <= 160 * 1024, "LDS");
   static_assert(PBUF < 65536 && (SW - 1) * WSTAGE < 65536, "LDS read offsets are 16-bit immediates");
@@ -157,7 +199,7 @@ __global__ __launch_bounds__(64 * (4 + NPW)) void conv3x3_halo_kernel(const Halo
   // =============================================================================== producer
   auto producer = [&](auto p_c) {
     constexpr int P = decltype(p_c)::value;
-    using Sched = HaloSchedule<LW, LP, SW, NPW, P>;
+    using Sched = HaloSchedule<LW, LP, SW, NPW, P, TR, PW>;
     const __amdgpu_buffer_rsrc_t x_rsrc =
         __builtin_amdgcn_make_buffer_rsrc((void*)args.x, (short)0, args.x_bytes, 0x00020000);
     const __amdgpu_buffer_rsrc_t w_rsrc =
@@ -202,54 +244,58 @@ __global__ __launch_bounds__(64 * (4 + NPW)) void conv3x3_halo_kernel(const Halo
       for (int gi = G0; gi < G1; ++gi)
         if (gi % NPW == P) dma16(x_rsrc, dst + gi * 1024, p_off[gi], soff);
     };
-    // prologue: the nine slots of a block before the first, back to back -- block 0's patch in
-    // the parts taps 0..6 issue, and the weights of steps 0 .. SW-2 in the slots of steps
-    // -(SW-1) .. -1 -- so that the loads in flight at every wait are the ones pending() counts.
-    auto pre_slot = [&](auto t_c) {
-      constexpr int T = decltype(t_c)::value, K = T - 10 + SW;  // weights of step K (if >= 0)
-      constexpr int PPS = Sched::PPS;
-      if constexpr (Sched::patch_in(T) > 0) issue_p(ic<T * PPS>{}, ic<T * PPS + Sched::patch_in(T)>{}, 0, 0);
-      if constexpr (K >= 0) issue_w(0, K, K);
+    // prologue: block 0's patch in row order, the rows of tap k ahead of the weights of step k
+    // (k = 0 .. SW-2), then the rest of the patch (first_pending counts this order)
+    auto pre = [&](auto k_c) {
+      constexpr int k = decltype(k_c)::value;
+      issue_p(ic<k == 0 ? 0 : Sched::need(k - 1)>{}, ic<Sched::need(k)>{}, 0, 0);
+      issue_w(0, k, k);
     };
-    pre_slot(ic<0>{});
-    pre_slot(ic<1>{});
-    pre_slot(ic<2>{});
-    pre_slot(ic<3>{});
-    pre_slot(ic<4>{});
-    pre_slot(ic<5>{});
-    pre_slot(ic<6>{});
-    pre_slot(ic<7>{});
-    pre_slot(ic<8>{});
+    pre(ic<0>{});
+    pre(ic<1>{});
+    if constexpr (SW > 3) {
+      pre(ic<2>{});
+      pre(ic<3>{});
+      pre(ic<4>{});
+    }
+    if constexpr (SW > 6) {
+      pre(ic<5>{});
+      pre(ic<6>{});
+      pre(ic<7>{});
+    }
+    issue_p(ic<Sched::need(SW - 2)>{}, ic<LP>{}, 0, 0);
     // step s = 9j + T of a block of parity JP: wait for step s's operands, the barrier that
     // opens step s, then slot s
-    auto slot = [&](int j, auto jp_c, auto t_c) {
+    auto slot = [&](int j, auto jp_c, auto t_c, auto first_c) {
       constexpr int JP = decltype(jp_c)::value, T = decltype(t_c)::value;
       constexpr int STAGE = (9 * JP + T + SW - 1) % SW;  // ring stage of step s + SW - 1 (SW | 18)
       constexpr int WC = (T + SW - 1) / 9, WT = (T + SW - 1) % 9;
       constexpr int PPS = Sched::PPS;
-      __builtin_amdgcn_s_waitcnt(vmcnt_only(Sched::pending(T)));
+      constexpr int PEND = decltype(first_c)::value ? Sched::first_pending(T) : Sched::pending(T);
+      __builtin_amdgcn_s_waitcnt(vmcnt_only(PEND));
       __builtin_amdgcn_s_barrier();
       if constexpr (Sched::patch_in(T) > 0)
         issue_p(ic<T * PPS>{}, ic<T * PPS + Sched::patch_in(T)>{}, j + 1, 1 - JP);
       issue_w(j + WC, WT, STAGE);
     };
-    auto block = [&](int j, auto jp_c) {
-      slot(j, jp_c, ic<0>{});
-      slot(j, jp_c, ic<1>{});
-      slot(j, jp_c, ic<2>{});
-      slot(j, jp_c, ic<3>{});
-      slot(j, jp_c, ic<4>{});
-      slot(j, jp_c, ic<5>{});
-      slot(j, jp_c, ic<6>{});
-      slot(j, jp_c, ic<7>{});
-      slot(j, jp_c, ic<8>{});
+    auto block = [&](int j, auto jp_c, auto first_c) {
+      slot(j, jp_c, ic<0>{}, first_c);
+      slot(j, jp_c, ic<1>{}, first_c);
+      slot(j, jp_c, ic<2>{}, first_c);
+      slot(j, jp_c, ic<3>{}, first_c);
+      slot(j, jp_c, ic<4>{}, first_c);
+      slot(j, jp_c, ic<5>{}, first_c);
+      slot(j, jp_c, ic<6>{}, first_c);
+      slot(j, jp_c, ic<7>{}, first_c);
+      slot(j, jp_c, ic<8>{}, first_c);
     };
-    int j = 0;
+    block(0, ic<0>{}, ic<1>{});
+    int j = 1;
     for (; j + 1 < ncb; j += 2) {
-      block(j, ic<0>{});
-      block(j + 1, ic<1>{});
+      block(j, ic<1>{}, ic<0>{});
+      block(j + 1, ic<0>{}, ic<0>{});
     }
-    if (j < ncb) block(j, ic<0>{});
+    if (j < ncb) block(j, ic<1>{}, ic<0>{});
     // the barrier the compute waves pass at the end of their last step (its operands are the
     // clamped loads of the slots past the slice; nothing reads them)
     __builtin_amdgcn_s_barrier();

@@ -192,9 +192,31 @@ int launch_dtl(int device, const GemmArgs& a, int64_t batch, hipStream_t s) {
   using T = uint16_t;
   constexpr bool F = MODE == MODE_CONV;
   if constexpr (EPI == EPI_GEGLU) {
-    return launch_tile<T, 128, 64, MODE, EPI, ACT, F, 4, 3>(device, a, batch, s);
+    // MTHIP_GEMM_GEGLU_TILE: 0 = 128x64 (4x1 waves of 32x64), 1 = 128x128 (2x2 waves of 64x64)
+    // with 3 stages, 2 = 128x128 with 2 stages.  By default 128x128 / 2 stages where the 128x64
+    // tiles number >= 2560 or, over >= 512 rows, <= 640 (SD feed-forward, graph-replayed:
+    // 8192x2560x320 43.7 -> 38.9 us, 512x10240x1280 30.7 -> 29.4; 4096x2560x320 22.7 against
+    // 23.6 and 2048x5120x640 even stay on 128x64; 3 stages hold one workgroup per CU and lose
+    // everywhere).
+    const int64_t t64 = ceil_div(a.M, 128) * ceil_div(a.N, 64) * batch;
+    const int dflt = (t64 >= 2560 || (a.M >= 512 && t64 <= 640)) ? 2 : 0;
+    switch (env_flag("MTHIP_GEMM_GEGLU_TILE", dflt)) {
+      case 1:
+        return launch_tile<T, 128, 128, MODE, EPI, ACT, F, 2, 3>(device, a, batch, s);
+      case 2:
+        return launch_tile<T, 128, 128, MODE, EPI, ACT, F, 2, 2>(device, a, batch, s);
+      default:
+        return launch_tile<T, 128, 64, MODE, EPI, ACT, F, 4, 3>(device, a, batch, s);
+    }
   } else if constexpr (ACT != MTHIP_ACT_NONE) {
-    return launch_tile<T, 64, 64, MODE, EPI, ACT, F, 2, 3>(device, a, batch, s);
+    switch (env_flag("MTHIP_GEMM_DTL_TILE", 0)) {
+      case 3:
+        return launch_tile<T, 64, 128, MODE, EPI, ACT, F, 2, 3>(device, a, batch, s);
+      case 5:
+        return launch_tile<T, 128, 128, MODE, EPI, ACT, F, 2, 2>(device, a, batch, s);
+      default:
+        return launch_tile<T, 64, 64, MODE, EPI, ACT, F, 2, 3>(device, a, batch, s);
+    }
   } else {
     switch (dtl_tile_for(MODE, a.M, a.N, a.K)) {
       case 1:

@@ -451,17 +451,19 @@ __device__ __forceinline__ void gemm_finish_unit(const GemmArgs& args, const Gem
     // wave owns 64 columns = fragment 0 (values) + fragment 1 (gates) of 32 output columns:
     // out[row][col] = value * gelu(gate), each factor narrowed as the unfused
     // linear -> chunk -> gelu -> mul sequence narrows it.  N is a multiple of 64 (the launcher
-    // requires 32 output columns per block), so all 64 columns of a tile exist.
-    static_assert(FN == 2 && WGN == 1 && BN == 64, "GEGLU epilogue pairs two 32-column fragments");
+    // requires 32 output columns per block), so a wave's 64 columns exist whole or not at all.
+    static_assert(FN == 2 && WN == 64, "GEGLU epilogue pairs two 32-column fragments");
     const T* bias = reinterpret_cast<const T*>(args.bias);
     T* Cp = reinterpret_cast<T*>(args.c);
     const int Nout = (int)args.N / 2;
+    const int n0 = (int)un.n0 + wn * WN;  // the wave's first (permuted) column
+    if (n0 >= (int)args.N) return;
     const bool has_b = bias != nullptr;
     float bval[4][4], bgate[4][4];
     if (has_b && ((uintptr_t)bias & (sizeof(T) == 2 ? 7 : 15)) == 0) {
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
-        const int pc = (int)un.n0 + 8 * g + lane_col;  // permuted column of the value
+        const int pc = n0 + 8 * g + lane_col;  // permuted column of the value
         const Raw4<T> bv = load_raw4<T>(bias + pc), bg = load_raw4<T>(bias + pc + 32);
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
@@ -472,7 +474,7 @@ __device__ __forceinline__ void gemm_finish_unit(const GemmArgs& args, const Gem
     } else if (has_b) {
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
-        const int pc = (int)un.n0 + 8 * g + lane_col;
+        const int pc = n0 + 8 * g + lane_col;
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
           bval[g][t] = Elem<T>::load(bias, pc + t);
@@ -519,7 +521,7 @@ __device__ __forceinline__ void gemm_finish_unit(const GemmArgs& args, const Gem
         if (row >= M) continue;
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
-          const int col0 = (int)un.n0 / 2 + 8 * g + lane_col;
+          const int col0 = n0 / 2 + 8 * g + lane_col;
           uint16_t* p = reinterpret_cast<uint16_t*>(Cp) + (int64_t)row * args.ldc + col0;
           const uint32_t hv[4] = {out[i][g].x & 0xffffu, out[i][g].x >> 16, out[i][g].y & 0xffffu, out[i][g].y >> 16};
           if (col0 + 4 <= Nout && ((uintptr_t)p & 7) == 0) {
@@ -550,7 +552,7 @@ __device__ __forceinline__ void gemm_finish_unit(const GemmArgs& args, const Gem
       if (row < M) {
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
-          const int col0 = (int)un.n0 / 2 + 8 * g + lane_col;
+          const int col0 = n0 / 2 + 8 * g + lane_col;
           if (col0 < Nout) {
             float v[4];
 #pragma unroll
