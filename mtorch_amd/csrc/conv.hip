@@ -18,6 +18,8 @@
 namespace mthip {
 
 int launch_conv_gemm(int device, int dtype, const GemmArgs& a, hipStream_t s);
+int try_stream_conv1x1(int device, const void* x_nhwc, const void* wp, const void* b, void* y, const void* residual,
+                       int64_t B, int64_t HW, int64_t Cp, int64_t O, hipStream_t s);
 
 namespace {
 
@@ -240,6 +242,10 @@ int run_conv_gemm_nhwc(int device, int dtype, const void* xp, const void* wp, co
     const int rc = try_conv_halo(device, xp, wp, b, y, B, H, W, Cp, O, KH, KW, sh, sw, ph, pw, dh, dw, residual,
                                  chan_add, chan_add_ld, s);
     if (rc >= 0) return rc;
+    if (KH == 1 && KW == 1 && sh == 1 && sw == 1 && ph == 0 && pw == 0 && !chan_add) {
+      const int rs = try_stream_conv1x1(device, xp, wp, b, y, residual, B, H * W, Cp, O, s);
+      if (rs >= 0) return rs;
+    }
   }
   GemmArgs a{};
   a.M = O;

@@ -352,6 +352,135 @@ int launch_conv_gemm(int device, int dtype, const GemmArgs& a, hipStream_t s) {
   return launch_gemm_fast<float, MODE_CONV, EPI_CONV, false>(device, a, 1, s);
 }
 
+namespace {
+
+// Token tile and K split of the streamed kernel from a makespan model: a persistent workgroup
+// per CU runs ceil(units / CUs) units of `steps` K steps each plus an epilogue, and a split adds
+// the fp32 slices' write and read and the reduction launch.  Per-step and per-unit costs (µs) of
+// 64- and 128-token units come from graph-replayed sweeps; 128-token units lost on every SD
+// shape (8192x960x320: 37.1 against 23.8 us), so they run only when MTHIP_GEMM_STREAM_BT=128
+// forces them.
+void stream_plan(int64_t M, int64_t N, int64_t K, int64_t cus, int& best_bt, int64_t& best_ks) {
+  const int64_t nk = K / 64, groups = nk / 5;
+  const double step_us[2] = {0.40, 0.55}, epi_us = 0.4;
+  const int force_bt = env_flag("MTHIP_GEMM_STREAM_BT", 64);
+  best_bt = 64;
+  best_ks = 1;
+  double best = 0.0;
+  for (int bi = 0; bi < 2; ++bi) {
+    const int bt = bi ? 128 : 64;
+    if (force_bt && force_bt != bt) continue;
+    for (int64_t ks = 1; ks <= std::min<int64_t>(8, groups); ++ks) {
+      if (groups % ks) continue;
+      const int64_t units = ceil_div(M, bt) * ceil_div(N, 80) * ks;
+      double t = (double)ceil_div(units, cus) * ((double)(nk / ks) * step_us[bi] + epi_us);
+      if (ks > 1) t += 3.0 + (double)((ks + 1) * M * N * 4) / 3.0e6;
+      if (best == 0.0 || t < best) {
+        best = t;
+        best_bt = bt;
+        best_ks = ks;
+      }
+    }
+  }
+}
+
+// Launches the streamed kernel over sa (operands, bias, residual, layout already set) with the
+// planned tile and split, then the slice reduction (r: the reduction's GemmArgs, EPI_LINEAR
+// row-major or EPI_CONV NCHW).
+template <bool NCHW>
+int launch_stream(int device, StreamArgs sa, GemmArgs r, int64_t K, hipStream_t s) {
+  const int64_t M = sa.M, N = sa.N, cus = cu_count(device);
+  int bt;
+  int64_t ks;
+  stream_plan(M, N, K, cus, bt, ks);
+  sa.tiles_m = (int)ceil_div(M, bt);
+  sa.tiles_n = (int)ceil_div(N, 80);
+  sa.ksplit = (int)ks;
+  sa.steps = (int)(K / 64 / ks);
+  sa.units = sa.tiles_m * sa.tiles_n * sa.ksplit;
+  // consecutive units share the operand with fewer tiles (held in the XCD's L2)
+  sa.m_fast = sa.tiles_m <= sa.tiles_n ? 1 : 0;
+  void* ws = nullptr;
+  if (ks > 1) {
+    const int64_t rows = NCHW ? N : M, cols = NCHW ? M : N;
+    r.ld_partial = ceil_div(cols, 4) * 4;
+    r.ksplit = ks;
+    if (int rc = mthip_malloc(device, (size_t)(ks * rows * r.ld_partial) * sizeof(float), &ws)) return rc;
+    r.partial = static_cast<float*>(ws);
+    sa.partial = r.partial;
+    sa.ld_partial = (int)r.ld_partial;
+  }
+  int64_t g = std::min<int64_t>(sa.units, cus);
+  if (g > 8) g = g / 8 * 8;
+  const bool hr = sa.residual != nullptr && ks == 1;
+  if (bt == 128) {
+    if (hr)
+      hipLaunchKernelGGL((gemm_stream_kernel<128, true, NCHW>), dim3((unsigned)g), dim3(320), 0, s, sa);
+    else
+      hipLaunchKernelGGL((gemm_stream_kernel<128, false, NCHW>), dim3((unsigned)g), dim3(320), 0, s, sa);
+  } else {
+    if (hr)
+      hipLaunchKernelGGL((gemm_stream_kernel<64, true, NCHW>), dim3((unsigned)g), dim3(320), 0, s, sa);
+    else
+      hipLaunchKernelGGL((gemm_stream_kernel<64, false, NCHW>), dim3((unsigned)g), dim3(320), 0, s, sa);
+  }
+  int rc = check_launch("gemm_stream_kernel");
+  if (rc == MTHIP_OK && ks > 1) {
+    const int64_t work = r.M * ceil_div(r.N, 4);
+    const unsigned rg = (unsigned)std::min<int64_t>(ceil_div(work, 256), 8192);
+    if constexpr (NCHW)
+      hipLaunchKernelGGL((gemm_splitk_reduce_kernel<uint16_t, EPI_CONV, MTHIP_ACT_NONE>), dim3(rg), dim3(256), 0, s, r);
+    else
+      hipLaunchKernelGGL((gemm_splitk_reduce_kernel<uint16_t, EPI_LINEAR, MTHIP_ACT_NONE>), dim3(rg), dim3(256), 0, s, r);
+    rc = check_launch("gemm_splitk_reduce_kernel(stream)");
+  }
+  if (ws) mthip_free(device, ws);  // stream-ordered: reused only by later work
+  return rc;
+}
+
+}  // namespace
+
+// fp16 1x1 stride-1 unpadded convs of a channels-last activation (x_nhwc [B][HW][Cp], Cp == K a
+// multiple of 320, HW % 4 == 0) with an NCHW output: the streamed kernel's NCHW mode -- the
+// SD transformer's proj_out and the ResBlock shortcuts.  MTHIP_CONV_STREAM=0 turns it off
+// (1, the default: up to 1280 output channels; 2: wherever it applies).  Returns -1 when it
+// does not apply.  (Shared with conv.hip.)
+int try_stream_conv1x1(int device, const void* x_nhwc, const void* wp, const void* b, void* y, const void* residual,
+                       int64_t B, int64_t HW, int64_t Cp, int64_t O, hipStream_t s) {
+  const int mode = env_flag("MTHIP_CONV_STREAM", 1);
+  if (!mode || (mode == 1 && O > 1280)) return -1;
+  const int64_t M = B * HW;
+  if (Cp % 320 != 0 || HW % 4 != 0 || O % 16 != 0 || ((uintptr_t)y & 7) || ((uintptr_t)b & 1) ||
+      ((uintptr_t)residual & 7) || !aligned16(x_nhwc) || !aligned16(wp))
+    return -1;
+  if (M * O >= (int64_t(1) << 30) || M * Cp >= (int64_t(1) << 30) || O * Cp >= (int64_t(1) << 30)) return -1;
+  StreamArgs sa{};
+  sa.a = x_nhwc;
+  sa.b = wp;
+  sa.c = y;
+  sa.bias = b;
+  sa.residual = residual;
+  sa.M = (int)M;
+  sa.N = (int)O;
+  sa.lda = (int)Cp;
+  sa.ldb = (int)Cp;
+  sa.a_bytes = (int)(M * Cp * 2);
+  sa.b_bytes = (int)(O * Cp * 2);
+  sa.hw = (int)HW;
+  sa.div_hw = FastDiv((uint32_t)HW);
+  // the slice reduction as the conv GEMM's: rows = output channels, columns = pixels
+  GemmArgs r{};
+  r.M = O;
+  r.N = M;
+  r.c = y;
+  r.bias = b;
+  r.residual = residual;
+  r.OH = HW;
+  r.OW = 1;
+  r.div_ohw = FastDiv((uint32_t)HW);
+  return launch_stream<true>(device, sa, r, Cp, s);
+}
+
 }  // namespace mthip
 
 using namespace mthip;
@@ -361,11 +490,8 @@ extern "C" {
 namespace {
 
 // fp16 linears without an activation whose K is a multiple of 320 (units of whole 5-step ring
-// cycles) can take the streamed kernel (gemm_stream.h); MTHIP_GEMM_STREAM=0 turns it off.  The
-// K split comes from a makespan model: a persistent workgroup per CU runs ceil(units / CUs)
-// units of `steps` K steps each plus an epilogue, and a split adds the fp32 slices' write and
-// read and the reduction launch; MTHIP_GEMM_STREAM_BT=64/128 forces the token tile.  Returns -1
-// when it does not apply.
+// cycles) can take the streamed kernel (gemm_stream.h); MTHIP_GEMM_STREAM=0 turns it off.
+// Returns -1 when it does not apply.
 int try_stream_linear(int device, const GemmArgs& a, hipStream_t s) {
   const int mode = env_flag("MTHIP_GEMM_STREAM", 1);
   if (!mode) return -1;
@@ -383,31 +509,6 @@ int try_stream_linear(int device, const GemmArgs& a, hipStream_t s) {
   if (M * a.ldc >= (int64_t(1) << 31) || (a.residual && M * a.ld_res >= (int64_t(1) << 31)) ||
       M * a.lda >= (int64_t(1) << 30) || N * a.ldb >= (int64_t(1) << 30))
     return -1;
-  const int64_t nk = K / 64, groups = nk / 5;
-  const int64_t cus = cu_count(device);
-  // per-step and per-unit costs (µs) of 64- and 128-token units, from graph-replayed sweeps;
-  // 128-token units lost on every SD shape (8192x960x320: 37.1 against 23.8 us), so they run
-  // only when forced
-  const double step_us[2] = {0.40, 0.55}, epi_us = 0.4;
-  const int force_bt = env_flag("MTHIP_GEMM_STREAM_BT", 64);
-  int best_bt = 64;
-  int64_t best_ks = 1;
-  double best = 0.0;
-  for (int bi = 0; bi < 2; ++bi) {
-    const int bt = bi ? 128 : 64;
-    if (force_bt && force_bt != bt) continue;
-    for (int64_t ks = 1; ks <= std::min<int64_t>(8, groups); ++ks) {
-      if (groups % ks) continue;
-      const int64_t units = ceil_div(M, bt) * ceil_div(N, 80) * ks;
-      double t = (double)ceil_div(units, cus) * ((double)(nk / ks) * step_us[bi] + epi_us);
-      if (ks > 1) t += 3.0 + (double)((ks + 1) * M * N * 4) / 3.0e6;
-      if (best == 0.0 || t < best) {
-        best = t;
-        best_bt = bt;
-        best_ks = ks;
-      }
-    }
-  }
   StreamArgs sa{};
   sa.a = a.a;
   sa.b = a.b;
@@ -420,48 +521,9 @@ int try_stream_linear(int device, const GemmArgs& a, hipStream_t s) {
   sa.ldb = (int)a.ldb;
   sa.ldc = (int)a.ldc;
   sa.ld_res = (int)a.ld_res;
-  sa.tiles_m = (int)ceil_div(M, best_bt);
-  sa.tiles_n = (int)ceil_div(N, 80);
-  sa.ksplit = (int)best_ks;
-  sa.steps = (int)(nk / best_ks);
-  sa.units = sa.tiles_m * sa.tiles_n * sa.ksplit;
   sa.a_bytes = (int)a.a_bytes;
   sa.b_bytes = (int)a.b_bytes;
-  // consecutive units share the operand with fewer tiles (held in the XCD's L2)
-  sa.m_fast = sa.tiles_m <= sa.tiles_n ? 1 : 0;
-  void* ws = nullptr;
-  GemmArgs r = a;
-  if (best_ks > 1) {
-    r.ld_partial = ceil_div(N, 4) * 4;
-    r.ksplit = best_ks;
-    if (int rc = mthip_malloc(device, (size_t)(best_ks * M * r.ld_partial) * sizeof(float), &ws)) return rc;
-    r.partial = static_cast<float*>(ws);
-    sa.partial = r.partial;
-    sa.ld_partial = (int)r.ld_partial;
-  }
-  int64_t g = std::min<int64_t>(sa.units, cus);
-  if (g > 8) g = g / 8 * 8;
-  const bool hr = a.residual != nullptr && best_ks == 1;
-  if (best_bt == 128) {
-    if (hr)
-      hipLaunchKernelGGL((gemm_stream_kernel<128, true>), dim3((unsigned)g), dim3(320), 0, s, sa);
-    else
-      hipLaunchKernelGGL((gemm_stream_kernel<128, false>), dim3((unsigned)g), dim3(320), 0, s, sa);
-  } else {
-    if (hr)
-      hipLaunchKernelGGL((gemm_stream_kernel<64, true>), dim3((unsigned)g), dim3(320), 0, s, sa);
-    else
-      hipLaunchKernelGGL((gemm_stream_kernel<64, false>), dim3((unsigned)g), dim3(320), 0, s, sa);
-  }
-  int rc = check_launch("gemm_stream_kernel");
-  if (rc == MTHIP_OK && best_ks > 1) {
-    const int64_t work = M * ceil_div(N, 4);
-    const unsigned rg = (unsigned)std::min<int64_t>(ceil_div(work, 256), 8192);
-    hipLaunchKernelGGL((gemm_splitk_reduce_kernel<uint16_t, EPI_LINEAR, MTHIP_ACT_NONE>), dim3(rg), dim3(256), 0, s, r);
-    rc = check_launch("gemm_splitk_reduce_kernel(stream)");
-  }
-  if (ws) mthip_free(device, ws);  // stream-ordered: reused only by later work
-  return rc;
+  return launch_stream<false>(device, sa, a, K, s);
 }
 
 }  // namespace

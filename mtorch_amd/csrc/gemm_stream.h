@@ -20,6 +20,12 @@
 // (the launcher requires K / 64 to be a multiple of 5), so every unit starts at ring stage 0
 // and a group of SW steps has compile-time stages; the register set of step s is s & 1.
 //
+// NCHW: the 1x1 conv of a channels-last activation (A = x_nhwc [B*HW][Cp], B = the packed weight
+// [O][Cp]) stored NCHW, y[img][n][p] for token m = img*HW + p: the MFMA operands swap so that a
+// lane's accumulator is 4 consecutive pixels of one output channel (HW % 4 == 0: one image,
+// one 8-byte store), the bias is per channel and the residual NCHW like y; K-split partials go
+// to [split][N][ld_partial] (channel rows, pixel columns), the layout the conv reduction reads.
+//
 // LDS stage layout: the 80 weight rows, then the BT token rows, each row 64 halves (128 bytes)
 // with 16-byte chunk c at chunk c ^ ((row >> 1) & 7) (the ds_read_b128 passes of a fragment
 // cover all 64 banks).  Rows past M or N are fetched from an out-of-range offset and read as
@@ -47,9 +53,11 @@ struct StreamArgs {
   float* partial;  // ksplit > 1: [ksplit][M][ld_partial] fp32
   int ld_partial;
   int m_fast;  // 1: consecutive units walk the token tiles of one channel tile
+  int hw;          // NCHW: pixels per image
+  FastDiv div_hw;  // NCHW: division by hw
 };
 
-template <int BT, bool HAS_R>
+template <int BT, bool HAS_R, bool NCHW = false>
 __global__ __launch_bounds__(320) void gemm_stream_kernel(const StreamArgs args) {
   constexpr int BC = 80, NW = 4, SW = 5;
   constexpr int WT = BT / NW;              // tokens per compute wave
@@ -164,7 +172,8 @@ __global__ __launch_bounds__(320) void gemm_stream_kernel(const StreamArgs args)
   const __amdgpu_buffer_rsrc_t bias_rsrc =
       __builtin_amdgcn_make_buffer_rsrc((void*)bias, (short)0, bias ? N * 2 : 0, 0x00020000);
   const __amdgpu_buffer_rsrc_t res_rsrc = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)res, (short)0, (HAS_R && args.ksplit == 1) ? ((M - 1) * args.ld_res + N) * 2 : 0, 0x00020000);
+      (void*)res, (short)0,
+      (HAS_R && args.ksplit == 1) ? (NCHW ? M * N * 2 : ((M - 1) * args.ld_res + N) * 2) : 0, 0x00020000);
 
   // LDS read addresses in stage 0 (stage k is + k * STAGE; the second 32 k is ^ 64)
   uint32_t wa[FC], pa[FP];
@@ -204,20 +213,28 @@ __global__ __launch_bounds__(320) void gemm_stream_kernel(const StreamArgs args)
 
   // The current unit's epilogue operands, read when the unit starts (they arrive under its K
   // steps).  Lane l of fragment (fc, fp) holds channels n0 + fc*16 + 4*(l/16) .. +3 of token
-  // m0 + wave*WT + fp*16 + l%16.
+  // m0 + wave*WT + fp*16 + l%16 (NCHW: tokens m0 + wave*WT + fp*16 + 4*(l/16) .. +3 of channel
+  // n0 + fc*16 + l%16).
   // (A 128-token unit reads its residual at the epilogue: its registers would not fit beside
   // the tile under the K steps.)
   constexpr bool R_EARLY = FC * FP <= 5;
   Unit cur{};
   uint2 bz[FC], rz[FC][FP];
+  // this lane's channel and first token of fragment (fc, fp)
+  auto chan = [&](int fc) { return cur.n0 + fc * 16 + (NCHW ? (lane & 15) : 4 * (lane >> 4)); };
+  auto tok = [&](int fp) { return cur.m0 + wave * WT + fp * 16 + (NCHW ? 4 * (lane >> 4) : (lane & 15)); };
+  // NCHW element offset of (token m, channel n): image m / hw, pixel m % hw
+  auto nchw_off = [&](int m, int n) {
+    const int img = (int)args.div_hw.div((uint32_t)m);
+    return (img * N + n) * args.hw + (m - img * args.hw);
+  };
   auto load_residual = [&]() {
 #pragma unroll
     for (int fc = 0; fc < FC; ++fc)
 #pragma unroll
       for (int fp = 0; fp < FP; ++fp) {
-        const int n = cur.n0 + fc * 16 + 4 * (lane >> 4);
-        const int m = cur.m0 + wave * WT + fp * 16 + (lane & 15);
-        const int o = (m < M && n < N) ? m * args.ld_res + n : 0;
+        const int n = chan(fc), m = tok(fp);
+        const int o = (m < M && n < N) ? (NCHW ? nchw_off(m, n) : m * args.ld_res + n) : 0;
         const auto v = __builtin_amdgcn_raw_buffer_load_b64(res_rsrc, o * 2, 0, 0);
         rz[fc][fp] = make_uint2(v[0], v[1]);
       }
@@ -226,9 +243,15 @@ __global__ __launch_bounds__(320) void gemm_stream_kernel(const StreamArgs args)
     cur = decode(u);
 #pragma unroll
     for (int fc = 0; fc < FC; ++fc) {
-      const int n = cur.n0 + fc * 16 + 4 * (lane >> 4);
-      const auto v = __builtin_amdgcn_raw_buffer_load_b64(bias_rsrc, (n < N ? n : 0) * 2, 0, 0);
-      bz[fc] = make_uint2(v[0], v[1]);
+      const int n = chan(fc);
+      if constexpr (NCHW) {
+        // one channel per lane: its bias in both halves of every word
+        const uint32_t h = __builtin_amdgcn_raw_buffer_load_b16(bias_rsrc, (n < N ? n : 0) * 2, 0, 0);
+        bz[fc] = make_uint2(h | (h << 16), h | (h << 16));
+      } else {
+        const auto v = __builtin_amdgcn_raw_buffer_load_b64(bias_rsrc, (n < N ? n : 0) * 2, 0, 0);
+        bz[fc] = make_uint2(v[0], v[1]);
+      }
     }
     if constexpr (HAS_R && R_EARLY) load_residual();
     zero_acc();
@@ -239,10 +262,11 @@ __global__ __launch_bounds__(320) void gemm_stream_kernel(const StreamArgs args)
       for (int fc = 0; fc < FC; ++fc)
 #pragma unroll
         for (int fp = 0; fp < FP; ++fp) {
-          const int n = cur.n0 + fc * 16 + 4 * (lane >> 4);
-          const int m = cur.m0 + wave * WT + fp * 16 + (lane & 15);
+          const int n = chan(fc), m = tok(fp);
+          const int64_t o = NCHW ? ((int64_t)cur.split * N + n) * args.ld_partial + m
+                                 : ((int64_t)cur.split * M + m) * args.ld_partial + n;
           if (m < M && n < N)
-            *reinterpret_cast<float4*>(args.partial + ((int64_t)cur.split * M + m) * args.ld_partial + n) =
+            *reinterpret_cast<float4*>(args.partial + o) =
                 make_float4(acc[fc][fp][0], acc[fc][fp][1], acc[fc][fp][2], acc[fc][fp][3]);
         }
       return;
@@ -280,9 +304,9 @@ __global__ __launch_bounds__(320) void gemm_stream_kernel(const StreamArgs args)
     for (int fc = 0; fc < FC; ++fc)
 #pragma unroll
       for (int fp = 0; fp < FP; ++fp) {
-        const int n = cur.n0 + fc * 16 + 4 * (lane >> 4);
-        const int m = cur.m0 + wave * WT + fp * 16 + (lane & 15);
-        if (m < M && n < N) *reinterpret_cast<uint2*>(C + (int64_t)m * args.ldc + n) = out[fc][fp];
+        const int n = chan(fc), m = tok(fp);
+        if (m < M && n < N)
+          *reinterpret_cast<uint2*>(C + (NCHW ? (int64_t)nchw_off(m, n) : (int64_t)m * args.ldc + n)) = out[fc][fp];
       }
   };
 
@@ -301,7 +325,8 @@ __global__ __launch_bounds__(320) void gemm_stream_kernel(const StreamArgs args)
       for (int fc = 0; fc < FC; ++fc)
 #pragma unroll
         for (int fp = 0; fp < FP; ++fp)
-          acc[fc][fp] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wf[SET][kk][fc], pf[SET][kk][fp], acc[fc][fp], 0, 0, 0);
+          acc[fc][fp] = NCHW ? __builtin_amdgcn_mfma_f32_16x16x32_f16(pf[SET][kk][fp], wf[SET][kk][fc], acc[fc][fp], 0, 0, 0)
+                             : __builtin_amdgcn_mfma_f32_16x16x32_f16(wf[SET][kk][fc], pf[SET][kk][fp], acc[fc][fp], 0, 0, 0);
     constexpr int NMF = 2 * FP * FC, NDS = 2 * (FP + FC);
     constexpr int A = NDS < NMF ? NDS : NMF;
 #pragma unroll

@@ -742,6 +742,37 @@ def test_conv3x3_halo_whole_image_tiles(C, H):
     assert rel(val(fused), ref) <= 1e-2
 
 
+@pytest.mark.parametrize("B,C,H,W,O", [(2, 320, 8, 8, 320), (2, 640, 4, 4, 640), (2, 960, 6, 6, 320),
+                                         (1, 1920, 4, 5, 640), (2, 320, 8, 8, 1280), (1, 640, 2, 6, 48)])
+def test_conv1x1_streamed_nchw(B, C, H, W, O, monkeypatch):
+    """fp16 1x1 convs of a channels-last activation with K a multiple of 320 take the streamed
+    kernel in its NCHW mode (the SD transformer's proj_out, the ResBlock shortcuts), through
+    conv2d_tokens (bias + residual, and no bias) and through conv2d on an NCHW input: checked
+    against the oracle on a strided subset of output channels, as is the implicit-GEMM path
+    (MTHIP_CONV_STREAM=0; its fp32 sums are grouped differently, so the two agree to rounding,
+    not bit for bit).  Covers partial 80-channel and 64-token tiles, images that split a token
+    tile (6x6), K splits with the conv reduction (K = 1920 over few pixels) and, forced, 1280
+    output channels."""
+    from mtorch_amd import _ops
+    g = Gen(B + C + H + W + O)
+    x = g.randn((B, C, H, W), "float16")
+    w = g.randn((O, C, 1, 1), "float16", 1.0 / np.sqrt(C))
+    b = g.randn((O,), "float16")
+    r = g.randn((B, O, H, W), "float16")
+    tok = np.ascontiguousarray(x.transpose(0, 2, 3, 1).reshape(B, H * W, C))
+    sel = np.unique(np.r_[np.arange(0, O, 7), O - 1])
+    ws, bs = np.ascontiguousarray(w[sel]), np.ascontiguousarray(b[sel])
+    refs = (orc.binary(orc.conv2d(x, ws, bs), np.ascontiguousarray(r[:, sel]), "add"), orc.conv2d(x, ws, None),
+            orc.conv2d(x, ws, bs))
+    for mode in ("2", "0"):
+        monkeypatch.setenv("MTHIP_CONV_STREAM", mode)
+        outs = (host(_ops.conv2d_tokens(dev(tok), dev(w), dev(b), H, W, residual=dev(r))),
+                host(_ops.conv2d_tokens(dev(tok), dev(w), None, H, W)), host(F.conv2d(dev(x), dev(w), dev(b))))
+        for got, ref in zip(outs, refs):
+            assert got.shape == (B, O, H, W)
+            assert rel(val(got[:, sel]), val(ref)) <= 1e-2
+
+
 @pytest.mark.parametrize("dt", ["float32", "float16"])
 @pytest.mark.parametrize("B,C,H,W,O,G", [(2, 64, 16, 16, 48, 32), (2, 40, 9, 7, 40, 8), (1, 16, 8, 8, 24, 4)])
 def test_group_norm_silu_conv2d_channel_add_is_the_separate_add(dt, B, C, H, W, O, G):
