@@ -530,6 +530,35 @@ __global__ void upsample_nearest_kernel(const T* __restrict__ x, T* __restrict__
   }
 }
 
+// 2x2 nearest upsampling with W % 4 == 0: a thread reads 4 consecutive inputs of one row and
+// writes the 8 outputs of each of the two output rows they cover (16-byte stores for fp16, two
+// for fp32).  Chunk index -> (plane row, chunk) by one 32-bit division (FastDiv).
+template <typename T>
+__global__ __launch_bounds__(256) void upsample2x_vec_kernel(const T* __restrict__ x, T* __restrict__ y,
+                                                             uint32_t rows, uint32_t W, FastDiv div_cw) {
+  const uint32_t cw = div_cw.d;  // chunks per input row
+  const uint32_t n = rows * cw;
+  for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
+    const uint32_t r = div_cw.div(i), c = i - r * cw;  // input row (plane * H + iy), chunk
+    const T* src = x + (size_t)r * W + 4 * c;
+    T* dst = y + (size_t)r * 4 * W + 8 * c;  // output row 2 * (plane * H + iy) = plane * 2H + 2iy
+    if constexpr (sizeof(T) == 2) {
+      const uint2 v = *reinterpret_cast<const uint2*>(src);
+      const uint32_t a = v.x & 0xffffu, b = v.x >> 16, cc = v.y & 0xffffu, d = v.y >> 16;
+      const uint4 o = make_uint4(a | (a << 16), b | (b << 16), cc | (cc << 16), d | (d << 16));
+      *reinterpret_cast<uint4*>(dst) = o;
+      *reinterpret_cast<uint4*>(dst + 2 * W) = o;
+    } else {
+      const uint4 v = *reinterpret_cast<const uint4*>(src);
+      const uint4 o0 = make_uint4(v.x, v.x, v.y, v.y), o1 = make_uint4(v.z, v.z, v.w, v.w);
+      *reinterpret_cast<uint4*>(dst) = o0;
+      *reinterpret_cast<uint4*>(dst + 4) = o1;
+      *reinterpret_cast<uint4*>(dst + 2 * W) = o0;
+      *reinterpret_cast<uint4*>(dst + 2 * W + 4) = o1;
+    }
+  }
+}
+
 int elem_size(int dtype) {
   switch (dtype) {
     case MTHIP_F16: return 2;
@@ -823,6 +852,20 @@ int mthip_upsample_nearest2d(int device, int dtype, const void* x, void* y, int6
   hipStream_t s = stream_for(device);
   if (!s) return MTHIP_ERR_HIP;
   if (int rc = use_device(device)) return rc;
+  const int64_t rows = planes * H;
+  if (scale_h == 2 && scale_w == 2 && W % 4 == 0 && rows * W < (int64_t(1) << 31) && ((uintptr_t)x & 15) == 0 &&
+      ((uintptr_t)y & 15) == 0) {
+    // the decoder's 2x upsampling: vectorised rows
+    const FastDiv div_cw((uint32_t)(W / 4));
+    const unsigned g = grid_for(rows * (W / 4));
+    if (es == 2)
+      hipLaunchKernelGGL(upsample2x_vec_kernel<uint16_t>, dim3(g), dim3(kThreads), 0, s, (const uint16_t*)x,
+                         (uint16_t*)y, (uint32_t)rows, (uint32_t)W, div_cw);
+    else
+      hipLaunchKernelGGL(upsample2x_vec_kernel<uint32_t>, dim3(g), dim3(kThreads), 0, s, (const uint32_t*)x,
+                         (uint32_t*)y, (uint32_t)rows, (uint32_t)W, div_cw);
+    return check_launch("mthip_upsample_nearest2d");
+  }
   if (es == 2)
     hipLaunchKernelGGL(upsample_nearest_kernel<uint16_t>, dim3(grid_for(n)), dim3(kThreads), 0, s, (const uint16_t*)x, (uint16_t*)y, planes, H, W, scale_h, scale_w);
   else

@@ -969,6 +969,17 @@ def test_cat_and_upsample():
     assert np.array_equal(got, a.repeat(2, axis=2).repeat(2, axis=3))
 
 
+@pytest.mark.parametrize("dt", ["float16", "float32"])
+@pytest.mark.parametrize("shape,scale", [((2, 640, 32, 32), 2), ((2, 1280, 8, 8), 2), ((1, 3, 5, 12), 2),
+                                         ((2, 4, 6, 8), 3), ((1, 2, 3, 5), 2)])
+def test_upsample_nearest_rows(dt, shape, scale):
+    """Nearest upsampling is a copy: bit-exact against numpy's repeat, at the SD decoder shapes
+    (2x, width a multiple of 4: the vectorised row kernel) and off them (odd widths, 3x)."""
+    a = Gen(sum(shape) + scale).randn(shape, dt)
+    got = host(F.interpolate(dev(a), scale_factor=scale, mode="nearest"))
+    assert np.array_equal(got, a.repeat(scale, axis=2).repeat(scale, axis=3))
+
+
 def test_graph_capture_replay_matches_eager():
     g = Gen(111)
     x = dev(g.randn((2, 32, 8, 8), "float16"))
