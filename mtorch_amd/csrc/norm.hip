@@ -10,7 +10,9 @@
 // form (tensor.cpp:18765-18767, 18822-18824) with fp32 tree sums.
 #include <hip/hip_runtime.h>
 
+#include <cstdlib>
 #include <mutex>
+#include <type_traits>
 
 #include <algorithm>
 
@@ -47,8 +49,8 @@ __device__ __forceinline__ float block_sum256(float v, float* scratch /* [4] */)
 template <typename T>
 struct Vec16 {
   static constexpr int N = 16 / sizeof(T);
-  static __device__ __forceinline__ void load(const T* p, float (&f)[N]) {
-    const uint4 r = *reinterpret_cast<const uint4*>(p);
+  static __device__ __forceinline__ void load(const T* p, float (&f)[N]) { unpack(*reinterpret_cast<const uint4*>(p), f); }
+  static __device__ __forceinline__ void unpack(const uint4 r, float (&f)[N]) {
     if constexpr (sizeof(T) == 2) {
       const uint32_t w[4] = {r.x, r.y, r.z, r.w};
 #pragma unroll
@@ -275,6 +277,116 @@ __global__ __launch_bounds__(256) void group_norm_apply_kernel(const T* __restri
       Elem<T>::store(yb, i, gn_value<T, P>(Elem<T>::load(xb, i), mean, inv, gm, bt, fuse_silu));
     }
   }
+}
+
+// GroupNorm in one pass over x for batches with many (sample, group) pairs (>= 2 per CU): a
+// 512-thread workgroup holds one whole group in registers, so x is read once (the two-kernel
+// path reads it twice).  Values are bit-identical to group_norm_stats_kernel +
+// group_norm_apply_kernel<T, P, true>: the two halves of the workgroup (threads t and t + 256)
+// take alternate stats chunks and replay that kernel's per-thread vectors (IPC vectors of V
+// elements per chunk, summed in order), wave butterflies and four-wave combine, and wave 0
+// folds the chunk partials as fold_group_stats does.  Needs NCHW, whole 16-byte vectors, at
+// most 2 * CPT chunks and chunk == IPC * 256 * V (all but possibly the last chunk full).  (fp16
+// holding more than 10 vectors per thread goes to scratch memory instead of registers.)
+template <typename T, typename P, int CPT, int IPC>
+__global__ __launch_bounds__(512) void group_norm_single_kernel(const T* __restrict__ x, const P* __restrict__ gamma,
+                                                                const P* __restrict__ beta, T* __restrict__ y,
+                                                                int64_t C, int64_t groups, int64_t inner,
+                                                                int64_t group_size, int64_t chunk, int splits,
+                                                                float eps, int fuse_silu, FastDiv div_inner) {
+  constexpr int V = Vec16<T>::N;
+  __shared__ float red_s[2 * CPT][4], red_ss[2 * CPT][4];
+  __shared__ float2 st_s;
+  const int64_t bg = blockIdx.x;
+  const int t = threadIdx.x & 255, half = threadIdx.x >> 8, wave = (threadIdx.x >> 6) & 3, lane = threadIdx.x & 63;
+  const T* xb = x + bg * group_size;
+  T* yb = y + bg * group_size;
+  uint4 d[CPT][IPC];
+  // phase 1: chunk k = 2 * kk + half of this thread's half; the stats kernel's thread t
+#pragma unroll
+  for (int kk = 0; kk < CPT; ++kk) {
+    const int k = 2 * kk + half;
+    const int64_t begin = (int64_t)k * chunk, end = min(begin + chunk, group_size);
+    float s = 0.0f, ss = 0.0f;
+#pragma unroll
+    for (int it = 0; it < IPC; ++it) {
+      const int64_t i = begin + (int64_t)(t + it * 256) * V;
+      d[kk][it] = make_uint4(0u, 0u, 0u, 0u);
+      if (k < splits && i < end) {
+        d[kk][it] = *reinterpret_cast<const uint4*>(xb + i);
+        float f[V];
+        Vec16<T>::unpack(d[kk][it], f);
+#pragma unroll
+        for (int j = 0; j < V; ++j) {
+          s += f[j];
+          ss += f[j] * f[j];
+        }
+      }
+    }
+    s = wave_sum(s);
+    ss = wave_sum(ss);
+    if (lane == 0 && k < splits) {
+      red_s[k][wave] = s;
+      red_ss[k][wave] = ss;
+    }
+  }
+  __syncthreads();
+  if (threadIdx.x < 64) {
+    // the chunk partials (stats kernel: red[0] + red[1] + red[2] + red[3]), folded as
+    // fold_group_stats folds them (splits <= 64: one per lane)
+    float s = 0.0f, ss = 0.0f;
+    if (lane < splits) {
+      s += red_s[lane][0] + red_s[lane][1] + red_s[lane][2] + red_s[lane][3];
+      ss += red_ss[lane][0] + red_ss[lane][1] + red_ss[lane][2] + red_ss[lane][3];
+    }
+    s = wave_sum(s);
+    ss = wave_sum(ss);
+    if (lane == 0) st_s = gn_stats(s, ss, (float)group_size, eps);
+  }
+  __syncthreads();
+  const float mean = st_s.x, inv = st_s.y;
+  const int64_t g = (uint32_t)bg % (uint32_t)groups;
+  const int64_t gc = (uint32_t)C / (uint32_t)groups;
+  // phase 2: group_norm_apply_kernel<T, P, true>'s arithmetic on the held vectors (the fused
+  // SiLU chosen outside the loop, which keeps each loop body small enough to unroll: the held
+  // vectors must stay in registers)
+  auto apply = [&](auto silu_c) {
+    constexpr bool SILU = decltype(silu_c)::value;
+#pragma unroll
+    for (int kk = 0; kk < CPT; ++kk) {
+      const int k = 2 * kk + half;
+      const int64_t begin = (int64_t)k * chunk, end = min(begin + chunk, group_size);
+#pragma unroll
+      for (int it = 0; it < IPC; ++it) {
+        const int64_t i = begin + (int64_t)(t + it * 256) * V;
+        if (k < splits && i < end) {
+          const int64_t c = g * gc + div_inner.div((uint32_t)i);
+          const float gm = gamma ? Elem<P>::load(gamma, c) : 1.0f;
+          const float bt = beta ? Elem<P>::load(beta, c) : 0.0f;
+          float f[V];
+          Vec16<T>::unpack(d[kk][it], f);
+          if constexpr (SILU && sizeof(T) == 2) {
+            uint32_t w[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              const uint32_t lo = silu_half(f2h_fast(gn_value<T, P>(f[2 * j], mean, inv, gm, bt, 0)));
+              const uint32_t hi = silu_half(f2h_fast(gn_value<T, P>(f[2 * j + 1], mean, inv, gm, bt, 0)));
+              w[j] = lo | (hi << 16);
+            }
+            *reinterpret_cast<uint4*>(yb + i) = make_uint4(w[0], w[1], w[2], w[3]);
+          } else {
+#pragma unroll
+            for (int j = 0; j < V; ++j) f[j] = gn_value<T, P>(f[j], mean, inv, gm, bt, SILU ? 1 : 0);
+            Vec16<T>::store(yb + i, f);
+          }
+        }
+      }
+    }
+  };
+  if (fuse_silu)
+    apply(std::true_type{});
+  else
+    apply(std::false_type{});
 }
 
 // Same values written channels-last: y[b][p][0..Cp) with channels C..Cp-1 zero, the layout the
@@ -799,6 +911,22 @@ __global__ __launch_bounds__(256) void softmax_long_kernel(const T* __restrict__
   }
 }
 
+int gn_cu_count(int device) {
+  static int cached[64] = {0};
+  if (device < 0 || device >= 64) return 256;
+  if (!cached[device]) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess || n < 1) n = 256;
+    cached[device] = n;
+  }
+  return cached[device];
+}
+
+bool gn_single_enabled() {
+  const char* e = std::getenv("MTHIP_GN_SINGLE");
+  return !(e && e[0] == '0');
+}
+
 // Stats (chunked partials), then the apply pass, which folds its group's partials: NCHW as x
 // (y_nhwc == false) or channels-last with Cp channels.
 // x1 (nullable): a second NCHW input of C - C0 channels concatenated after x's C0 channels
@@ -840,6 +968,32 @@ int run_group_norm(int device, const void* x, const void* weight, const void* bi
   } else {
     if (int rc = mthip_malloc(device, (size_t)(n_groups * splits) * sizeof(float2), &ws)) return rc;
     partial = static_cast<float2*>(ws);
+  }
+  // Many (sample, group) pairs, NCHW in and out: one pass over x (group_norm_single_kernel),
+  // bit-identical to the two kernels below.  MTHIP_GN_SINGLE=0 turns it off.
+  if constexpr (sizeof(T) == 2) if (!y_nhwc && vect && !x1 && !raw && !ws_given &&
+                                    n_groups >= 2 * (int64_t)gn_cu_count(device) && gn_single_enabled()) {
+    const int64_t per_iter = 256 * V;
+    const int ipc = (int)(chunk / per_iter);
+    // (the held vectors stay in registers up to 10 chunks per half: 20 chunks, e.g. a 10-channel
+    // 64x64 group; fp16 chunks are one vector per thread.  fp32, two vectors per chunk, measured
+    // slower than the two kernels: 361 -> 382 us at [128,320,64,64].)
+    if (chunk % per_iter == 0 && ipc == 1 && splits <= 20) {
+      const int cpt = (int)ceil_div(splits, 2);
+#define MTHIP_GN_SINGLE(CPT, IPC)                                                                                  \
+  hipLaunchKernelGGL((group_norm_single_kernel<T, P, CPT, IPC>), dim3((unsigned)n_groups), dim3(512), 0, s,        \
+                     (const T*)x, (const P*)weight, (const P*)bias, (T*)y, C, groups, inner, group_size, chunk,  \
+                     (int)splits, (float)eps, fuse_silu, FastDiv((uint32_t)inner))
+      constexpr int IPC = 1;
+      if (cpt <= 4)
+        MTHIP_GN_SINGLE(4, IPC);
+      else if (cpt <= 8)
+        MTHIP_GN_SINGLE(8, IPC);
+      else
+        MTHIP_GN_SINGLE(10, IPC);
+#undef MTHIP_GN_SINGLE
+      return check_launch("group_norm_single_kernel");
+    }
   }
   // The fp16 channels-last apply (the only one that reads two sources or writes `raw`).
   const bool nhwc_f16 = y_nhwc && sizeof(T) == 2 && ((uintptr_t)x % 16 == 0) && ((uintptr_t)y % 16 == 0) &&

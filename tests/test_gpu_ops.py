@@ -663,6 +663,38 @@ def test_group_norm(dt, shape, groups):
     assert rel(val(got), val(orc.silu(ref))) <= TOL[dt]
 
 
+@pytest.mark.parametrize("dt", ["float16", "float32"])
+@pytest.mark.parametrize("shape,groups", [((16, 320, 64, 64), 32), ((24, 320, 32, 32), 32), ((8, 64, 59, 104), 64),
+                                          ((40, 64, 9, 16), 16)])
+def test_group_norm_single_pass_large_batch(dt, shape, groups, monkeypatch):
+    """With >= 2 (sample, group) pairs per CU, NCHW GroupNorm runs in one pass (a workgroup holds
+    its whole group in registers): bit for bit the two-kernel result (MTHIP_GN_SINGLE=0), with
+    and without the fused SiLU, with fp16 or fp32 affine parameters, including a last stats chunk
+    shorter than the rest (one-channel groups of 59x104 pixels), and checked against the oracle on
+    a few samples.  (Groups of 9x16 pixels take the two-kernel path: chunks shorter than a
+    workgroup's vector sweep.)"""
+    from mtorch_amd import _ops
+    g = Gen(sum(shape) + groups)
+    x = g.randn(shape, dt)
+    C = shape[1]
+    w, b = g.randn((C,), dt), g.randn((C,), dt)
+    w32, b32 = g.randn((C,), "float32"), g.randn((C,), "float32")
+    runs = {}
+    for mode in ("1", "0"):
+        monkeypatch.setenv("MTHIP_GN_SINGLE", mode)
+        runs[mode] = [host(F.group_norm(dev(x), groups, dev(w), dev(b), 1e-5)),
+                      host(F.group_norm_silu(dev(x), groups, dev(w), dev(b), 1e-5)),
+                      host(F.group_norm(dev(x), groups, None, None, 1e-5))]
+        if dt == "float16":
+            runs[mode].append(host(_ops.group_norm(dev(x), groups, dev(w32), dev(b32), 1e-5, allow_upcast=True)))
+    for got, want in zip(runs["1"], runs["0"]):
+        assert np.array_equal(got, want)
+    xs = np.ascontiguousarray(x[::7])
+    ref = orc.group_norm(xs, groups, w, b, 1e-5)
+    assert rel(val(runs["1"][0][::7]), val(ref)) <= TOL[dt]
+    assert rel(val(runs["1"][1][::7]), val(orc.silu(ref))) <= TOL[dt]
+
+
 @pytest.mark.parametrize("dt", ["float32", "float16"])
 @pytest.mark.parametrize("B,C,H,W,O,G", [(2, 64, 16, 16, 48, 32), (1, 12, 9, 11, 8, 4), (2, 40, 8, 8, 40, 8)])
 def test_group_norm_silu_conv2d_channels_last_handoff(dt, B, C, H, W, O, G):
