@@ -22,10 +22,39 @@
 namespace mthip {
 namespace {
 
+// One level of the xor butterfly: v[lane] + v[lane ^ off], for off = 32, 16, 8, 4, 2, 1, with
+// the partner fetched by cross-lane VALU moves instead of an LDS permute (ds_bpermute): gfx950's
+// v_permlane32_swap / v_permlane16_swap (exchange half-waves / alternate 16-lane rows; the two
+// results hold v and its partner, whose sum is the same in either order), DPP row_ror:8 (within
+// 16 lanes a rotation by 8 is lane ^ 8), ds_swizzle's xor mode and DPP quad permutes.  The sums
+// are those of the shuffle loop, operand for operand.
+template <int OFF>
+__device__ __forceinline__ float xor_add(float v) {
+  const int b = __float_as_int(v);
+  if constexpr (OFF == 32) {
+    const auto r = __builtin_amdgcn_permlane32_swap((unsigned)b, (unsigned)b, false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  } else if constexpr (OFF == 16) {
+    const auto r = __builtin_amdgcn_permlane16_swap((unsigned)b, (unsigned)b, false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  } else if constexpr (OFF == 8) {
+    return v + __int_as_float(__builtin_amdgcn_update_dpp(0, b, 0x128, 0xf, 0xf, false));  // row_ror:8
+  } else if constexpr (OFF == 4) {
+    return v + __int_as_float(__builtin_amdgcn_ds_swizzle(b, 0x101f));  // xor_mask 4 within 32 lanes
+  } else if constexpr (OFF == 2) {
+    return v + __int_as_float(__builtin_amdgcn_update_dpp(0, b, 0x4e, 0xf, 0xf, false));  // quad_perm [2,3,0,1]
+  } else {
+    return v + __int_as_float(__builtin_amdgcn_update_dpp(0, b, 0xb1, 0xf, 0xf, false));  // quad_perm [1,0,3,2]
+  }
+}
+
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
-  return v;
+  v = xor_add<32>(v);
+  v = xor_add<16>(v);
+  v = xor_add<8>(v);
+  v = xor_add<4>(v);
+  v = xor_add<2>(v);
+  return xor_add<1>(v);
 }
 
 __device__ __forceinline__ float wave_max(float v) {
@@ -737,11 +766,8 @@ __global__ __launch_bounds__(256) void layer_norm_vec_kernel(const T* __restrict
       for (int j = 0; j < CPL; ++j)
 #pragma unroll
         for (int k = 0; k < V; ++k) ss += v[r][j][k] * v[r][j][k];
-#pragma unroll
-      for (int off = 32; off >= 1; off >>= 1) {
-        s += __shfl_xor(s, off, 64);
-        ss += __shfl_xor(ss, off, 64);
-      }
+      s = wave_sum(s);
+      ss = wave_sum(ss);
       mean = s / n;
       var = fmaxf(0.0f, ss / n - mean * mean);
     }
