@@ -129,6 +129,13 @@ int launch_halo(int device, HaloArgs h, hipStream_t s) {
   if (const char* f = std::getenv("MTHIP_CONV_HALO_KSPLIT")) ks = std::max(1, std::min(ncb, std::atoi(f)));
   h.cb_per_split = (int)ceil_div(ncb, ks);
   h.ksplit = (int)ceil_div(ncb, h.cb_per_split);
+  // Unit order: the images vary fastest (the two units that read one weight slice run side by
+  // side on one XCD) when a unit's weight slice is over twice its input patch, 9*BM rows against
+  // (TR+2)*(TW+2) (every SD shape but the 48-channel whole-image 16x16 units); graph-replayed:
+  // 8x8 1280->1280 19.2 -> 16.5 us, 64x64 and 32x32 2 % faster, 16x16 2 % slower, UNet 5.74 ->
+  // 5.71 ms.  MTHIP_CONV_HALO_IMGFAST=0/1 forces it.
+  h.img_fast = 9 * BM > 2 * (TR + 2) * (TW + 2) ? 1 : 0;
+  if (const char* f = std::getenv("MTHIP_CONV_HALO_IMGFAST")) h.img_fast = std::atoi(f) != 0;
   const int64_t units = base * h.ksplit;
   MTHIP_REQUIRE(units < (int64_t(1) << 31), "conv: too many units");
   h.units = (int)units;

@@ -55,6 +55,7 @@ struct HaloArgs {
   int chan_add_ld;
   int B, H, W, Cp, O;
   int tiles_m, row_blocks, ksplit, cb_per_split, units;
+  int img_fast;  // 1: the image index varies fastest in the unit order (units that share weights adjacent)
   int x_bytes, w_bytes;
   float* partial;  // ksplit > 1: [ksplit][O][ld_partial] fp32, columns = img*H*W + pixel
   int ld_partial;
@@ -183,12 +184,21 @@ __global__ __launch_bounds__(64 * (4 + NPW)) void conv3x3_halo_kernel(const Halo
   //      renumbered so each XCD (workgroups dealt round-robin) takes a contiguous range.
   const uint32_t U = (uint32_t)args.units, U8 = U / 8, u0 = blockIdx.x;
   const uint32_t q = u0 < 8 * U8 ? (u0 % 8) * U8 + u0 / 8 : u0;
-  const int mb = (int)(q % (uint32_t)args.tiles_m);
-  uint32_t rest = q / (uint32_t)args.tiles_m;
+  // Channel tiles fastest (neighbouring units share the input rows), or with img_fast the
+  // images (neighbouring units, on one XCD, share the weight slice: small images, where the
+  // weights outweigh the input patch)
+  uint32_t rest = q;
+  int img = 0;
+  if (args.img_fast) {
+    img = (int)(rest % (uint32_t)args.B);
+    rest /= (uint32_t)args.B;
+  }
+  const int mb = (int)(rest % (uint32_t)args.tiles_m);
+  rest /= (uint32_t)args.tiles_m;
   const int split = (int)(rest % (uint32_t)args.ksplit);
   rest /= (uint32_t)args.ksplit;
   const int rb = (int)(rest % (uint32_t)args.row_blocks);
-  const int img = (int)(rest / (uint32_t)args.row_blocks);
+  if (!args.img_fast) img = (int)(rest / (uint32_t)args.row_blocks);
   const int H = args.H, W = args.W, Cp = args.Cp, O = args.O;
   const int o0 = mb * BM, y0 = rb * TR;
   const int ncb_total = Cp / 64;
