@@ -363,6 +363,7 @@ namespace {
 void stream_plan(int64_t M, int64_t N, int64_t K, int64_t cus, int& best_bt, int64_t& best_ks) {
   const int64_t nk = K / 64, groups = nk / 5;
   const double step_us[2] = {0.40, 0.55}, epi_us = 0.4;
+  const double reduce_us = env_flag("MTHIP_GEMM_REDUCE_US", 3);  // fixed cost of a reduction launch
   const int force_bt = env_flag("MTHIP_GEMM_STREAM_BT", 64);
   best_bt = 64;
   best_ks = 1;
@@ -374,7 +375,7 @@ void stream_plan(int64_t M, int64_t N, int64_t K, int64_t cus, int& best_bt, int
       if (groups % ks) continue;
       const int64_t units = ceil_div(M, bt) * ceil_div(N, 80) * ks;
       double t = (double)ceil_div(units, cus) * ((double)(nk / ks) * step_us[bi] + epi_us);
-      if (ks > 1) t += 3.0 + (double)((ks + 1) * M * N * 4) / 3.0e6;
+      if (ks > 1) t += reduce_us + (double)((ks + 1) * M * N * 4) / 3.0e6;
       if (best == 0.0 || t < best) {
         best = t;
         best_bt = bt;
