@@ -309,32 +309,34 @@ __global__ __launch_bounds__(256) void group_norm_apply_kernel(const T* __restri
 }
 
 // GroupNorm in one pass over x for batches with many (sample, group) pairs (>= 2 per CU): a
-// 512-thread workgroup holds one whole group in registers, so x is read once (the two-kernel
+// 1024-thread workgroup holds one whole group in registers, so x is read once (the two-kernel
 // path reads it twice).  Values are bit-identical to group_norm_stats_kernel +
-// group_norm_apply_kernel<T, P, true>: the two halves of the workgroup (threads t and t + 256)
-// take alternate stats chunks and replay that kernel's per-thread vectors (IPC vectors of V
-// elements per chunk, summed in order), wave butterflies and four-wave combine, and wave 0
-// folds the chunk partials as fold_group_stats does.  Needs NCHW, whole 16-byte vectors, at
-// most 2 * CPT chunks and chunk == IPC * 256 * V (all but possibly the last chunk full).  (fp16
-// holding more than 10 vectors per thread goes to scratch memory instead of registers.)
+// group_norm_apply_kernel<T, P, true>: the four 256-thread parts of the workgroup take chunks
+// p, p + 4, ... and replay the stats kernel's per-thread vectors (IPC vectors of V elements per
+// chunk, summed in order), wave butterflies and four-wave combine, and wave 0 folds the chunk
+// partials as fold_group_stats does.  Needs NCHW, whole 16-byte vectors, at most 4 * CPT chunks
+// and chunk == IPC * 256 * V (all but possibly the last chunk full).  Four parts rather than two
+// halve each thread's serial reduce-and-store work between its loads and the next group's
+// (64x batch fp16: 200 -> 158 us); more than 10 fp16 vectors per thread would go to scratch.
 template <typename T, typename P, int CPT, int IPC>
-__global__ __launch_bounds__(512) void group_norm_single_kernel(const T* __restrict__ x, const P* __restrict__ gamma,
+__global__ __launch_bounds__(1024) void group_norm_single_kernel(const T* __restrict__ x, const P* __restrict__ gamma,
                                                                 const P* __restrict__ beta, T* __restrict__ y,
                                                                 int64_t C, int64_t groups, int64_t inner,
                                                                 int64_t group_size, int64_t chunk, int splits,
                                                                 float eps, int fuse_silu, FastDiv div_inner) {
   constexpr int V = Vec16<T>::N;
-  __shared__ float red_s[2 * CPT][4], red_ss[2 * CPT][4];
+  constexpr int NPART = 4;
+  __shared__ float red_s[NPART * CPT][4], red_ss[NPART * CPT][4];
   __shared__ float2 st_s;
   const int64_t bg = blockIdx.x;
-  const int t = threadIdx.x & 255, half = threadIdx.x >> 8, wave = (threadIdx.x >> 6) & 3, lane = threadIdx.x & 63;
+  const int t = threadIdx.x & 255, part = threadIdx.x >> 8, wave = (threadIdx.x >> 6) & 3, lane = threadIdx.x & 63;
   const T* xb = x + bg * group_size;
   T* yb = y + bg * group_size;
   uint4 d[CPT][IPC];
-  // phase 1: chunk k = 2 * kk + half of this thread's half; the stats kernel's thread t
+  // phase 1: chunk k = 4 * kk + part of this thread's part; the stats kernel's thread t
 #pragma unroll
   for (int kk = 0; kk < CPT; ++kk) {
-    const int k = 2 * kk + half;
+    const int k = NPART * kk + part;
     const int64_t begin = (int64_t)k * chunk, end = min(begin + chunk, group_size);
     float s = 0.0f, ss = 0.0f;
 #pragma unroll
@@ -383,7 +385,7 @@ __global__ __launch_bounds__(512) void group_norm_single_kernel(const T* __restr
     constexpr bool SILU = decltype(silu_c)::value;
 #pragma unroll
     for (int kk = 0; kk < CPT; ++kk) {
-      const int k = 2 * kk + half;
+      const int k = NPART * kk + part;
       const int64_t begin = (int64_t)k * chunk, end = min(begin + chunk, group_size);
 #pragma unroll
       for (int it = 0; it < IPC; ++it) {
@@ -1001,22 +1003,21 @@ int run_group_norm(int device, const void* x, const void* weight, const void* bi
                                     n_groups >= 2 * (int64_t)gn_cu_count(device) && gn_single_enabled()) {
     const int64_t per_iter = 256 * V;
     const int ipc = (int)(chunk / per_iter);
-    // (the held vectors stay in registers up to 10 chunks per half: 20 chunks, e.g. a 10-channel
-    // 64x64 group; fp16 chunks are one vector per thread.  fp32, two vectors per chunk, measured
-    // slower than the two kernels: 361 -> 382 us at [128,320,64,64].)
+    // (up to 20 chunks, five per thread, e.g. a 10-channel 64x64 group; fp16 chunks are one
+    // vector per thread.  fp32, two vectors per chunk, measured slower than the two kernels with
+    // two parts: 361 -> 382 us at [128,320,64,64].)
     if (chunk % per_iter == 0 && ipc == 1 && splits <= 20) {
-      const int cpt = (int)ceil_div(splits, 2);
-#define MTHIP_GN_SINGLE(CPT, IPC)                                                                                  \
-  hipLaunchKernelGGL((group_norm_single_kernel<T, P, CPT, IPC>), dim3((unsigned)n_groups), dim3(512), 0, s,        \
+      const int cpt = (int)ceil_div(splits, 4);
+#define MTHIP_GN_SINGLE(CPT)                                                                                       \
+  hipLaunchKernelGGL((group_norm_single_kernel<T, P, CPT, 1>), dim3((unsigned)n_groups), dim3(1024), 0, s,        \
                      (const T*)x, (const P*)weight, (const P*)bias, (T*)y, C, groups, inner, group_size, chunk,  \
                      (int)splits, (float)eps, fuse_silu, FastDiv((uint32_t)inner))
-      constexpr int IPC = 1;
-      if (cpt <= 4)
-        MTHIP_GN_SINGLE(4, IPC);
-      else if (cpt <= 8)
-        MTHIP_GN_SINGLE(8, IPC);
+      if (cpt <= 2)
+        MTHIP_GN_SINGLE(2);
+      else if (cpt <= 4)
+        MTHIP_GN_SINGLE(4);
       else
-        MTHIP_GN_SINGLE(10, IPC);
+        MTHIP_GN_SINGLE(5);
 #undef MTHIP_GN_SINGLE
       return check_launch("group_norm_single_kernel");
     }

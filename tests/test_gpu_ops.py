@@ -668,7 +668,8 @@ def test_group_norm(dt, shape, groups):
                                           ((40, 64, 9, 16), 16)])
 def test_group_norm_single_pass_large_batch(dt, shape, groups, monkeypatch):
     """With >= 2 (sample, group) pairs per CU, NCHW GroupNorm runs in one pass (a workgroup holds
-    its whole group in registers): bit for bit the two-kernel result (MTHIP_GN_SINGLE=0), with
+    its whole group in registers, four 256-thread parts replaying the stats kernel): bit for bit
+    the two-kernel result (MTHIP_GN_SINGLE=0), with
     and without the fused SiLU, with fp16 or fp32 affine parameters, including a last stats chunk
     shorter than the rest (one-channel groups of 59x104 pixels), and checked against the oracle on
     a few samples.  (Groups of 9x16 pixels take the two-kernel path: chunks shorter than a
