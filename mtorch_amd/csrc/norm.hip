@@ -999,17 +999,15 @@ int run_group_norm(int device, const void* x, const void* weight, const void* bi
   }
   // Many (sample, group) pairs, NCHW in and out: one pass over x (group_norm_single_kernel),
   // bit-identical to the two kernels below.  MTHIP_GN_SINGLE=0 turns it off.
-  if constexpr (sizeof(T) == 2) if (!y_nhwc && vect && !x1 && !raw && !ws_given &&
-                                    n_groups >= 2 * (int64_t)gn_cu_count(device) && gn_single_enabled()) {
-    const int64_t per_iter = 256 * V;
-    const int ipc = (int)(chunk / per_iter);
-    // (up to 20 chunks, five per thread, e.g. a 10-channel 64x64 group; fp16 chunks are one
-    // vector per thread.  fp32, two vectors per chunk, measured slower than the two kernels with
-    // two parts: 361 -> 382 us at [128,320,64,64].)
-    if (chunk % per_iter == 0 && ipc == 1 && splits <= 20) {
+  if (!y_nhwc && vect && !x1 && !raw && !ws_given && n_groups >= 2 * (int64_t)gn_cu_count(device) &&
+      gn_single_enabled()) {
+    // (up to 20 chunks, five per thread, e.g. a 10-channel 64x64 group; a chunk is one vector
+    // per thread in fp16, two in fp32)
+    constexpr int IPC = sizeof(T) == 2 ? 1 : 2;
+    if (chunk == (int64_t)IPC * 256 * V && splits <= 20) {
       const int cpt = (int)ceil_div(splits, 4);
 #define MTHIP_GN_SINGLE(CPT)                                                                                       \
-  hipLaunchKernelGGL((group_norm_single_kernel<T, P, CPT, 1>), dim3((unsigned)n_groups), dim3(1024), 0, s,        \
+  hipLaunchKernelGGL((group_norm_single_kernel<T, P, CPT, IPC>), dim3((unsigned)n_groups), dim3(1024), 0, s,      \
                      (const T*)x, (const P*)weight, (const P*)bias, (T*)y, C, groups, inner, group_size, chunk,  \
                      (int)splits, (float)eps, fuse_silu, FastDiv((uint32_t)inner))
       if (cpt <= 2)
