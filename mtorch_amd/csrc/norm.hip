@@ -206,11 +206,12 @@ __device__ __forceinline__ float2 fold_group_stats(const float2* __restrict__ pa
 // time, into st[k]; a wave takes groups k and k + 4 together so that both loads of partials are
 // in flight before either reduction (splits <= 64: one partial per lane).  The same sums, in the
 // same order, as fold_group_stats.
+template <int NWAVES = 4>
 __device__ __forceinline__ void fold_groups(const float2* __restrict__ partial, int64_t bg0, int ng, int splits,
                                             int64_t group_size, float eps, int wave, int lane, float2* st) {
   const float n = (float)group_size;
-  for (int k0 = wave; k0 < ng; k0 += 8) {
-    const int k1 = k0 + 4;
+  for (int k0 = wave; k0 < ng; k0 += 2 * NWAVES) {
+    const int k1 = k0 + NWAVES;
     float2 p0 = make_float2(0.0f, 0.0f), p1 = make_float2(0.0f, 0.0f);
     if (lane < splits) {
       p0 = partial[(bg0 + k0) * splits + lane];
@@ -548,17 +549,19 @@ const uint16_t* silu_f16_table(int device, hipStream_t s) {
 // The fused SiLU is a lookup of the narrowed normalised value (silu_f16_table).
 // raw (nullable) also receives the input itself channels-last, [B][HW][Cp]: the operand of a
 // 1x1 shortcut conv on the same (concatenated) input.
-template <typename P, bool CAT>
-__global__ __launch_bounds__(256) void group_norm_apply_nhwc_f16_kernel(
+template <typename P, bool CAT, int TPX = 64>
+__global__ __launch_bounds__(4 * TPX) void group_norm_apply_nhwc_f16_kernel(
     const GnSource<uint16_t> src, const P* __restrict__ gamma, const P* __restrict__ beta, uint16_t* __restrict__ y,
     uint16_t* __restrict__ raw, const float2* __restrict__ partial, int64_t C, int64_t Cp, int64_t groups, int64_t HW,
     int splits, float eps, const uint16_t* __restrict__ silu_tab) {
   constexpr int PW = 36;  // LDS words per pixel row: 64 channels + 8 pad (16-byte aligned rows)
-  __shared__ uint32_t tile[(CAT ? 2 : 1) * 64 * PW];
-  uint32_t* const raw_tile = tile + 64 * PW;  // CAT only
+  // TPX pixels x 64 channels per workgroup of 4 * TPX threads (TPX = 32 doubles the workgroups
+  // of the small latents)
+  __shared__ uint32_t tile[(CAT ? 2 : 1) * TPX * PW];
+  uint32_t* const raw_tile = tile + TPX * PW;  // CAT only
   __shared__ float2 st_s[64];
   const int64_t b = blockIdx.z;
-  const int64_t p0 = (int64_t)blockIdx.x * 64, c0 = (int64_t)blockIdx.y * 64;
+  const int64_t p0 = (int64_t)blockIdx.x * TPX, c0 = (int64_t)blockIdx.y * 64;
   const int t = threadIdx.x;
   const int cp = t & 31, po = t >> 5;  // channel pair, pixel octet
   const int64_t ca = c0 + 2 * cp;
@@ -590,7 +593,7 @@ __global__ __launch_bounds__(256) void group_norm_apply_nhwc_f16_kernel(
     // statistics of the (at most 64) groups this tile's channels belong to, one wave each
     const int64_t c_last = (c0 + 64 < C ? c0 + 64 : C) - 1;
     const int ng = c0 < C ? (int)((uint32_t)c_last / gc - g_first + 1) : 0;
-    fold_groups(partial, b * groups + g_first, ng, splits, (int64_t)gc * HW, eps, t >> 6, t & 63, st_s);
+    fold_groups<TPX / 16>(partial, b * groups + g_first, ng, splits, (int64_t)gc * HW, eps, t >> 6, t & 63, st_s);
   }
   __syncthreads();
   {
@@ -1052,15 +1055,30 @@ int run_group_norm(int device, const void* x, const void* weight, const void* bi
       // 16-byte row access: pixel rows and channel rows start on 16-byte boundaries.
       const int vec_io = ((uintptr_t)x % 16 == 0) && ((uintptr_t)y % 16 == 0) && inner % V == 0 && Cp % V == 0;
       const GnSource<uint16_t> src16{(const uint16_t*)x, (const uint16_t*)x1, C0, C - C0, C / groups, inner, groups};
-      if (nhwc_f16 && (cat || raw))
-        hipLaunchKernelGGL((group_norm_apply_nhwc_f16_kernel<P, true>), g2, dim3(256), 0, s, src16, (const P*)weight,
-                           (const P*)bias, (uint16_t*)y, (uint16_t*)raw, (const float2*)partial, C, Cp, groups, inner,
-                           (int)splits, (float)eps, silu_tab);
-      else if (nhwc_f16)
-        hipLaunchKernelGGL((group_norm_apply_nhwc_f16_kernel<P, false>), g2, dim3(256), 0, s, src16, (const P*)weight,
-                           (const P*)bias, (uint16_t*)y, (uint16_t*)nullptr, (const float2*)partial, C, Cp, groups,
-                           inner, (int)splits, (float)eps, silu_tab);
-      else
+      // 32-pixel tiles (128-thread workgroups) where 64-pixel tiles would leave fewer than two
+      // workgroups per CU (the 32x32, 16x16 and 8x8 latents); MTHIP_GN_TPX=32/64 forces one
+      int tpx = (int64_t)g2.x * g2.y * g2.z < 2 * (int64_t)gn_cu_count(device) ? 32 : 64;
+      if (const char* f = std::getenv("MTHIP_GN_TPX")) tpx = std::atoi(f) == 32 ? 32 : 64;
+      const dim3 g32((unsigned)ceil_div(inner, 32), g2.y, g2.z);
+      if (nhwc_f16 && (cat || raw)) {
+        if (tpx == 32)
+          hipLaunchKernelGGL((group_norm_apply_nhwc_f16_kernel<P, true, 32>), g32, dim3(128), 0, s, src16,
+                             (const P*)weight, (const P*)bias, (uint16_t*)y, (uint16_t*)raw, (const float2*)partial, C,
+                             Cp, groups, inner, (int)splits, (float)eps, silu_tab);
+        else
+          hipLaunchKernelGGL((group_norm_apply_nhwc_f16_kernel<P, true>), g2, dim3(256), 0, s, src16, (const P*)weight,
+                             (const P*)bias, (uint16_t*)y, (uint16_t*)raw, (const float2*)partial, C, Cp, groups,
+                             inner, (int)splits, (float)eps, silu_tab);
+      } else if (nhwc_f16) {
+        if (tpx == 32)
+          hipLaunchKernelGGL((group_norm_apply_nhwc_f16_kernel<P, false, 32>), g32, dim3(128), 0, s, src16,
+                             (const P*)weight, (const P*)bias, (uint16_t*)y, (uint16_t*)nullptr,
+                             (const float2*)partial, C, Cp, groups, inner, (int)splits, (float)eps, silu_tab);
+        else
+          hipLaunchKernelGGL((group_norm_apply_nhwc_f16_kernel<P, false>), g2, dim3(256), 0, s, src16, (const P*)weight,
+                             (const P*)bias, (uint16_t*)y, (uint16_t*)nullptr, (const float2*)partial, C, Cp, groups,
+                             inner, (int)splits, (float)eps, silu_tab);
+      } else
         hipLaunchKernelGGL((group_norm_apply_nhwc_kernel<T, P>), g2, dim3(256), 0, s, (const T*)x, (const P*)weight,
                            (const P*)bias, (T*)y, (const float2*)partial, C, Cp, groups, inner, (int)splits,
                            (float)eps, fuse_silu, vec_io);
