@@ -834,6 +834,17 @@ __global__ __launch_bounds__(256) void layer_norm_long_kernel(const T* __restric
 }
 
 // ------------------------------------------------------------------------------ softmax
+// e^d for d = x - max <= 0.  Half-width storage takes the native 2^x of d log2(e): its error
+// (about 1e-6 relative for every d that leaves a nonzero half) is far below a half ulp (5e-4),
+// and it costs a multiply and one transcendental where expf's range reduction costs eight more
+// operations per element, which made the 16-bit softmax VALU- rather than HBM-bound.  fp32
+// storage keeps expf.
+template <typename T>
+__device__ __forceinline__ float softmax_exp(float d) {
+  if constexpr (sizeof(T) == 2) return __builtin_amdgcn_exp2f(d * 1.44269504088896341f);
+  return expf(d);
+}
+
 template <typename T, int MAXV>
 __global__ __launch_bounds__(256) void softmax_kernel(const T* __restrict__ x, T* __restrict__ y, int64_t rows,
                                                       int64_t cols, int divide) {
@@ -854,7 +865,7 @@ __global__ __launch_bounds__(256) void softmax_kernel(const T* __restrict__ x, T
 #pragma unroll
   for (int j = 0; j < MAXV; ++j) {
     const int64_t i = lane + (int64_t)j * 64;
-    v[j] = i < cols ? expf(v[j] - mx) : 0.0f;
+    v[j] = i < cols ? softmax_exp<T>(v[j] - mx) : 0.0f;
     s += v[j];
   }
   s = wave_sum(s);
@@ -900,7 +911,7 @@ __global__ __launch_bounds__(256) void softmax_vec_kernel(const T* __restrict__ 
     const bool in = lane + 64 * j < chunks;
 #pragma unroll
     for (int q = 0; q < V; ++q) {
-      v[j][q] = in ? expf(v[j][q] - mx) : 0.0f;
+      v[j][q] = in ? softmax_exp<T>(v[j][q] - mx) : 0.0f;
       s += v[j][q];
     }
   }
@@ -932,12 +943,12 @@ __global__ __launch_bounds__(256) void softmax_long_kernel(const T* __restrict__
   __syncthreads();
   mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
   float s = 0.0f;
-  for (int64_t i = threadIdx.x; i < cols; i += 256) s += expf(Elem<T>::load(xr, i) - mx);
+  for (int64_t i = threadIdx.x; i < cols; i += 256) s += softmax_exp<T>(Elem<T>::load(xr, i) - mx);
   s = block_sum256(s, red);
   const float inv = 1.0f / s;
   T* yr = y + row * cols;
   for (int64_t i = threadIdx.x; i < cols; i += 256) {
-    const float e = expf(Elem<T>::load(xr, i) - mx);
+    const float e = softmax_exp<T>(Elem<T>::load(xr, i) - mx);
     Elem<T>::store(yr, i, divide ? e / s : e * inv);
   }
 }
