@@ -457,7 +457,7 @@ def run_suite(args):
         rows.append(_suite_row(f"softmax fp16 [{rws},{N}]", lambda: F.softmax(s, dim=-1), reps,
                                nbytes=2 * rws * N * 2, bound="hbm"))
         del s
-    for rws, C in ((8192, 320), (2048, 640), (8192 * 64, 320)):
+    for rws, C in ((8192, 320), (2048, 640), (512, 1280), (8192 * 64, 320)):
         t = rnd(rws, C)
         lw, lb = rnd(C), rnd(C)
         rows.append(_suite_row(f"layer_norm fp16 [{rws},{C}]", lambda: F.layer_norm(t, (C,), lw, lb, 1e-5), reps,
