@@ -938,6 +938,22 @@ def test_softmax(dt, shape):
     assert rel(val(got), val(orc.softmax_lastdim(x))) <= TOL[dt]
 
 
+@pytest.mark.parametrize("shape", [(64, 1024), (333, 77), (3, 5000)])
+def test_softmax_fp16_within_one_ulp(shape):
+    """The 16-bit softmax takes e^d as the native 2^(d log2 e): every output stays within one
+    fp16 ulp of the oracle's (tensor.cpp:15145-15221), on each of the three kernels -- rows of
+    whole 16-byte chunks in registers, short ragged rows, rows past 4096 columns."""
+    g = Gen(97 + shape[-1])
+    x = g.randn(shape, "float16", 4.0)
+    got = host(F.softmax(dev(x), dim=-1))
+    ref = orc.softmax_lastdim(x)
+    assert got.dtype == np.uint16 and ref.dtype == np.uint16
+    # outputs are >= +0, so the distance in ulps is the difference of the bit patterns
+    d = np.abs(got.astype(np.int32) - ref.astype(np.int32))
+    assert d.max() <= 1, (int(d.max()), int((d > 1).sum()))
+    assert (d == 0).mean() > 0.99
+
+
 @pytest.mark.parametrize("src,out", [("float32", "float16"), ("float16", "float32")])
 def test_softmax_with_another_output_dtype(src, out):
     """softmax(x, dtype=...) reads x at its own precision and narrows only the results
