@@ -57,16 +57,27 @@ __device__ __forceinline__ float gelu_tanh_f16(float xf) {
 // 2^x and reciprocal instead of expf and an IEEE divide.  The inputs where the native form's
 // result differs are pinned: x <= -60 (finite), where x e^x underflows to -0; +-0; 0xc173,
 // whose exact quotient lies within an fp32 ulp of an fp16 rounding tie; NaNs (the quieted
-// input, as x86 propagates it).
+// input, as x86 propagates it).  All but 0xc173 have |h| = 0 or |x| > 60 (and x > 60 keeps the
+// native result), so one unsigned compare finds them and a wave-uniform branch, taken only by
+// waves holding such an input, applies the pins.
 __device__ __forceinline__ uint16_t silu_half(uint16_t h) {
 #pragma clang fp contract(off)
   const float x = h2f_bits(h);
   const float e = __builtin_amdgcn_exp2f(-x * 1.44269504088896341f);
   uint32_t r = f2h_fast(x * __builtin_amdgcn_rcpf(1.0f + e));
-  if (x < -60.0f && h != 0xfc00u) r = 0x8000u;
-  if ((h & 0x7fffu) == 0u) r = h;
-  if (h == 0xc173u) r = 0xb15du;
-  if ((h & 0x7c00u) == 0x7c00u && (h & 0x3ffu) != 0u) r = h | 0x200u;
+  r = h == 0xc173u ? 0xb15du : r;
+  const uint32_t a = h & 0x7fffu;
+  const bool rare = a - 1u >= 0x5380u;  // a == 0 (wraps) or a >= 0x5381 (|x| > 60, inf, NaN)
+  if (__builtin_amdgcn_ballot_w64(rare)) {
+    if (rare) {
+      if (a == 0u)
+        r = h;  // +-0
+      else if (a > 0x7c00u)
+        r = h | 0x200u;  // NaN: the quieted input
+      else if ((h & 0x8000u) && h != 0xfc00u)
+        r = 0x8000u;  // finite x < -60: x e^x underflows to -0
+    }
+  }
   return (uint16_t)r;
 }
 
