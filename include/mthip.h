@@ -195,7 +195,9 @@ int mthip_linear(int device, int dtype, const void* x, int64_t lda, const void* 
  * b is [K,N]) or b^T (b_trans=1, b is [N,K]).  Strides in elements; batch strides may be 0
  * to broadcast.  c_in (may be NULL) is read with its own strides (broadcast allowed) and is
  * narrowed as narrow(beta*c_in) before alpha*product is added, as addmm does
- * (tensor.cpp:25253-25258, 25320-25334).  Serves matmul (tensor.cpp:24896-25064),
+ * (tensor.cpp:25253-25258, 25320-25334); it is read at beta = 0 too (0 * inf gives NaN there),
+ * and alpha = 0 skips the product, as the reference's loops do (tensor.cpp:25320, 25621).
+ * Serves matmul (tensor.cpp:24896-25064),
  * batched_matmul (:24822-24894), bmm (:25066) and addmm (:25184-25366). */
 /* The SD feed-forward's GEGLU input projection in one GEMM: for h = x . W^T + b with
  * W = [W_value; W_gate] ([2N, K]), y[M, N] = h[:, :N] * gelu(h[:, N:]) -- the reference's
@@ -265,13 +267,16 @@ enum { MTHIP_MASK_NONE = 0, MTHIP_MASK_BOOL = 1, MTHIP_MASK_ADD = 2 };
  * Hk divides H (H/Hk query heads share a key head: enable_gqa).  mask: MTHIP_MASK_BOOL
  * (uint8, false -> -inf) or MTHIP_MASK_ADD (mask_dtype F32 or the query dtype, added to the
  * scaled score), read through 4 strides {b, h, q, k} with 0 on broadcast axes.  is_causal
- * masks keys after the query.  scale <= 0 selects 1/sqrt(E).  q/k/v/o share dtype F16
- * (fp16 MFMA, fp32 softmax) or F32.  Fully-masked rows give NaN, as the reference does. */
+ * masks keys after the query.  has_scale = 0 selects 1/sqrt(E) (the reference's scale=None,
+ * tensor.cpp:31019); otherwise scale multiplies every score as given -- zero (softmax of the mask
+ * alone: the mean of V over the unmasked keys) and negative values included.  q/k/v/o share
+ * dtype F16 (fp16 MFMA, fp32 softmax) or F32.  Fully-masked rows give NaN, as the reference
+ * does. */
 int mthip_sdpa(int device, int dtype, const void* q, const int64_t* qs, const void* k,
                const int64_t* ks, const void* v, const int64_t* vs, void* o, const int64_t* os,
                int64_t B, int64_t H, int64_t Hk, int64_t Lq, int64_t Lk, int64_t E, int64_t Ev, int mask_kind,
                int mask_dtype, const void* mask, const int64_t* mask_strides, int is_causal,
-               double scale);
+               int has_scale, double scale);
 
 /* ===================================================================== normalisation */
 

@@ -73,7 +73,8 @@ _SIGNATURES = {
                                  _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _c_void_p,
                                  _c_void_p, _i64]),
     "mthip_sdpa": (_int, [_int, _int, _c_void_p, _i64p, _c_void_p, _i64p, _c_void_p, _i64p, _c_void_p, _i64p,
-                          _i64, _i64, _i64, _i64, _i64, _i64, _i64, _int, _int, _c_void_p, _i64p, _int, _dbl]),
+                          _i64, _i64, _i64, _i64, _i64, _i64, _i64, _int, _int, _c_void_p, _i64p, _int, _int,
+                          _dbl]),
     "mthip_group_norm": (_int, [_int, _int, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i64,
                                 _i64, _dbl, _int, _int]),
     "mthip_group_norm_noalloc": (_int, [_int, _int, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i64,

@@ -151,12 +151,25 @@ def contiguous_copy(t: Tensor) -> Tensor:
     return out
 
 
+def _last_writes(dst: Tensor, src: Tensor):
+    """The elements of dst that the reference's copy writes last.  Tensor::copy_from
+    (tensor.cpp:8335-8338) writes every index in row-major order, so along a zero-stride
+    (expanded) dimension of dst the last index wins; only that index of dst and of the
+    same-shaped src is kept.  (Expansion is the only way a view here overlaps itself.)"""
+    for d in range(dst.dim()):
+        if dst.stride(d) == 0 and dst.shape[d] > 1:
+            dst = dst.narrow(d, dst.shape[d] - 1, 1)
+            src = src.narrow(d, src.shape[d] - 1, 1)
+    return dst, src
+
+
 def copy_into(dst: Tensor, src: Tensor) -> None:
     """dst[...] = src with broadcasting and dtype conversion (Tensor::copy_from)."""
     if not isinstance(src, Tensor):
         fill_(dst, float(src))
         return
     src = src.expand(dst.shape) if list(src.shape) != list(dst.shape) else src
+    dst, src = _last_writes(dst, src)
     if dst.device.type == "cpu":
         vals = np.ascontiguousarray((src if src.device.type == "cpu" else src.cpu())._host_view())
         if src.dtype is not dst.dtype:
@@ -579,8 +592,9 @@ def addmm(inp: Tensor, m1: Tensor, m2: Tensor, beta=1.0, alpha=1.0) -> Tensor:
     e = inp.expand(M, N)
     out = _empty([M, N], m1.dtype, dev)
     if out.numel():
-        c_in = e if beta != 0.0 else None
-        _gemm(m1, m2, out, 1, M, N, K, 0, 0, alpha, beta, c_in, e.stride(0), e.stride(1), 0)
+        # beta * input is stored even at beta = 0 (an inf/NaN input gives NaN, tensor.cpp:25256);
+        # at alpha = 0 the library skips the product, as the reference does (tensor.cpp:25320).
+        _gemm(m1, m2, out, 1, M, N, K, 0, 0, alpha, beta, e, e.stride(0), e.stride(1), 0)
     return out
 
 
@@ -596,10 +610,10 @@ def baddbmm(inp: Tensor, b1: Tensor, b2: Tensor, beta=1.0, alpha=1.0) -> Tensor:
     e = inp.expand(B, M, N)
     out = _empty([B, M, N], b1.dtype, dev)
     if out.numel():
-        c_in = e if beta != 0.0 else None
+        # beta * input always stored (tensor.cpp:1452); product skipped at alpha = 0 (:25621).
         sa = _collapse_batch(b1, 1)
         sb = _collapse_batch(b2, 1)
-        _gemm(b1, b2, out, B, M, N, K, sa, sb, alpha, beta, c_in, e.stride(1), e.stride(2), e.stride(0))
+        _gemm(b1, b2, out, B, M, N, K, sa, sb, alpha, beta, e, e.stride(1), e.stride(2), e.stride(0))
     return out
 
 
@@ -954,11 +968,11 @@ def scaled_dot_product_attention(query: Tensor, key: Tensor, value: Tensor, attn
         mask_kind = 1 if m2.dtype is T.bool_ else 2
         mask_dt = m2.dtype.code
         mptr = m2.data_ptr()
-    sc = -1.0 if scale is None else float(scale)
     _lib.check(_L().mthip_sdpa(dev, query.dtype.code, q2.data_ptr(), _lib.int64_array(qs), k2.data_ptr(),
                                _lib.int64_array(ks), v2.data_ptr(), _lib.int64_array(vs), out.data_ptr(), None, B, H,
                                Hk, Lq, Lk, E, Ev, mask_kind, mask_dt, mptr, _lib.int64_array(ms) if ms else None,
-                               1 if is_causal else 0, sc))
+                               1 if is_causal else 0, 0 if scale is None else 1,
+                               0.0 if scale is None else float(scale)))
     return out
 
 

@@ -42,7 +42,7 @@ struct FlashArgs {
   const void* mask;
   int64_t ms[4];  // mask strides: b, h, q, k
   int causal;
-  float scale;
+  float scale;  // as given: zero and negative values multiply the scores like any other
   int cus;  // compute units of the device (launch-shape choices)
 };
 
@@ -121,7 +121,10 @@ void flash_fwd_f16_kernel(const FlashArgs a) {
   const uint16_t* K = reinterpret_cast<const uint16_t*>(a.k) + b * a.ks[0] + kvh * a.ks[1];
   const uint16_t* V = reinterpret_cast<const uint16_t*>(a.v) + b * a.vs[0] + kvh * a.vs[1];
 
-  // Q^T fragments (B operand of S^T): query q, dims step*16 + hh*8 + [0, 8).
+  // Q^T fragments (B operand of S^T): query q, dims step*16 + hh*8 + [0, 8).  A negative scale
+  // runs as softmax((-q) k^T |scale|): the sign goes into Q (an exact fp16 negation), so the
+  // scores stay in the "larger is heavier" order the running max relies on.
+  const uint32_t qneg = a.scale < 0.0f ? 0x80008000u : 0u;
   halfx8 qf[NSTEP];
 #pragma unroll
   for (int st = 0; st < NSTEP; ++st) {
@@ -129,12 +132,16 @@ void flash_fwd_f16_kernel(const FlashArgs a) {
     if constexpr (VEC) {
       uint4 r = make_uint4(0, 0, 0, 0);
       if (q < a.Lq && d0 < E) r = *reinterpret_cast<const uint4*>(Q + q * a.qs[2] + d0);
+      r.x ^= qneg;
+      r.y ^= qneg;
+      r.z ^= qneg;
+      r.w ^= qneg;
       qf[st] = __builtin_bit_cast(halfx8, r);
     } else {
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         uint16_t bits = 0;
-        if (q < a.Lq && d0 + j < E) bits = Q[q * a.qs[2] + d0 + j];
+        if (q < a.Lq && d0 + j < E) bits = Q[q * a.qs[2] + d0 + j] ^ (uint16_t)qneg;
         qf[st][j] = __builtin_bit_cast(_Float16, bits);
       }
     }
@@ -216,8 +223,7 @@ void flash_fwd_f16_kernel(const FlashArgs a) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[i][r] = 0.0f;
   float m_run = -INFINITY, l_run = 0.0f;
-  const float sl2 = a.scale * kLog2e;
-  const float inv_scale = 1.0f / a.scale;
+  const float sl2 = fabsf(a.scale) * kLog2e;  // >= 0; the sign went into Q
   const bool qok = q < a.Lq;
   const int mask_kind = MASK >= 0 ? MASK : a.mask_kind;
   // This lane's mask row (query q of head `head`), addressed per key by one 32-bit multiply.
@@ -245,7 +251,9 @@ void flash_fwd_f16_kernel(const FlashArgs a) {
     if (kv0 + KG * BKV < Lk) fetch(kv0 + KG * BKV);  // next tile's loads overlap this tile's math
     if (KG > 1 && kv0 >= Lk) continue;  // a key group past the last tile only keeps the barriers
 
-    // Raw scores (unscaled; an additive mask enters divided by the scale) and their max.
+    // Scores and their max: raw (unscaled) on tiles with every key valid and unmasked, scaled to
+    // log2 units on the others, so that an additive mask enters as given whatever the scale
+    // (zero included).  mult takes either to log2 units below.
     float s[2][16];
     float mx = -INFINITY;
     const bool checked = kv0 + BKV > Lk || a.causal || mask_kind != MTHIP_MASK_NONE;
@@ -269,7 +277,7 @@ void flash_fwd_f16_kernel(const FlashArgs a) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int key = kv0 + sb * 32 + 8 * (r >> 2) + 4 * hh + (r & 3);
-          float v = t[r];
+          float v = t[r] * sl2;
           if (key >= Lk) {
             v = -INFINITY;
           } else {
@@ -277,7 +285,7 @@ void flash_fwd_f16_kernel(const FlashArgs a) {
             if (mask_kind == MTHIP_MASK_BOOL) {
               if (qok && !mrow_b[key * mk]) v = -INFINITY;
             } else if (mask_kind == MTHIP_MASK_ADD && qok) {
-              v += (mrow_h ? h2f_bits(mrow_h[key * mk]) : mrow_f[key * mk]) * inv_scale;
+              v = fmaf(mrow_h ? h2f_bits(mrow_h[key * mk]) : mrow_f[key * mk], kLog2e, v);
             }
           }
           s[sb][r] = v;
@@ -289,7 +297,8 @@ void flash_fwd_f16_kernel(const FlashArgs a) {
     // Lazy rescaling: the running max (log2 units) moves only when a score exceeds it by more
     // than 8, so P <= 2^8 (exact in fp16 and in the fp32 sums) and most tiles skip the
     // accumulator rescale.  O = acc / l is unchanged by the choice of reference max.
-    const float m_cand = fmaxf(m_run, mx * sl2);
+    const float mult = checked ? 1.0f : sl2;
+    const float m_cand = fmaxf(m_run, mx * mult);
     if (m_cand > m_run + 8.0f) {
       const float alpha = __builtin_amdgcn_exp2f(m_run - m_cand);  // 0 when m_run = -inf
       l_run *= alpha;
@@ -304,14 +313,14 @@ void flash_fwd_f16_kernel(const FlashArgs a) {
 #pragma unroll
       for (int sb = 0; sb < 2; ++sb)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) s[sb][r] = __builtin_amdgcn_exp2f(fmaf(s[sb][r], sl2, -m_use));
+        for (int r = 0; r < 16; ++r) s[sb][r] = __builtin_amdgcn_exp2f(fmaf(s[sb][r], mult, -m_use));
     } else {
       float psum = 0.0f;
 #pragma unroll
       for (int sb = 0; sb < 2; ++sb)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          s[sb][r] = __builtin_amdgcn_exp2f(fmaf(s[sb][r], sl2, -m_use));
+          s[sb][r] = __builtin_amdgcn_exp2f(fmaf(s[sb][r], mult, -m_use));
           psum += s[sb][r];
         }
       psum += __shfl_xor(psum, 32, 64);
@@ -558,7 +567,7 @@ extern "C" int mthip_sdpa(int device, int dtype, const void* q, const int64_t* q
                           const void* v, const int64_t* vs, void* o, const int64_t* os, int64_t B, int64_t H,
                           int64_t Hk, int64_t Lq,
                           int64_t Lk, int64_t E, int64_t Ev, int mask_kind, int mask_dtype, const void* mask,
-                          const int64_t* mask_strides, int is_causal, double scale) {
+                          const int64_t* mask_strides, int is_causal, int has_scale, double scale) {
   MTHIP_REQUIRE(dtype == MTHIP_F16 || dtype == MTHIP_F32, "mthip_sdpa: dtype must be F16 or F32");
   MTHIP_REQUIRE(B >= 0 && H > 0 && Hk > 0 && H % Hk == 0, "mthip_sdpa: key heads must divide query heads");
   MTHIP_REQUIRE(Lq >= 0 && Lk >= 0 && E > 0 && Ev > 0, "mthip_sdpa: bad extents");
@@ -611,12 +620,15 @@ extern "C" int mthip_sdpa(int device, int dtype, const void* q, const int64_t* q
   if (mask_kind != MTHIP_MASK_NONE)
     for (int i = 0; i < 4; ++i) a.ms[i] = mask_strides[i];
   a.causal = is_causal;
-  a.scale = (float)(scale > 0.0 ? scale : 1.0 / std::sqrt((double)E));
+  // scale=None is 1/sqrt(E); a given scale is used as is (tensor.cpp:31019, 31182).
+  a.scale = (float)(has_scale ? scale : 1.0 / std::sqrt((double)E));
   const int64_t bh = B * H;
   const int64_t dmax = std::max(E, Ev);
   // One head's K and V must be addressable by 32-bit buffer offsets.
   const bool small_heads = ((Lk > 0 ? Lk - 1 : 0) * std::max(ks[2], vs[2]) + dmax) * 2 < (int64_t(1) << 31);
-  if (dtype == MTHIP_F16 && Lk > 0 && dmax <= 160 && small_heads) {
+  // The flash kernel needs a finite scale (its running max works in scaled units); an infinite
+  // or NaN one takes the row-wise kernel, which multiplies each score by it as the reference does.
+  if (dtype == MTHIP_F16 && Lk > 0 && dmax <= 160 && small_heads && std::isfinite(a.scale)) {
     const bool vec = E % 8 == 0 && Ev % 8 == 0 && qs[2] % 8 == 0 && ks[2] % 8 == 0 && vs[2] % 8 == 0 &&
                      qs[0] % 8 == 0 && qs[1] % 8 == 0 && ks[0] % 8 == 0 && ks[1] % 8 == 0 && vs[0] % 8 == 0 &&
                      vs[1] % 8 == 0 && a.os[0] % 8 == 0 && a.os[1] % 8 == 0 && a.os[2] % 8 == 0 &&

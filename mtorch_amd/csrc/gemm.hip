@@ -482,6 +482,25 @@ int try_stream_conv1x1(int device, const void* x_nhwc, const void* wp, const voi
   return launch_stream<true>(device, sa, r, Cp, s);
 }
 
+namespace {
+
+// c = narrow(beta * c_in) (0 without c_in): addmm / baddbmm at alpha = 0, where the reference
+// skips the product (tensor.cpp:25320, 25621), so an inf or NaN in the operands never reaches the
+// output while one in c_in does (0 * inf = NaN even at beta = 0, tensor.cpp:25256).
+template <typename T>
+__global__ __launch_bounds__(256) void gemm_beta_only_kernel(const GemmArgs a, int64_t batch) {
+  const int64_t total = batch * a.M * a.N;
+  const T* cin = reinterpret_cast<const T*>(a.c_in);
+  T* c = reinterpret_cast<T*>(a.c);
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
+    const int64_t col = i % a.N, t = i / a.N, row = t % a.M, bz = t / a.M;
+    const float v = cin ? a.beta * Elem<T>::load(cin, bz * a.stride_c_in + row * a.c_in_rs + col * a.c_in_cs) : 0.0f;
+    Elem<T>::store(c, bz * a.stride_c + row * a.ldc + col, v);
+  }
+}
+
+}  // namespace
+
 }  // namespace mthip
 
 using namespace mthip;
@@ -662,6 +681,15 @@ int mthip_gemm(int device, int dtype, int64_t batch, int64_t M, int64_t N, int64
   a.c_in_rs = c_in_rs;
   a.c_in_cs = c_in_cs;
   a.stride_c_in = stride_c_in;
+  if (alpha == 0.0) {
+    const int64_t total = batch * M * N;
+    const unsigned grid = (unsigned)std::min<int64_t>(ceil_div(total, 256), 4096);
+    if (dtype == MTHIP_F16)
+      hipLaunchKernelGGL(gemm_beta_only_kernel<uint16_t>, dim3(grid), dim3(256), 0, s, a, batch);
+    else
+      hipLaunchKernelGGL(gemm_beta_only_kernel<float>, dim3(grid), dim3(256), 0, s, a, batch);
+    return check_launch("gemm_beta_only_kernel");
+  }
   const int vec = dtype == MTHIP_F16 ? 8 : 4;
   const int64_t es = dtype == MTHIP_F16 ? 2 : 4;
   const int64_t b_cols = b_trans ? K : N;   // contiguous extent of a B row

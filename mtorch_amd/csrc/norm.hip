@@ -1000,21 +1000,10 @@ int run_group_norm(int device, const void* x, const void* weight, const void* bi
   int64_t chunk = ceil_div(group_size, splits);
   if (vect) chunk = ceil_div(chunk, V) * V;
   splits = ceil_div(group_size, chunk);
-  void* ws = nullptr;
-  float2* partial = ws_given;
-  if (ws_given) {
-    if (n_groups * splits > ws_capacity)
-      return fail(MTHIP_ERR_UNSUPPORTED, "mthip_group_norm_noalloc: batch*groups*chunks = " +
-                                             std::to_string(n_groups * splits) + " partial sums exceed the scratch of " +
-                                             std::to_string(ws_capacity));
-  } else {
-    if (int rc = mthip_malloc(device, (size_t)(n_groups * splits) * sizeof(float2), &ws)) return rc;
-    partial = static_cast<float2*>(ws);
-  }
   // Many (sample, group) pairs, NCHW in and out: one pass over x (group_norm_single_kernel),
-  // bit-identical to the two kernels below.  MTHIP_GN_SINGLE=0 turns it off.
-  if (!y_nhwc && vect && !x1 && !raw && !ws_given && n_groups >= 2 * (int64_t)gn_cu_count(device) &&
-      gn_single_enabled()) {
+  // bit-identical to the two kernels below and without their partials buffer.  MTHIP_GN_SINGLE=0
+  // turns it off.
+  if (!y_nhwc && vect && !x1 && !raw && n_groups >= 2 * (int64_t)gn_cu_count(device) && gn_single_enabled()) {
     // (up to 20 chunks, five per thread, e.g. a 10-channel 64x64 group; a chunk is one vector
     // per thread in fp16, two in fp32)
     constexpr int IPC = sizeof(T) == 2 ? 1 : 2;
@@ -1038,9 +1027,19 @@ int run_group_norm(int device, const void* x, const void* weight, const void* bi
   const bool nhwc_f16 = y_nhwc && sizeof(T) == 2 && ((uintptr_t)x % 16 == 0) && ((uintptr_t)y % 16 == 0) &&
                         inner % V == 0 && Cp % V == 0 && ((uintptr_t)x1 % 16 == 0) && ((uintptr_t)raw % 16 == 0) &&
                         C0 % 2 == 0;
-  if ((x1 || raw) && !nhwc_f16) {
-    mthip_free(device, ws);
+  if ((x1 || raw) && !nhwc_f16)
     return fail(MTHIP_ERR_UNSUPPORTED, "mthip_group_norm_nhwc_cat: needs fp16, 16-byte aligned rows and an even split");
+  // The two-kernel path's per-chunk partial sums: a caching-allocator block, or the caller's scratch.
+  void* ws = nullptr;
+  float2* partial = ws_given;
+  if (ws_given) {
+    if (n_groups * splits > ws_capacity)
+      return fail(MTHIP_ERR_UNSUPPORTED, "mthip_group_norm_noalloc: batch*groups*chunks = " +
+                                             std::to_string(n_groups * splits) + " partial sums exceed the scratch of " +
+                                             std::to_string(ws_capacity));
+  } else {
+    if (int rc = mthip_malloc(device, (size_t)(n_groups * splits) * sizeof(float2), &ws)) return rc;
+    partial = static_cast<float2*>(ws);
   }
   dim3 grid((unsigned)splits, (unsigned)n_groups);
   const bool cat = x1 != nullptr;

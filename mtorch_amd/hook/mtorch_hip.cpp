@@ -631,8 +631,7 @@ TensorPtr addmm(const TensorPtr& input, const TensorPtr& mat1, const TensorPtr& 
   auto e = broadcast_view(input, {M, N});
   auto out = empty({M, N}, mat1->dtype, mat1->device);
   if (out->numel() != 0) {
-    gemm(mat1, mat2, *out, 1, M, N, K, 0, 0, alpha, beta, beta != 0.0 ? e : nullptr, e->strides[0], e->strides[1],
-         0);
+    gemm(mat1, mat2, *out, 1, M, N, K, 0, 0, alpha, beta, e, e->strides[0], e->strides[1], 0);
   }
   return out;
 }
@@ -657,8 +656,7 @@ TensorPtr baddbmm(const TensorPtr& input, const TensorPtr& batch1, const TensorP
     int64_t sa = 0, sb = 0;
     collapse_batch(*batch1, 1, sa);
     collapse_batch(*batch2, 1, sb);
-    gemm(batch1, batch2, *out, B, M, N, K, sa, sb, alpha, beta, beta != 0.0 ? e : nullptr, e->strides[1],
-         e->strides[2], e->strides[0]);
+    gemm(batch1, batch2, *out, B, M, N, K, sa, sb, alpha, beta, e, e->strides[1], e->strides[2], e->strides[0]);
   }
   return out;
 }
@@ -813,7 +811,7 @@ TensorPtr scaled_dot_product_attention(const TensorPtr& query, const TensorPtr& 
   }
   check(mthip_sdpa(d, code(query->dtype), data(*q), qs.data(), data(*k), ks.data(), data(*v), vs.data(), data(*out),
                    nullptr, B, H, Hk, Lq, Lk, E, Ev, mask_kind, mask_dtype, m ? data(*m) : nullptr,
-                   m ? ms.data() : nullptr, is_causal ? 1 : 0, scale ? *scale : -1.0));
+                   m ? ms.data() : nullptr, is_causal ? 1 : 0, scale ? 1 : 0, scale ? *scale : 0.0));
   return out;
 }
 

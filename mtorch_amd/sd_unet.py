@@ -113,7 +113,7 @@ def _attention_tokens(q: Tensor, k: Tensor, v: Tensor, heads: int) -> Tensor:
     _lib.check(_lib.lib().mthip_sdpa(dev, q.dtype.code, q.data_ptr(), a([q.stride(0), D, q.stride(1)]), k.data_ptr(),
                                      a([k.stride(0), D, k.stride(1)]), v.data_ptr(), a([v.stride(0), D, v.stride(1)]),
                                      out.data_ptr(), a([Lq * C, D, C]), B, heads, heads, Lq, Lk, D, D, 0,
-                                     _lib.F32, None, None, 0, -1.0))
+                                     _lib.F32, None, None, 0, 0, 0.0))
     return out
 
 

@@ -58,7 +58,7 @@ def lib():
         L.orc_conv2d.argtypes = [i32, vp, vp, vp, vp] + [i64] * 14
         L.orc_conv2d_out_size.restype = i64
         L.orc_conv2d_out_size.argtypes = [i64] * 5
-        L.orc_sdpa.argtypes = [i32, vp, vp, vp, vp, i64, i64, i64, i64, i64, i32, vp, i32, dbl]
+        L.orc_sdpa.argtypes = [i32, vp, vp, vp, vp, i64, i64, i64, i64, i64, i32, vp, i32, i32, dbl]
         L.orc_group_norm.argtypes = [i32, vp, vp, vp, vp, i64, i64, i64, i64, dbl]
         L.orc_layer_norm.argtypes = [i32, vp, vp, vp, vp, i64, i64, dbl]
         L.orc_softmax_lastdim.argtypes = [i32, vp, vp, i64, i64, i32]
@@ -216,7 +216,8 @@ def conv2d(x, w, b=None, stride=1, padding=0, dilation=1, groups=1):
 
 def sdpa(q, k, v, mask=None, is_causal=False, scale=None):
     """q[..., Lq, E], k[..., Lk, E], v[..., Lk, Ev]; mask broadcastable to [..., Lq, Lk]
-    (bool -> keep where True; float32 -> added)."""
+    (bool -> keep where True; float32 -> added).  scale=None is 1/sqrt(E); any other value,
+    zero and negative ones included, multiplies the scores as given (tensor.cpp:31019)."""
     q, k, v = _c(q), _c(k), _c(v)
     lead = q.shape[:-2]
     P = int(np.prod(lead)) if lead else 1
@@ -234,7 +235,7 @@ def sdpa(q, k, v, mask=None, is_causal=False, scale=None):
             kind = 2
         mp = m
     lib().orc_sdpa(_dt(q), _p(q), _p(k), _p(v), _p(o), P, Lq, Lk, E, Ev, kind, _p(mp), 1 if is_causal else 0,
-                   -1.0 if scale is None else float(scale))
+                   0 if scale is None else 1, 0.0 if scale is None else float(scale))
     return o
 
 

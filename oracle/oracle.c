@@ -333,11 +333,13 @@ static void softmax_scores(double* s, int64_t n) {
 
 /* Generic SDPA loop (tensor.cpp:31158-31207).  fp16 q/k/v are widened to fp32 exactly, the
  * output is computed as fp32 and then narrowed with f2h (tensor.cpp:30969-30982), which equals
- * storing f2h((float)total).  std::max on doubles with -inf start keeps NaN-free rows exact. */
+ * storing f2h((float)total).  std::max on doubles with -inf start keeps NaN-free rows exact.
+ * has_scale = 0 is the reference's scale=None (1/sqrt(E)); any given scale, zero and negative
+ * ones included, multiplies the score as given (tensor.cpp:31019, 31182). */
 int orc_sdpa(int dtype, const void* q, const void* k, const void* v, void* o,
              int64_t P, int64_t Lq, int64_t Lk, int64_t E, int64_t Ev,
-             int mask_kind, const void* mask, int is_causal, double scale) {
-  const double s = scale > 0.0 ? scale : 1.0 / sqrt((double)E);
+             int mask_kind, const void* mask, int is_causal, int has_scale, double scale) {
+  const double s = has_scale ? scale : 1.0 / sqrt((double)E);
   double* scores = (double*)malloc(sizeof(double) * (size_t)(Lk > 0 ? Lk : 1));
   if (!scores) return -1;
   for (int64_t p = 0; p < P; ++p) {
@@ -390,7 +392,7 @@ int orc_group_norm(int dtype, const void* x, const void* weight, const void* bia
       const int64_t base = (n * C + g * gc_count) * inner;
       if (dtype == ORC_F16)
         orc_h2f_array((const uint16_t*)x + base, vals, group_size);
-      else
+      else if (group_size > 0)
         memcpy(vals, (const float*)x + base, sizeof(float) * (size_t)group_size);
       /* Sequential fp32 sum and sum of squares, one-pass variance
        * (tensor.cpp:18752-18767 fp16, :18812-18824 fp32). */

@@ -78,10 +78,11 @@ int64_t orc_conv2d_out_size(int64_t in, int64_t k, int64_t stride, int64_t pad, 
 
 /* ---- scaled_dot_product_attention: generic path tensor.cpp:31158-31207; fp16 casts :30969-30982.
  * q[P,Lq,E], k[P,Lk,E], v[P,Lk,Ev] -> o[P,Lq,Ev].  mask_kind: 0 none, 1 bool (uint8), 2 additive
- * (float32); the mask is a dense [P,Lq,Lk] expansion.  scale <= 0 selects 1/sqrt(E). */
+ * (float32); the mask is a dense [P,Lq,Lk] expansion.  has_scale = 0 selects 1/sqrt(E) (the
+ * reference's scale=None); otherwise scale multiplies the scores as given, zero and negative too. */
 int orc_sdpa(int dtype, const void* q, const void* k, const void* v, void* o,
              int64_t P, int64_t Lq, int64_t Lk, int64_t E, int64_t Ev,
-             int mask_kind, const void* mask, int is_causal, double scale);
+             int mask_kind, const void* mask, int is_causal, int has_scale, double scale);
 
 /* ---- group_norm on contiguous input: fp32 tensor.cpp:18797-18841; fp16 :18734-18783.
  * x[B, C, inner]; weight/bias [C] or NULL. */

@@ -417,6 +417,38 @@ def test_addmm_and_baddbmm(dt):
     assert rel(val(got), val(ref)) <= TOL[dt]
 
 
+@pytest.mark.parametrize("dt", ["float32", "float16"])
+def test_addmm_and_baddbmm_non_finite_beta0_alpha0(dt):
+    """The Linux path's semantics at beta = 0 and alpha = 0 (tensor.cpp:25253-25258, 25320,
+    1452, 25621): beta*input is stored even at beta = 0, so an inf/NaN input element gives NaN;
+    alpha = 0 skips the product, so NaN/inf operands leave exactly beta*input (bit for bit)."""
+    g = Gen(34)
+    inp = g.randn((25, 40), dt)
+    bits = 0x7C00 if dt == "float16" else np.float32(np.inf)
+    nanb = 0x7E00 if dt == "float16" else np.float32(np.nan)
+    inp[3, 5], inp[7, 0] = bits, nanb
+    m1 = g.randn((25, 30), dt)
+    m2 = g.randn((30, 40), dt)
+    got = host(mt.addmm(dev(inp), dev(m1), dev(m2), beta=0.0, alpha=1.5))
+    ref = orc.addmm(inp, m1, m2, 0.0, 1.5)
+    assert rel(val(got), val(ref)) <= TOL[dt]
+    assert np.isnan(val(got)[3, 5]) and np.isnan(val(got)[7, 0])
+    m1n = m1.copy()
+    m1n[0, 0], m1n[10, 29] = nanb, bits
+    got = host(mt.addmm(dev(inp), dev(m1n), dev(m2), beta=0.75, alpha=0.0))
+    assert np.array_equal(val(got), val(orc.addmm(inp, m1n, m2, 0.75, 0.0)), equal_nan=True)
+    bi = np.stack([inp] * 3)
+    b1 = np.stack([m1n] * 3)
+    b2 = np.stack([m2] * 3)
+    got = host(mt.baddbmm(dev(bi), dev(b1), dev(b2), beta=0.75, alpha=0.0))
+    want = orc.addmm(inp, m1n, m2, 0.75, 0.0)
+    for i in range(3):
+        assert np.array_equal(val(got[i]), val(want), equal_nan=True)
+    got = host(mt.baddbmm(dev(bi), dev(np.stack([m1] * 3)), dev(b2), beta=0.0, alpha=1.0))
+    assert np.isnan(val(got)[:, 3, 5]).all() and np.isnan(val(got)[:, 7, 0]).all()
+    assert rel(val(got[1]), val(orc.addmm(inp, m1, m2, 0.0, 1.0))) <= TOL[dt]
+
+
 CONV_CASES = [
     dict(B=2, C=32, H=16, W=16, O=48, k=3, stride=1, padding=1, dilation=1, groups=1),
     dict(B=1, C=40, H=15, W=13, O=24, k=3, stride=2, padding=1, dilation=1, groups=1),
@@ -600,6 +632,34 @@ def test_sdpa_masks_causal_scale(dt):
         assert rel(val(got), val(ref)) <= TOL[dt], c
 
 
+@pytest.mark.parametrize("dt,E,Lk", [("float16", 40, 1100), ("float16", 40, 77), ("float16", 80, 150),
+                                     ("float16", 160, 90), ("float32", 40, 90), ("float32", 160, 77)])
+def test_sdpa_explicit_scale(dt, E, Lk):
+    """An explicit scale is used as given (tensor.cpp:31019, 31182): 0 (softmax of the mask alone:
+    the mean of V over the unmasked keys), a negative scale and a positive one, on the flash
+    kernel (fp16; head dims 40/80/160; 1100 keys take the two-key-group instance, 77 a ragged
+    tile) and the row-wise kernel (fp32), unmasked, with bool and additive masks and causal."""
+    g = Gen(E + Lk + (1 if dt == "float16" else 2))
+    q = g.randn((2, 2, 70, E), dt)
+    k = g.randn((2, 2, Lk, E), dt)
+    v = g.randn((2, 2, Lk, E), dt)
+    rng = np.random.default_rng(E + Lk)
+    bmask = rng.random((2, 1, 70, Lk)) > 0.4
+    bmask[..., 1] = True
+    amask = (rng.standard_normal((70, Lk)) * 2).astype(np.float32)
+    for scale in (0.0, -0.125, 0.3):
+        for m, causal in ((None, False), (bmask, False), (amask, False), (None, True)):
+            md = None if m is None else mt.from_numpy(m).to("cuda")
+            got = host(F.scaled_dot_product_attention(dev(q), dev(k), dev(v), attn_mask=md, is_causal=causal,
+                                                      scale=scale))
+            ref = orc.sdpa(q, k, v, m, causal, scale)
+            assert rel(val(got), val(ref)) <= TOL[dt], (scale, m is None, causal)
+    # scale 0 without a mask: every query gets the mean of V
+    got = val(host(F.scaled_dot_product_attention(dev(q), dev(k), dev(v), scale=0.0))).astype(np.float64)
+    mean = val(v).astype(np.float64).mean(2, keepdims=True)
+    assert rel(got, np.broadcast_to(mean, got.shape)) <= TOL[dt]
+
+
 @pytest.mark.parametrize("Lq,Lk,E,Ev", [(70, 90, 136, 136), (33, 200, 96, 96), (64, 77, 160, 120), (130, 64, 160, 160)])
 def test_sdpa_dim_parts(Lq, Lk, E, Ev):
     """Head dims above 80 run four dim parts per 32-query block (each wave: the block's scores, a
@@ -694,6 +754,43 @@ def test_group_norm_single_pass_large_batch(dt, shape, groups, monkeypatch):
     ref = orc.group_norm(xs, groups, w, b, 1e-5)
     assert rel(val(runs["1"][0][::7]), val(ref)) <= TOL[dt]
     assert rel(val(runs["1"][1][::7]), val(orc.silu(ref))) <= TOL[dt]
+
+
+@pytest.mark.parametrize("shape", [(16, 320, 64, 64), (2, 320, 64, 64)])
+def test_group_norm_leaves_allocated_bytes_unchanged(shape, monkeypatch):
+    """Neither GroupNorm path keeps device memory past the call: the one-pass kernel (16 samples:
+    512 (sample, group) pairs) needs no partials buffer, the two-kernel path (2 samples) returns
+    its partials block to the cache.  Checked through the C ABI into existing outputs and through
+    F.group_norm / F.group_norm_silu with their outputs dropped."""
+    monkeypatch.setenv("MTHIP_GN_SINGLE", "1")
+    g = Gen(sum(shape))
+    xd = dev(g.randn(shape, "float16"))
+    wd, bd = dev(g.randn((shape[1],), "float16")), dev(g.randn((shape[1],), "float16"))
+    y1 = F.group_norm(xd, 32, wd, bd, 1e-5)  # warm the caches (tables, blocks)
+    y2 = F.group_norm_silu(xd, 32, wd, bd, 1e-5)
+    mt.cuda.synchronize()
+    before = mt.cuda.memory_allocated()
+    for _ in range(3):
+        _ops_gn_into(xd, wd, bd, y1, silu=False)
+        _ops_gn_into(xd, wd, bd, y2, silu=True)
+    mt.cuda.synchronize()
+    assert mt.cuda.memory_allocated() == before
+    for _ in range(3):
+        t = F.group_norm(xd, 32, wd, bd, 1e-5)
+        u = F.group_norm_silu(xd, 32, wd, bd, 1e-5)
+        assert np.array_equal(host(t), host(y1)) and np.array_equal(host(u), host(y2))
+        del t, u
+    mt.cuda.synchronize()
+    assert mt.cuda.memory_allocated() == before
+
+
+def _ops_gn_into(xd, wd, bd, y, silu):
+    """mthip_group_norm into an existing output (so the count sees only the call's own memory)."""
+    from mtorch_amd import _lib
+    B, C = xd.shape[0], xd.shape[1]
+    inner = xd.numel() // (B * C)
+    _lib.check(_lib.lib().mthip_group_norm(0, xd.dtype.code, xd.data_ptr(), wd.data_ptr(), bd.data_ptr(),
+                                           y.data_ptr(), B, C, inner, 32, 1e-5, 1 if silu else 0, xd.dtype.code))
 
 
 @pytest.mark.parametrize("dt", ["float32", "float16"])
@@ -995,6 +1092,21 @@ def test_copy_into_strided_views():
     h[:, 2:8:2][:, :3] = dev(v)  # dtype conversion on the way in
     hx[:, 2:8:2] = orc.f2h(v)
     assert np.array_equal(host(h), hx)
+
+
+def test_copy_into_expanded_destination_last_write_wins():
+    """A destination with zero strides (an expanded view) overlaps itself.  The reference writes
+    every index in row-major order (tensor.cpp:8335-8338), so each element ends as the value of
+    the last index along the expanded dims; the device copy gives exactly that."""
+    g = Gen(95)
+    base = dev(np.zeros((3, 1, 5), np.float32))
+    src = g.randn((3, 4, 5), "float32")
+    base.expand(3, 4, 5).copy_(dev(src))
+    assert np.array_equal(host(base), src[:, 3:4, :])
+    row = dev(np.zeros((1, 6), np.float32))
+    s2 = g.randn((5, 6), "float32")
+    row.expand(5, 6).copy_(dev(s2).transpose(0, 1).transpose(0, 1))
+    assert np.array_equal(host(row), s2[4:5])
 
 
 def test_softmax_other_dim():

@@ -128,3 +128,16 @@ def test_einsum_and_masked_fill_argument_checks():
         x.masked_fill(mt.zeros((3, 3)), 1.0)
     with pytest.raises(ValueError, match="broadcastable"):
         x.masked_fill(mt.ones((2, 3, 3), dtype=mt.bool), 1.0)
+
+
+def test_copy_into_expanded_host_destination_last_write_wins():
+    """Tensor::copy_from writes every index in row-major order (tensor.cpp:8335-8338): along a
+    zero-stride (expanded) destination dim the last index's value stays.  Host tensors follow
+    the same rule as device ones."""
+    base = mt.from_numpy(np.zeros((3, 1, 5), np.float32))
+    src = np.arange(60, dtype=np.float32).reshape(3, 4, 5)
+    base.expand(3, 4, 5).copy_(mt.from_numpy(src))
+    assert np.array_equal(base.numpy(), src[:, 3:4, :])
+    col = mt.from_numpy(np.zeros((4, 1), np.float32))
+    col.expand(4, 6)[:, :] = mt.from_numpy(np.arange(24, dtype=np.float32).reshape(4, 6))
+    assert np.array_equal(col.numpy()[:, 0], np.arange(24, dtype=np.float32).reshape(4, 6)[:, 5])

@@ -80,6 +80,31 @@ def test_addmm_rounds_beta_term_first(orc, rng):
     assert ulps32(got, ref).max() <= 1
 
 
+@pytest.mark.parametrize("dt", ["float32", "float16"])
+def test_addmm_non_finite_beta0_alpha0(orc, rng, dt):
+    """The Linux path stores beta*input even at beta = 0 (tensor.cpp:25253-25258), so an inf or
+    NaN input gives NaN there (IEEE 0*inf), and skips the product at alpha = 0 (:25320), so a NaN
+    or inf in mat1/mat2 never reaches the output, which is then beta*input narrowed once."""
+    cast = (lambda a: orc.f2h(a)) if dt == "float16" else (lambda a: a)
+    back = (lambda a: orc.h2f(a)) if dt == "float16" else (lambda a: a)
+    inp = rng.standard_normal((4, 6)).astype(np.float32)
+    inp[1, 2], inp[3, 0] = np.inf, np.nan
+    m1 = rng.standard_normal((4, 5)).astype(np.float32)
+    m2 = rng.standard_normal((5, 6)).astype(np.float32)
+    inp, m1, m2 = cast(inp), cast(m1), cast(m2)
+    got = back(orc.addmm(inp, m1, m2, beta=0.0, alpha=1.0))
+    nonfinite = ~np.isfinite(back(inp))
+    assert np.array_equal(np.isnan(got), nonfinite)
+    prod = back(m1).astype(np.float64) @ back(m2).astype(np.float64)
+    assert np.allclose(got[~nonfinite], prod[~nonfinite], rtol=2e-3 if dt == "float16" else 1e-6, atol=1e-3)
+    # alpha = 0 with NaN/inf operands: exactly beta*input, narrowed once
+    m1b = back(m1).copy()
+    m1b[0, 0], m1b[2, 4] = np.nan, np.inf
+    got = back(orc.addmm(inp, cast(m1b), m2, beta=0.5, alpha=0.0))
+    ref = back(cast((0.5 * back(inp).astype(np.float64)).astype(np.float32)))
+    assert np.array_equal(got, ref, equal_nan=True)
+
+
 @pytest.mark.parametrize("cfg", [
     dict(C=5, O=7, H=9, W=8, k=3, stride=1, padding=1, dilation=1, groups=1),
     dict(C=6, O=4, H=10, W=7, k=3, stride=2, padding=1, dilation=1, groups=1),
@@ -153,6 +178,51 @@ def test_sdpa_masks_and_causal(orc, rng):
     m[:, 2, :] = False
     out = orc.sdpa(q, k, v, m)
     assert np.isnan(out[:, 2]).all() and not np.isnan(out[:, 1]).any()
+
+
+@pytest.mark.parametrize("dt", ["float32", "float16"])
+def test_sdpa_explicit_scale_closed_forms(orc, rng, dt):
+    """An explicit scale multiplies the scores as given (tensor.cpp:31019, 31182), zero and
+    negative values included; scale=None is 1/sqrt(E).  Pinned by what the mathematics fixes:
+    scale 0 leaves softmax(mask) -- the mean of V over the unmasked keys for a bool mask, the
+    mask's own softmax weights for an additive one; a negative scale is the positive one on -q
+    (negation is exact, so bit for bit); None equals an explicit 1/sqrt(E) bit for bit."""
+    cast = (lambda a: orc.f2h(a)) if dt == "float16" else (lambda a: a)
+    back = (lambda a: orc.h2f(a)) if dt == "float16" else (lambda a: a)
+    q = cast(rng.standard_normal((2, 7, 12)).astype(np.float32))
+    k = cast(rng.standard_normal((2, 11, 12)).astype(np.float32))
+    v = cast(rng.standard_normal((2, 11, 6)).astype(np.float32))
+    vf = back(v).astype(np.float64)
+    tol = 1e-6 if dt == "float32" else 1e-3
+    # scale 0, no mask: the mean of V over all keys, for every query
+    got = back(orc.sdpa(q, k, v, scale=0.0)).astype(np.float64)
+    assert np.allclose(got, np.broadcast_to(vf.mean(1, keepdims=True), got.shape), rtol=tol, atol=tol)
+    # scale 0, bool mask: the mean over the unmasked keys
+    bmask = rng.random((2, 7, 11)) > 0.5
+    bmask[:, :, 3] = True
+    got = back(orc.sdpa(q, k, v, bmask, scale=0.0)).astype(np.float64)
+    ref = np.einsum("pqk,pke->pqe", bmask / bmask.sum(-1, keepdims=True), vf)
+    assert np.allclose(got, ref, rtol=tol, atol=tol)
+    # scale 0, additive mask: softmax of the mask alone
+    fmask = (rng.standard_normal((2, 7, 11)) * 3).astype(np.float32)
+    w = np.exp(fmask - fmask.max(-1, keepdims=True))
+    w = w / w.sum(-1, keepdims=True)
+    got = back(orc.sdpa(q, k, v, fmask, scale=0.0)).astype(np.float64)
+    assert np.allclose(got, np.einsum("pqk,pke->pqe", w, vf), rtol=tol, atol=tol)
+    # scale 0 with causal: the mean over keys 0..i
+    got = back(orc.sdpa(q, k, v, is_causal=True, scale=0.0)).astype(np.float64)
+    ref = np.stack([vf[:, : i + 1].mean(1) for i in range(7)], axis=1)
+    assert np.allclose(got, ref, rtol=tol, atol=tol)
+    # a negative scale is the positive one on -q, bit for bit, with and without masks
+    nq = (q ^ np.uint16(0x8000)) if dt == "float16" else -q
+    for m in (None, bmask, fmask):
+        assert np.array_equal(orc.sdpa(q, k, v, m, scale=-0.125), orc.sdpa(nq, k, v, m, scale=0.125))
+    # None is 1/sqrt(E)
+    assert np.array_equal(orc.sdpa(q, k, v), orc.sdpa(q, k, v, scale=1.0 / math.sqrt(12)))
+    if dt == "float32":  # and against torch in float64 at the non-positive scales
+        for s in (0.0, -0.125, -1.5):
+            ref = _torch_sdpa(q, k, v, fmask, False, s).astype(np.float32)
+            assert np.allclose(orc.sdpa(q, k, v, fmask, scale=s), ref, rtol=1e-6, atol=1e-6), s
 
 
 def test_sd_cross_attention_fixture(orc):
