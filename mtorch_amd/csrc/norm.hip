@@ -953,6 +953,178 @@ __global__ __launch_bounds__(256) void softmax_long_kernel(const T* __restrict__
   }
 }
 
+// Channels-last GroupNorm (+ SiLU) of fp16 NCHW input in ONE launch, for groups of at most
+// 4 * CPT stats chunks of <= 2048 elements (every SD group up to 40960 elements): NSPLIT
+// 1024-thread workgroups per (sample, group), each covering HW / NSPLIT pixels of it.
+//  phase 1: every workgroup reads the whole group (its chunks replayed as the stats kernel's
+//           workgroups sum them: thread t of part p takes vector t of chunks p, p + 4, ...;
+//           the same per-thread sums, wave butterflies and four-wave combine), keeping the
+//           vectors of its own pixels in LDS as [channel][pixel] rows;
+//  phase 2: wave 0 folds the chunk partials as fold_groups does, so the statistics are bit for
+//           bit those of the two-kernel path, and the per-channel affine terms go to LDS;
+//  phase 3: each thread forms `unit` consecutive channels of one pixel from the LDS rows
+//           (normalised as group_norm_apply_nhwc_f16_kernel normalises, then the fp16 SiLU
+//           evaluated on the narrowed value -- the values of silu_f16_table) and stores them
+//           with one 4-, 8- or 16-byte store into y[b][p][g*gc ...]; raw (CAT) receives the
+//           input channels-last the same way.
+// Against stats + apply (two launches, a partials round trip through memory and a table
+// gather per value) this takes one launch; the NSPLIT workgroups of a group run on one XCD and
+// the XCD's workgroups take consecutive groups, so one L2 serves a group's repeated reads and
+// each XCD writes whole runs of a pixel's channels.
+template <typename P, int CPT, bool CAT>
+__global__ __launch_bounds__(1024) void group_norm_nhwc_onepass_kernel(
+    const GnSource<uint16_t> src, const P* __restrict__ gamma, const P* __restrict__ beta, uint16_t* __restrict__ y,
+    uint16_t* __restrict__ raw, int C, int Cp, int groups, int HW, int group_size, int chunk, int splits, int nsplit,
+    float eps, int fuse_silu, int unit, FastDiv div_hw, FastDiv div_units, int xcd_map) {
+  constexpr int V = 8;
+  constexpr int NPART = 4;
+  constexpr int TILE = NPART * CPT * 2048 + 4096;  // halves: this workgroup's [gc][px + 8] rows
+  __shared__ __align__(16) uint16_t tile[TILE];
+  __shared__ float red_s[NPART * CPT][4], red_ss[NPART * CPT][4];
+  __shared__ float2 ch_s[256];  // per channel: (scale, shift) for fp16 parameters, (gamma, beta) for fp32
+  __shared__ float2 st_s;
+  const int n_wg = (int)gridDim.x;
+  int w = (int)blockIdx.x;
+  if (xcd_map) {
+    // workgroup w runs on XCD w % 8: give each XCD a contiguous run of (group, part) pairs
+    const int per = n_wg >> 3;
+    w = (w & 7) * per + (w >> 3);
+  }
+  const int bg = w / nsplit, r = w - bg * nsplit;
+  const int t = threadIdx.x & 255, part = threadIdx.x >> 8, wave = (threadIdx.x >> 6) & 3, lane = threadIdx.x & 63;
+  const int gc = C / groups;
+  const int px = HW / nsplit, p_lo = r * px;
+  const int pitch = px + 8;  // halves per LDS channel row (16-byte multiple)
+  const uint16_t* lo = src.x0 + (int64_t)bg * group_size;
+  const uint16_t* hi = lo;
+  int64_t cut64 = group_size;
+  if constexpr (CAT) src.group(bg, lo, hi, cut64);
+  const int cut = (int)cut64;
+  // phase 1: all loads first (CPT vectors per thread in flight), then the sums
+  uint4 d[CPT];
+#pragma unroll
+  for (int kk = 0; kk < CPT; ++kk) {
+    const int k = NPART * kk + part;
+    const int i = k * chunk + t * V;
+    d[kk] = make_uint4(0u, 0u, 0u, 0u);
+    if (k < splits && t * V < chunk && i < group_size) d[kk] = *reinterpret_cast<const uint4*>((i < cut ? lo : hi) + i);
+  }
+#pragma unroll
+  for (int kk = 0; kk < CPT; ++kk) {
+    const int k = NPART * kk + part;
+    const int i = k * chunk + t * V;
+    const bool have = k < splits && t * V < chunk && i < group_size;
+    float s = 0.0f, ss = 0.0f;
+    if (have) {
+      float f[V];
+      Vec16<uint16_t>::unpack(d[kk], f);
+#pragma unroll
+      for (int j = 0; j < V; ++j) {
+        s += f[j];
+        ss += f[j] * f[j];
+      }
+      const int c = (int)div_hw.div((uint32_t)i), p = i - c * HW;
+      if (p >= p_lo && p < p_lo + px) *reinterpret_cast<uint4*>(&tile[c * pitch + (p - p_lo)]) = d[kk];
+    }
+    s = wave_sum(s);
+    ss = wave_sum(ss);
+    if (lane == 0 && k < splits) {
+      red_s[k][wave] = s;
+      red_ss[k][wave] = ss;
+    }
+  }
+  __syncthreads();
+  // phase 2: the chunk partials folded as fold_groups folds them (splits <= 64: one per lane)
+  if (threadIdx.x < 64) {
+    float s = 0.0f, ss = 0.0f;
+    if (lane < splits) {
+      s += red_s[lane][0] + red_s[lane][1] + red_s[lane][2] + red_s[lane][3];
+      ss += red_ss[lane][0] + red_ss[lane][1] + red_ss[lane][2] + red_ss[lane][3];
+    }
+    s = wave_sum(s);
+    ss = wave_sum(ss);
+    if (lane == 0) st_s = gn_stats(s, ss, (float)group_size, eps);
+  }
+  __syncthreads();
+  const int g = bg % groups, b = bg / groups;
+  if ((int)threadIdx.x < gc) {
+    const int c = g * gc + (int)threadIdx.x;
+    const float gm = gamma ? Elem<P>::load(gamma, c) : 1.0f;
+    const float bt = beta ? Elem<P>::load(beta, c) : 0.0f;
+    if constexpr (sizeof(P) == 2) {
+      // gn_value's fp16-parameter form: scale = gamma*inv, shift = beta - mean*gamma*inv
+      const float scale = gm * st_s.y;
+      const float shift = bt - st_s.x * gm * st_s.y;
+      ch_s[threadIdx.x] = make_float2(scale, shift);
+    } else {
+      ch_s[threadIdx.x] = make_float2(gm, bt);
+    }
+  }
+  __syncthreads();
+  const float mean = st_s.x, inv = st_s.y;
+  // phase 3
+  auto run = [&](auto unit_c, auto silu_c) {
+    constexpr int U = decltype(unit_c)::value;
+    constexpr bool SILU = decltype(silu_c)::value;
+    const int upp = gc / U;  // store units per pixel
+    const int n_units = px * upp;
+    for (int q = threadIdx.x; q < n_units; q += 1024) {
+      const int pl = (int)div_units.div((uint32_t)q), u = q - pl * upp;
+      uint32_t hv[U], rv[U];
+#pragma unroll
+      for (int j = 0; j < U; ++j) {
+        const int cl = u * U + j;
+        const uint16_t h = tile[cl * pitch + pl];
+        rv[j] = h;
+        const float v = h2f_bits(h);
+        const float2 cs = ch_s[cl];
+        float out;
+        if constexpr (sizeof(P) == 2)
+          out = v * cs.x + cs.y;
+        else
+          out = (v - mean) * inv * cs.x + cs.y;
+        uint16_t o = f2h_fast(out);
+        if constexpr (SILU) o = silu_half(o);
+        hv[j] = o;
+      }
+      const int64_t off = ((int64_t)b * HW + p_lo + pl) * Cp + g * gc + u * U;
+      if constexpr (U == 2) {
+        *reinterpret_cast<uint32_t*>(y + off) = hv[0] | (hv[1] << 16);
+        if (CAT && raw) *reinterpret_cast<uint32_t*>(raw + off) = rv[0] | (rv[1] << 16);
+      } else if constexpr (U == 4) {
+        *reinterpret_cast<uint2*>(y + off) = make_uint2(hv[0] | (hv[1] << 16), hv[2] | (hv[3] << 16));
+        if (CAT && raw) *reinterpret_cast<uint2*>(raw + off) = make_uint2(rv[0] | (rv[1] << 16), rv[2] | (rv[3] << 16));
+      } else {
+        *reinterpret_cast<uint4*>(y + off) = make_uint4(hv[0] | (hv[1] << 16), hv[2] | (hv[3] << 16),
+                                                       hv[4] | (hv[5] << 16), hv[6] | (hv[7] << 16));
+        if (CAT && raw)
+          *reinterpret_cast<uint4*>(raw + off) = make_uint4(rv[0] | (rv[1] << 16), rv[2] | (rv[3] << 16),
+                                                           rv[4] | (rv[5] << 16), rv[6] | (rv[7] << 16));
+      }
+    }
+  };
+  if (unit == 8) {
+    if (fuse_silu) run(std::integral_constant<int, 8>{}, std::true_type{});
+    else run(std::integral_constant<int, 8>{}, std::false_type{});
+  } else if (unit == 4) {
+    if (fuse_silu) run(std::integral_constant<int, 4>{}, std::true_type{});
+    else run(std::integral_constant<int, 4>{}, std::false_type{});
+  } else {
+    if (fuse_silu) run(std::integral_constant<int, 2>{}, std::true_type{});
+    else run(std::integral_constant<int, 2>{}, std::false_type{});
+  }
+  // channels [C, Cp) of this workgroup's pixels are zero (written by the last group's workgroups)
+  if (g == groups - 1 && Cp > C) {
+    const int padc = Cp - C;
+    for (int q = threadIdx.x; q < px * padc; q += 1024) {
+      const int pl = q / padc, c = C + (q - pl * padc);
+      const int64_t off = ((int64_t)b * HW + p_lo + pl) * Cp + c;
+      y[off] = 0;
+      if (CAT && raw) raw[off] = 0;
+    }
+  }
+}
+
 int gn_cu_count(int device) {
   static int cached[64] = {0};
   if (device < 0 || device >= 64) return 256;
@@ -967,6 +1139,56 @@ int gn_cu_count(int device) {
 bool gn_single_enabled() {
   const char* e = std::getenv("MTHIP_GN_SINGLE");
   return !(e && e[0] == '0');
+}
+
+// The one-launch channels-last GroupNorm (group_norm_nhwc_onepass_kernel) where it applies: fp16
+// data with whole 16-byte vectors, an even channel count per group (<= 256), at most 20 stats
+// chunks per group.  Returns -1 when it does not apply.  Workgroups per group: MTHIP_GN1_SPLIT,
+// else 4, 2 or 1 -- the most that keep the grid within two workgroups per CU.  MTHIP_GN_ONEPASS=0
+// turns it off (the two-kernel path then runs).
+template <typename P>
+int try_gn_onepass(int device, const GnSource<uint16_t>& src, const P* gamma, const P* beta, uint16_t* y,
+                   uint16_t* raw, int64_t C, int64_t Cp, int64_t groups, int64_t HW, int64_t B, int64_t group_size,
+                   int64_t chunk, int64_t splits, float eps, int fuse_silu, hipStream_t s) {
+  if (const char* e = std::getenv("MTHIP_GN_ONEPASS"))
+    if (e[0] == '0') return -1;
+  const int64_t gc = C / groups;
+  if (gc % 2 != 0 || gc > 256 || splits > 20 || chunk > 2048 || Cp % 8 != 0 || HW % 8 != 0) return -1;
+  const int cpt = (int)ceil_div(splits, 4);
+  const int tile_halves = 4 * (cpt <= 2 ? 2 : cpt <= 4 ? 4 : 5) * 2048 + 4096;
+  const int64_t n_groups = B * groups;
+  const int cus = gn_cu_count(device);
+  int nsplit = 1;
+  for (int cand : {4, 2}) {
+    if (n_groups * cand <= 2 * (int64_t)cus) {
+      nsplit = cand;
+      break;
+    }
+  }
+  if (const char* e = std::getenv("MTHIP_GN1_SPLIT")) nsplit = std::max(1, std::atoi(e));
+  while (nsplit > 1 && (HW % (8 * nsplit) != 0 || gc * (HW / nsplit + 8) > tile_halves)) nsplit /= 2;
+  if (HW % (8 * nsplit) != 0 || gc * (HW / nsplit + 8) > tile_halves) return -1;
+  const int64_t n_wg = n_groups * nsplit;
+  if (n_wg > 2147483647) return -1;
+  const int unit = gc % 8 == 0 ? 8 : gc % 4 == 0 ? 4 : 2;
+  const int xcd_map = (n_wg % 8 == 0 && n_groups % 8 == 0) ? 1 : 0;
+  const FastDiv div_hw((uint32_t)HW), div_units((uint32_t)(gc / unit));
+  const bool cat = src.x1 != nullptr || raw != nullptr;
+#define MTHIP_GN1(CPT, CATV)                                                                                     \
+  hipLaunchKernelGGL((group_norm_nhwc_onepass_kernel<P, CPT, CATV>), dim3((unsigned)n_wg), dim3(1024), 0, s, src, \
+                     gamma, beta, y, raw, (int)C, (int)Cp, (int)groups, (int)HW, (int)group_size, (int)chunk,   \
+                     (int)splits, nsplit, eps, fuse_silu, unit, div_hw, div_units, xcd_map)
+  if (cat) {
+    if (cpt <= 2) MTHIP_GN1(2, true);
+    else if (cpt <= 4) MTHIP_GN1(4, true);
+    else MTHIP_GN1(5, true);
+  } else {
+    if (cpt <= 2) MTHIP_GN1(2, false);
+    else if (cpt <= 4) MTHIP_GN1(4, false);
+    else MTHIP_GN1(5, false);
+  }
+#undef MTHIP_GN1
+  return check_launch("group_norm_nhwc_onepass_kernel");
 }
 
 // Stats (chunked partials), then the apply pass, which folds its group's partials: NCHW as x
@@ -1029,6 +1251,14 @@ int run_group_norm(int device, const void* x, const void* weight, const void* bi
                         C0 % 2 == 0;
   if ((x1 || raw) && !nhwc_f16)
     return fail(MTHIP_ERR_UNSUPPORTED, "mthip_group_norm_nhwc_cat: needs fp16, 16-byte aligned rows and an even split");
+  if constexpr (sizeof(T) == 2) {
+    if (nhwc_f16) {
+      const GnSource<uint16_t> src16{(const uint16_t*)x, (const uint16_t*)x1, C0, C - C0, C / groups, inner, groups};
+      const int rc = try_gn_onepass<P>(device, src16, (const P*)weight, (const P*)bias, (uint16_t*)y, (uint16_t*)raw, C,
+                                       Cp, groups, inner, B, group_size, chunk, splits, (float)eps, fuse_silu, s);
+      if (rc >= 0) return rc;
+    }
+  }
   // The two-kernel path's per-chunk partial sums: a caching-allocator block, or the caller's scratch.
   void* ws = nullptr;
   float2* partial = ws_given;

@@ -756,6 +756,73 @@ def test_group_norm_single_pass_large_batch(dt, shape, groups, monkeypatch):
     assert rel(val(runs["1"][1][::7]), val(orc.silu(ref))) <= TOL[dt]
 
 
+GN1_CASES = [
+    # B, C0, C1, H, W, groups, parameter dtype, silu, workgroups per group (None: the default)
+    (2, 320, 0, 64, 64, 32, "float16", 1, None),  # the bench sub-block
+    (2, 320, 0, 64, 64, 32, "float32", 1, None),
+    (2, 320, 0, 64, 64, 32, "float16", 0, "1"),
+    (2, 320, 0, 64, 64, 32, "float16", 1, "2"),
+    (2, 640, 0, 32, 32, 32, "float32", 1, None),
+    (2, 1280, 0, 32, 32, 32, "float32", 1, None),
+    (2, 1280, 0, 16, 16, 32, "float32", 0, None),
+    (2, 1280, 0, 8, 8, 32, "float32", 1, None),
+    (2, 2560, 0, 8, 8, 32, "float32", 1, None),
+    (2, 640, 320, 32, 32, 32, "float32", 1, None),  # up-block cat inputs, read in place
+    (2, 1280, 640, 16, 16, 32, "float32", 1, None),
+    (2, 1280, 1280, 16, 16, 32, "float32", 1, None),
+    (2, 1280, 1280, 8, 8, 32, "float32", 1, "4"),
+    (3, 36, 0, 12, 20, 6, "float16", 1, None),  # channel padding (Cp 40 > C), 6-channel groups
+    (1, 18, 22, 8, 8, 4, "float16", 1, None),  # a group straddling the two sources
+    (4, 64, 0, 16, 24, 8, "float16", 1, None),  # 16-byte stores (8-channel groups)
+]
+
+
+@pytest.mark.parametrize("B,C0,C1,H,W,G,pdt,silu,split", GN1_CASES)
+def test_group_norm_nhwc_one_launch_equals_two_kernels(B, C0, C1, H, W, G, pdt, silu, split, monkeypatch):
+    """The one-launch channels-last GroupNorm (a 1024-thread workgroup per (sample, group) or
+    per part of one, replaying the stats kernel's sums) against the stats + apply kernels
+    (MTHIP_GN_ONEPASS=0): the normalised (+SiLU) output and, for the concatenated input, the raw
+    channels-last copy, bit for bit, including the zero padding channels; the one-source fp16
+    cases also against the oracle."""
+    from mtorch_amd import _lib
+    L = _lib.lib()
+    g = Gen(B + C0 + C1 + H + W + G)
+    C, HW = C0 + C1, H * W
+    Cp = -(-C // 8) * 8
+    x0 = dev(g.randn((B, C0, H, W), "float16"))
+    x1 = dev(g.randn((B, C1, H, W), "float16")) if C1 else None
+    pt = getattr(mt, pdt)
+    w = mt.from_numpy(g.randn((C,), pdt), dtype=pt).to("cuda")
+    b = mt.from_numpy(g.randn((C,), pdt), dtype=pt).to("cuda")
+    if split is not None:
+        monkeypatch.setenv("MTHIP_GN1_SPLIT", split)
+    outs = {}
+    for mode in ("1", "0"):
+        monkeypatch.setenv("MTHIP_GN_ONEPASS", mode)
+        y = mt.full((B, HW, Cp), 7.0, dtype=mt.float16, device="cuda")  # padding must come back zero
+        r = mt.full((B, HW, Cp), 7.0, dtype=mt.float16, device="cuda")
+        if C1:
+            _lib.check(L.mthip_group_norm_nhwc_cat(0, _lib.F16, x0.data_ptr(), C0, x1.data_ptr(), C1, w.data_ptr(),
+                                                   b.data_ptr(), y.data_ptr(), r.data_ptr(), B, HW, G, 1e-5, silu,
+                                                   pt.code))
+        else:
+            _lib.check(L.mthip_group_norm_nhwc(0, _lib.F16, x0.data_ptr(), w.data_ptr(), b.data_ptr(), y.data_ptr(), B,
+                                               C, HW, G, 1e-5, silu, pt.code))
+        outs[mode] = (host(y), host(r) if C1 else None)
+    assert np.array_equal(outs["1"][0], outs["0"][0])
+    if C1:
+        assert np.array_equal(outs["1"][1], outs["0"][1])
+    if Cp > C:
+        assert not outs["1"][0][..., C:].any()
+    if not C1 and pdt == "float16":
+        xs = host(x0)[:1]
+        ref = orc.group_norm(xs, G, host(w), host(b), 1e-5)
+        if silu:
+            ref = orc.silu(ref)
+        got = outs["1"][0][:1, :, :C].transpose(0, 2, 1).reshape(1, C, H, W)
+        assert rel(val(got), val(ref)) <= TOL["float16"]
+
+
 @pytest.mark.parametrize("shape", [(16, 320, 64, 64), (2, 320, 64, 64)])
 def test_group_norm_leaves_allocated_bytes_unchanged(shape, monkeypatch):
     """Neither GroupNorm path keeps device memory past the call: the one-pass kernel (16 samples:
