@@ -44,6 +44,13 @@ struct FlashArgs {
   int causal;
   float scale;  // as given: zero and negative values multiply the scores like any other
   int cus;  // compute units of the device (launch-shape choices)
+  // Key splits (flash kernel): workgroup z of gridDim.z takes keys [z * kv_chunk, (z+1) *
+  // kv_chunk) and, when gridDim.z > 1, writes its unnormalised accumulator and (max, sum) to
+  // part[z][b*H + h][q][pitch] (dims 0 .. DVB*32-1, then max at DVB*32 and sum at DVB*32 + 1,
+  // log2 units) for flash_combine_kernel instead of the output.
+  int kv_chunk;
+  float* part;
+  int part_pitch;
 };
 
 __device__ __forceinline__ float mask_value(const FlashArgs& a, int64_t b, int64_t h, int64_t q, int64_t k,
@@ -116,7 +123,9 @@ void flash_fwd_f16_kernel(const FlashArgs a) {
   // dp*DVBP + DVBP) of it, dp = wave % DS (each computes the block's scores itself).
   const int dp = wave % DS;
   const int64_t q = (int64_t)blockIdx.x * (32 * WAVES / DS) + (wave / DS) * 32 + col;
-  const int Lk = (int)a.Lk, E = (int)a.E, Ev = (int)a.Ev;
+  // this workgroup's key range [kb, Lk): all keys, or one split of them
+  const int kb = (int)blockIdx.z * a.kv_chunk;
+  const int Lk = min((int)a.Lk, kb + a.kv_chunk), E = (int)a.E, Ev = (int)a.Ev;
   const uint16_t* Q = reinterpret_cast<const uint16_t*>(a.q) + b * a.qs[0] + head * a.qs[1];
   const uint16_t* K = reinterpret_cast<const uint16_t*>(a.k) + b * a.ks[0] + kvh * a.ks[1];
   const uint16_t* V = reinterpret_cast<const uint16_t*>(a.v) + b * a.vs[0] + kvh * a.vs[1];
@@ -241,10 +250,10 @@ void flash_fwd_f16_kernel(const FlashArgs a) {
       mrow_f = reinterpret_cast<const float*>(a.mask) + off;
   }
 
-  fetch(grp * BKV);
-  const int iters = (Lk + BKV * KG - 1) / (BKV * KG);
+  fetch(kb + grp * BKV);
+  const int iters = (Lk - kb + BKV * KG - 1) / (BKV * KG);
   for (int it = 0; it < iters; ++it) {
-    const int kv0 = (it * KG + grp) * BKV;
+    const int kv0 = kb + (it * KG + grp) * BKV;
     __syncthreads();  // every wave is done with the previous tile
     stage(kv0);
     __syncthreads();
@@ -384,6 +393,7 @@ void flash_fwd_f16_kernel(const FlashArgs a) {
       a0 = m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m_run - m);
       a1 = m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m1 - m);
       l_run = l_run * a0 + l1 * a1;
+      m_run = m;  // the merged sum and accumulator are relative to the merged max
     }
 #pragma unroll
     for (int i = 0; i < DVB; ++i) {
@@ -402,6 +412,21 @@ void flash_fwd_f16_kernel(const FlashArgs a) {
   }
 
   if (!qok) return;
+  if (gridDim.z > 1) {
+    // one key split: the unnormalised accumulator and (max, sum) for flash_combine_kernel
+    float* row = a.part + (((int64_t)blockIdx.z * gridDim.y + bh) * a.Lq + q) * a.part_pitch;
+#pragma unroll
+    for (int i = 0; i < DVBP; ++i)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int d0 = (dp * DVBP + i) * 32 + 8 * g + 4 * hh;
+        if (d0 < DVB * 32)
+          *reinterpret_cast<float4*>(row + d0) = make_float4(acc[i][4 * g], acc[i][4 * g + 1], acc[i][4 * g + 2],
+                                                             acc[i][4 * g + 3]);
+      }
+    if (dp == 0 && hh == 0) *reinterpret_cast<float2*>(row + DVB * 32) = make_float2(m_run, l_run);
+    return;
+  }
   uint16_t* O = reinterpret_cast<uint16_t*>(a.o) + b * a.os[0] + head * a.os[1] + q * a.os[2];
   // A fully masked row has l = 0 and, every P being 0, a zero accumulator: 0 * (1/0) = NaN, the
   // reference's 0/0.
@@ -447,6 +472,39 @@ void flash_fwd_f16_kernel(const FlashArgs a) {
         for (int t = 0; t < 4 && d0 + t < Ev; ++t) O[d0 + t] = f2h_generic(acc[i][4 * g + t] * inv_l);
       }
   }
+}
+
+// Merges the key splits of the flash kernel: per query, m = max_z m_z, l = sum_z l_z 2^(m_z - m),
+// o = (sum_z acc_z 2^(m_z - m)) / l, narrowed once (a split that saw only masked keys has
+// m_z = -inf and weight 0; with none left, l = 0 and 0/0 gives the reference's NaN).  One thread
+// per 4 consecutive output dims of one query.
+__global__ __launch_bounds__(256) void flash_combine_kernel(const FlashArgs a, int splits, int dvb32) {
+  const int groups = (int)((a.Ev + 3) / 4);
+  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;  // (query, 4-dim group) of head blockIdx.y
+  if (t >= a.Lq * groups) return;
+  const int64_t bh = blockIdx.y, BH = gridDim.y;
+  const int64_t q = t / groups;
+  const int d0 = (int)(t - q * groups) * 4;
+  float m = -INFINITY;
+  for (int z = 0; z < splits; ++z) m = fmaxf(m, a.part[((z * BH + bh) * a.Lq + q) * a.part_pitch + dvb32]);
+  float l = 0.0f, o[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (int z = 0; z < splits; ++z) {
+    const float* row = a.part + ((z * BH + bh) * a.Lq + q) * a.part_pitch;
+    const float2 ml = *reinterpret_cast<const float2*>(row + dvb32);
+    const float w = ml.x == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(ml.x - m);
+    const float4 v = *reinterpret_cast<const float4*>(row + d0);
+    l += ml.y * w;
+    o[0] += v.x * w;
+    o[1] += v.y * w;
+    o[2] += v.z * w;
+    o[3] += v.w * w;
+  }
+  const float inv_l = 1.0f / l;
+  const int64_t b = bh / a.H, h = bh - b * a.H;
+  uint16_t* O = reinterpret_cast<uint16_t*>(a.o) + b * a.os[0] + h * a.os[1] + q * a.os[2];
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    if (d0 + j < a.Ev) O[d0 + j] = f2h_generic(o[j] * inv_l);
 }
 
 // One wave per query: lanes split the head dims; online softmax over keys in fp32 (scores and
@@ -502,12 +560,12 @@ __global__ __launch_bounds__(256) void attention_rowwise_kernel(const FlashArgs 
 }
 
 template <int DK, int WAVES, int KG, int DS = 1>
-void launch_flash_w(const FlashArgs& a, int64_t bh, hipStream_t s, bool vec) {
-  const dim3 grid((unsigned)ceil_div(a.Lq, 32 * WAVES / DS), (unsigned)bh);
+void launch_flash_w(const FlashArgs& a, int64_t bh, hipStream_t s, bool vec, unsigned splits) {
+  const dim3 grid((unsigned)ceil_div(a.Lq, 32 * WAVES / DS), (unsigned)bh, splits);
   const dim3 block(64 * WAVES * KG);
   if (!vec) {
-    hipLaunchKernelGGL((flash_fwd_f16_kernel<DK, false, -1, WAVES, KG>), dim3((unsigned)ceil_div(a.Lq, 32 * WAVES),
-                       (unsigned)bh), block, 0, s, a);
+    hipLaunchKernelGGL((flash_fwd_f16_kernel<DK, false, -1, WAVES, KG>),
+                       dim3((unsigned)ceil_div(a.Lq, 32 * WAVES), (unsigned)bh, splits), block, 0, s, a);
   } else if (a.mask_kind == MTHIP_MASK_NONE) {
     hipLaunchKernelGGL((flash_fwd_f16_kernel<DK, true, MTHIP_MASK_NONE, WAVES, KG, DS>), grid, block, 0, s, a);
   } else if (a.mask_kind == MTHIP_MASK_BOOL) {
@@ -517,11 +575,15 @@ void launch_flash_w(const FlashArgs& a, int64_t bh, hipStream_t s, bool vec) {
   }
 }
 
-// 4 waves (128 queries) per workgroup.  Measured on every SD shape (self/cross attention at
-// 64x64, 32x32, 16x16 latents), 4 waves were at least as fast as 2 even where they leave CUs
-// idle: each wave then stages a quarter of the K/V tile, and the shared tile serves 128 queries.
+// Which flash instance serves a problem: waves per key group, key groups, dim parts and the
+// query blocks of its grid (so that the key-split planner and the launch agree).
+struct FlashShape {
+  int waves, kg, ds;
+  int64_t gx;  // workgroups along the queries
+};
+
 template <int DK>
-void launch_flash(const FlashArgs& a, int64_t bh, hipStream_t s, bool vec) {
+FlashShape flash_shape(const FlashArgs& a, int64_t bh, bool vec) {
   // Two key groups (8 waves) for small heads over long key sequences, where the extra waves per
   // SIMD hide the score -> softmax -> PV chain (SD self-attention at 64x64: -6 %); with few
   // keys (cross-attention on 77 tokens) the merge costs more than it saves.
@@ -533,13 +595,7 @@ void launch_flash(const FlashArgs& a, int64_t bh, hipStream_t s, bool vec) {
       // MTHIP_FLASH_W=4 keeps four.
       const char* wenv = std::getenv("MTHIP_FLASH_W");
       const bool w8 = wenv ? wenv[0] == '8' : ceil_div(a.Lq, 256) * bh >= a.cus;
-      if (w8)
-        hipLaunchKernelGGL((flash_fwd_f16_kernel<DK, true, MTHIP_MASK_NONE, 8, 2>),
-                           dim3((unsigned)ceil_div(a.Lq, 256), (unsigned)bh), dim3(1024), 0, s, a);
-      else
-        hipLaunchKernelGGL((flash_fwd_f16_kernel<DK, true, MTHIP_MASK_NONE, 4, 2>),
-                           dim3((unsigned)ceil_div(a.Lq, 128), (unsigned)bh), dim3(512), 0, s, a);
-      return;
+      return w8 ? FlashShape{8, 2, 1, ceil_div(a.Lq, 256)} : FlashShape{4, 2, 1, ceil_div(a.Lq, 128)};
     }
   }
   // Head dims above 80 (SD's 160 at the 16x16 and 8x8 latents): four dim parts, so a workgroup
@@ -549,11 +605,52 @@ void launch_flash(const FlashArgs& a, int64_t bh, hipStream_t s, bool vec) {
   // 16x16: one key tile 9.9 -> 7.0 us, 77 keys 12.1 -> 9.5 us, 256 keys 14.6 -> 12.5 us).  At
   // head dim 80 the recomputed scores cost as much as the parts save (32x32, 1024 keys: 25.5
   // against 27.3 us with two parts).
-  if constexpr (DK > 80) {
-    launch_flash_w<DK, 4, 1, 4>(a, bh, s, vec);
-    return;
+  if (DK > 80 && vec) return FlashShape{4, 1, 4, ceil_div(a.Lq, 32)};
+  // 4 waves (128 queries) per workgroup.  Measured on every SD shape (self/cross attention at
+  // 64x64, 32x32, 16x16 latents), 4 waves were at least as fast as 2 even where they leave CUs
+  // idle: each wave then stages a quarter of the K/V tile, and the shared tile serves 128 queries.
+  return FlashShape{4, 1, 1, ceil_div(a.Lq, 128)};
+}
+
+template <int DK>
+void launch_flash(const FlashArgs& a, int64_t bh, hipStream_t s, bool vec, unsigned splits) {
+  const FlashShape sh = flash_shape<DK>(a, bh, vec);
+  if constexpr (DK <= 48) {
+    if (sh.kg == 2) {
+      if (sh.waves == 8)
+        hipLaunchKernelGGL((flash_fwd_f16_kernel<DK, true, MTHIP_MASK_NONE, 8, 2>),
+                           dim3((unsigned)sh.gx, (unsigned)bh, splits), dim3(1024), 0, s, a);
+      else
+        hipLaunchKernelGGL((flash_fwd_f16_kernel<DK, true, MTHIP_MASK_NONE, 4, 2>),
+                           dim3((unsigned)sh.gx, (unsigned)bh, splits), dim3(512), 0, s, a);
+      return;
+    }
   }
-  launch_flash_w<DK, 4, 1>(a, bh, s, vec);
+  if constexpr (DK > 80) {
+    if (sh.ds == 4) {
+      launch_flash_w<DK, 4, 1, 4>(a, bh, s, vec, splits);
+      return;
+    }
+  }
+  launch_flash_w<DK, 4, 1>(a, bh, s, vec, splits);
+}
+
+// Key splits for a grid that leaves CUs idle (the 32x32 latent's 128 workgroups): enough splits
+// of whole 128-key runs to give every CU a workgroup, each keeping >= 512 keys, at most 8; 1 =
+// none.  A split's own pipeline start and the combine launch cost ~3 us, so short key ranges
+// stay whole (SD 32x32 self-attention, 1024 keys: 25.1 -> 23.1 us with 2 splits; 16x16, 256
+// keys: 11.0 -> 13.6 us with 2, so none).  MTHIP_FLASH_SPLIT=n forces n (1 turns it off).
+template <int DK>
+int flash_splits(const FlashArgs& a, int64_t bh, bool vec, int* chunk) {
+  const FlashShape sh = flash_shape<DK>(a, bh, vec);
+  const int64_t wgs = sh.gx * bh;
+  const int64_t runs = ceil_div(a.Lk, 128);
+  int64_t n = wgs < a.cus ? std::min<int64_t>(ceil_div((int64_t)a.cus, wgs), runs / 4) : 1;
+  if (const char* e = std::getenv("MTHIP_FLASH_SPLIT")) n = std::max(1, std::atoi(e));
+  n = std::max<int64_t>(1, std::min<int64_t>({n, runs, 8}));
+  const int64_t c = ceil_div(runs, n) * 128;
+  *chunk = (int)c;
+  return (int)ceil_div(a.Lk, c);
 }
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
@@ -633,19 +730,38 @@ extern "C" int mthip_sdpa(int device, int dtype, const void* q, const int64_t* q
                      qs[0] % 8 == 0 && qs[1] % 8 == 0 && ks[0] % 8 == 0 && ks[1] % 8 == 0 && vs[0] % 8 == 0 &&
                      vs[1] % 8 == 0 && a.os[0] % 8 == 0 && a.os[1] % 8 == 0 && a.os[2] % 8 == 0 &&
                      aligned16(q) && aligned16(k) && aligned16(v) && aligned16(o);
-    if (dmax <= 32)
-      launch_flash<32>(a, bh, s, vec);
-    else if (dmax <= 48)
-      launch_flash<48>(a, bh, s, vec);
-    else if (dmax <= 64)
-      launch_flash<64>(a, bh, s, vec);
-    else if (dmax <= 80)
-      launch_flash<80>(a, bh, s, vec);
-    else if (dmax <= 128)
-      launch_flash<128>(a, bh, s, vec);
-    else
-      launch_flash<160>(a, bh, s, vec);
-    return check_launch("flash_fwd_f16_kernel");
+    // the instance's padded value dims (DVB * 32) and key splits
+    auto run = [&](auto dk_c) -> int {
+      constexpr int DK = decltype(dk_c)::value;
+      int chunk = 0;
+      const int splits = flash_splits<DK>(a, bh, vec, &chunk);
+      void* ws = nullptr;
+      a.kv_chunk = splits > 1 ? chunk : (int)Lk;
+      if (splits > 1) {
+        constexpr int dvb32 = (DK + 31) / 32 * 32;
+        a.part_pitch = dvb32 + 4;
+        if (int rc = mthip_malloc(device, (size_t)splits * (size_t)bh * (size_t)Lq * a.part_pitch * sizeof(float), &ws))
+          return rc;
+        a.part = static_cast<float*>(ws);
+      }
+      launch_flash<DK>(a, bh, s, vec, (unsigned)splits);
+      int rc = check_launch("flash_fwd_f16_kernel");
+      if (rc == MTHIP_OK && splits > 1) {
+        constexpr int dvb32 = (DK + 31) / 32 * 32;
+        const int64_t per_bh = Lq * ceil_div(Ev, 4);
+        hipLaunchKernelGGL(flash_combine_kernel, dim3((unsigned)ceil_div(per_bh, 256), (unsigned)bh), dim3(256), 0, s,
+                           a, splits, dvb32);
+        rc = check_launch("flash_combine_kernel");
+      }
+      mthip_free(device, ws);
+      return rc;
+    };
+    if (dmax <= 32) return run(std::integral_constant<int, 32>{});
+    if (dmax <= 48) return run(std::integral_constant<int, 48>{});
+    if (dmax <= 64) return run(std::integral_constant<int, 64>{});
+    if (dmax <= 80) return run(std::integral_constant<int, 80>{});
+    if (dmax <= 128) return run(std::integral_constant<int, 128>{});
+    return run(std::integral_constant<int, 160>{});
   }
   dim3 grid((unsigned)ceil_div(Lq, 4), (unsigned)bh);
   if (dtype == MTHIP_F16) {

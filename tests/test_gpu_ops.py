@@ -660,6 +660,36 @@ def test_sdpa_explicit_scale(dt, E, Lk):
     assert rel(got, np.broadcast_to(mean, got.shape)) <= TOL[dt]
 
 
+@pytest.mark.parametrize("Lq,Lk,E,split", [(1024, 1024, 80, None), (256, 256, 160, None), (1024, 77, 80, None),
+                                           (256, 77, 160, "2"), (200, 1100, 40, "3"), (300, 700, 64, "8"),
+                                           (130, 520, 160, "5"), (96, 200, 40, "1")])
+def test_sdpa_key_splits(Lq, Lk, E, split, monkeypatch):
+    """Small query grids split the keys over workgroups (each writes its unnormalised accumulator
+    and running max/sum) and a combine kernel merges them: the SD 32x32 / 16x16 self and cross
+    shapes at the default split count, and forced counts with a ragged last split, the
+    two-key-group instance (1100 keys), dim parts (head dim 160), masks and causal."""
+    if split is not None:
+        monkeypatch.setenv("MTHIP_FLASH_SPLIT", split)
+    g = Gen(Lq + Lk + E + 7)
+    q = g.randn((2, 4, Lq, E), "float16")
+    k = g.randn((2, 4, Lk, E), "float16")
+    v = g.randn((2, 4, Lk, E), "float16")
+    rng = np.random.default_rng(Lq + Lk)
+    bmask = rng.random((2, 1, Lq, Lk)) > 0.3
+    bmask[..., -1] = True
+    amask = (rng.standard_normal((Lq, Lk)) * 2).astype(np.float32)
+    rows = np.arange(0, Lq, max(1, Lq // 40))
+    for m, causal in ((None, False), (bmask, False), (amask, False), (None, True)):
+        md = None if m is None else mt.from_numpy(m).to("cuda")
+        got = host(F.scaled_dot_product_attention(dev(q), dev(k), dev(v), attn_mask=md, is_causal=causal))
+        mr = None if m is None else np.ascontiguousarray(np.broadcast_to(m, (2, 4, Lq, Lk))[:, :, rows])
+        if causal:  # the oracle's causal mask counts query positions: evaluate on all rows
+            ref = orc.sdpa(q, k, v, None, True)[:, :, rows]
+        else:
+            ref = orc.sdpa(np.ascontiguousarray(q[:, :, rows]), k, v, mr)
+        assert rel(val(got[:, :, rows]), val(ref)) <= TOL["float16"], (m is None, causal)
+
+
 @pytest.mark.parametrize("Lq,Lk,E,Ev", [(70, 90, 136, 136), (33, 200, 96, 96), (64, 77, 160, 120), (130, 64, 160, 160)])
 def test_sdpa_dim_parts(Lq, Lk, E, Ev):
     """Head dims above 80 run four dim parts per 32-query block (each wave: the block's scores, a
