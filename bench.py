@@ -185,6 +185,8 @@ def run_resnet(args):
         out["cpu_baseline"] = cpu_baseline_resnet(x, gamma, beta, w, b)
     if args.extras:
         out.update(headline_extras(args))
+        if args.cpu:
+            out["cpu_baselines"] = cpu_baselines_extra(out["cpu_baseline"])
     return out
 
 
@@ -223,8 +225,77 @@ def headline_extras(args):
     st = sd_unet.SpatialTransformer(sd_unet._Init("cuda"), 640)
     xt, ctx = rnd(2, 640, 32, 32), rnd(2, 77, 768)
     put("c3_spatial_transformer", _suite_row("c3", lambda: st(xt, ctx), 5, flops=39.63e9, quiet=True))
+    del st, xt, ctx
+    # configs[1], fp32 leg: the same sub-block in fp32 (GN+SiLU written channels-last, conv3x3 on
+    # the fp32 MFMA GEMM with bias and residual fused), priced against the fp32 peak.
+    x32, g32, b32 = rnd(2, 320, 64, 64, dt=mt.float32), rnd(320, dt=mt.float32), rnd(320, dt=mt.float32)
+    w32, bb32 = rnd(320, 320, 3, 3, dt=mt.float32, scale=0.02), rnd(320, dt=mt.float32, scale=0.02)
+    conv_flops = 2.0 * 2 * 4096 * 320 * 2880
+    put("c1_resnet_fp32", _suite_row("c1", lambda: F.group_norm_silu_conv2d(x32, 32, g32, b32, 1e-5, w32, bb32,
+                                                                          padding=1, residual=x32), 10,
+                                     flops=conv_flops, peak=PEAK["fp32_tflops"], quiet=True))
+    put("c1_conv3x3_fp32", _suite_row("c1", lambda: F.conv2d(x32, w32, bb32, padding=1), 10, flops=conv_flops,
+                                      peak=PEAK["fp32_tflops"], quiet=True))
     extras["configs"] = rows
     return extras
+
+
+def cpu_baselines_extra(resnet_cpu):
+    """CPU baselines of the other configs on the same line, 1 core, the oracle's restatement of
+    mtorch's Linux path (kind "port"):
+      * fp32 linear + erf-GELU on 2048 of the 8192 rows (the rate scales: rows are
+        independent);
+      * a per-op-family estimate of one UNet step, labelled as such -- each family's
+        FLOP (sd_unet.unet_flops) divided by the oracle's measured 1-core rate for it: 3x3 convs
+        at the rate of the main sample (cpu_baseline), 1x1 convs, linears and attention on
+        bounded fp16 samples; GroupNorm / LayerNorm / softmax / elementwise ops (linear in the
+        data, no contraction) are left out."""
+    import numpy as np
+
+    import oracle
+    from mtorch_amd import sd_unet
+
+    os.sched_setaffinity(0, {sorted(os.sched_getaffinity(0))[0]})
+    r = oracle.Rng(0)
+
+    def timed(fn):
+        t0 = time.perf_counter()
+        fn()
+        return time.perf_counter() - t0
+
+    out = {}
+    x = r.randn((2048, 320), "float32", 0.0, 1.0)
+    bound = 1.0 / math.sqrt(320)
+    w = r.uniform((1280, 320), -bound, bound, "float32")
+    b = r.uniform((1280,), -bound, bound, "float32")
+    dt = timed(lambda: oracle.gelu(oracle.linear(x, w, b)))
+    fl = 2.0 * 2048 * 1280 * 320
+    out["c0_linear_gelu_fp32"] = {"value": round(fl / dt / 1e12, 6), "unit": "TFLOP/s", "cores": 1, "kind": "port",
+                                  "sample": f"fp32 linear+GELU on 2048/8192 rows of X[8192,320].W[1280,320]^T+b; "
+                                            f"{dt:.2f} s on 1 core", "seconds": round(dt, 3)}
+    rates = {"conv3x3": resnet_cpu["value"] * 1e12}
+    xh, wh = r.randn((512, 640), "float16", 0.0, 1.0), r.randn((640, 640), "float16", 0.0, 0.05)
+    rates["linear"] = 2.0 * 512 * 640 * 640 / timed(lambda: oracle.linear(xh, wh))
+    xc, wc = r.randn((1, 640, 16, 16), "float16", 0.0, 1.0), r.randn((640, 640, 1, 1), "float16", 0.0, 0.05)
+    rates["conv1x1"] = 2.0 * 256 * 640 * 640 / timed(lambda: oracle.conv2d(xc, wc))
+    q = r.randn((1, 1, 512, 80), "float16", 0.0, 1.0)
+    k, v = r.randn((1, 1, 1024, 80), "float16", 0.0, 1.0), r.randn((1, 1, 1024, 80), "float16", 0.0, 1.0)
+    rates["attention"] = 4.0 * 512 * 1024 * 80 / timed(lambda: oracle.sdpa(q, k, v))
+    parts = {}
+    total = sd_unet.unet_flops(parts=parts)
+    est = {f: parts[f] / rates[f] for f in parts}
+    secs = sum(est.values())
+    out["c4_unet_step_estimate"] = {
+        "value": round(secs, 1), "unit": "s per UNet step (estimate)", "cores": 1, "kind": "port",
+        "sample": "per-op-family sum: each family's FLOP of the step / the oracle's 1-core rate on a bounded fp16 "
+                  "sample (3x3 conv: the main cpu_baseline sample; linear [512,640]x[640,640]; 1x1 conv "
+                  "[1,640,16,16]; attention [512 queries x 1024 keys x 80]); norm/softmax/elementwise excluded",
+        "family_gflop": {f: round(parts[f] / 1e9, 1) for f in parts},
+        "family_gflops_rate": {f: round(rates[f] / 1e9, 3) for f in rates},
+        "family_seconds": {f: round(est[f], 1) for f in est},
+        "tflop_per_step": round(total / 1e12, 4),
+    }
+    return out
 
 
 def run_copy_calibration(args):

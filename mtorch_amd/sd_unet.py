@@ -389,51 +389,65 @@ class UNet(nn.Module):
                                         padding=1)
 
 
-def unet_flops(ch=(320, 640, 1280, 1280), B: int = 2, HW: int = 64, ctx_len: int = 77, ctx: int = 768) -> float:
-    """Algorithmic FLOP of one UNet forward (2 per MAC; convs, linears and attention products)."""
-    fl = 0.0
+def unet_flops(ch=(320, 640, 1280, 1280), B: int = 2, HW: int = 64, ctx_len: int = 77, ctx: int = 768,
+               parts: dict | None = None) -> float:
+    """Algorithmic FLOP of one UNet forward (2 per MAC; convs, linears and attention products).
+    parts (optional) receives the split by op family: "conv3x3", "conv1x1" (proj_in/out and
+    the ResBlock shortcuts), "linear" (projections, feed-forward, time MLPs) and "attention"
+    (the QK^T and PV products)."""
+    acc = {"conv3x3": 0.0, "conv1x1": 0.0, "linear": 0.0, "attention": 0.0}
 
     def conv(cin, cout, k, hw):
-        return 2.0 * B * hw * hw * cout * cin * k * k
+        f = 2.0 * B * hw * hw * cout * cin * k * k
+        acc["conv3x3" if k == 3 else "conv1x1"] += f
+
+    def linear(f):
+        acc["linear"] += f
 
     def transformer(C, hw):
         L = hw * hw
-        f = conv(C, C, 1, hw) * 2  # proj_in, proj_out
-        f += 2.0 * B * L * C * 3 * C + 2.0 * B * L * C * C  # qkv, out (self)
-        f += 4.0 * B * L * L * C  # self attention QK^T and PV
-        f += 2.0 * B * L * C * C + 2.0 * B * ctx_len * ctx * 2 * C + 2.0 * B * L * C * C  # q, kv, out (cross)
-        f += 4.0 * B * L * ctx_len * C
-        f += 2.0 * B * L * C * 8 * C + 2.0 * B * L * 4 * C * C  # GEGLU in, FF out
-        return f
+        conv(C, C, 1, hw)  # proj_in
+        conv(C, C, 1, hw)  # proj_out
+        linear(2.0 * B * L * C * 3 * C + 2.0 * B * L * C * C)  # qkv, out (self)
+        acc["attention"] += 4.0 * B * L * L * C  # self attention QK^T and PV
+        linear(2.0 * B * L * C * C + 2.0 * B * ctx_len * ctx * 2 * C + 2.0 * B * L * C * C)  # q, kv, out (cross)
+        acc["attention"] += 4.0 * B * L * ctx_len * C
+        linear(2.0 * B * L * C * 8 * C + 2.0 * B * L * 4 * C * C)  # GEGLU in, FF out
 
     def res(cin, cout, hw):
-        f = conv(cin, cout, 3, hw) + conv(cout, cout, 3, hw) + 2.0 * B * 4 * ch[0] * cout
+        conv(cin, cout, 3, hw)
+        conv(cout, cout, 3, hw)
+        linear(2.0 * B * 4 * ch[0] * cout)  # time embedding projection
         if cin != cout:
-            f += conv(cin, cout, 1, hw)
-        return f
+            conv(cin, cout, 1, hw)
 
-    fl += conv(4, ch[0], 3, HW) + 2.0 * B * (ch[0] * 4 * ch[0] + 4 * ch[0] * 4 * ch[0])
+    conv(4, ch[0], 3, HW)
+    linear(2.0 * B * (ch[0] * 4 * ch[0] + 4 * ch[0] * 4 * ch[0]))
     hw, cin, skips = HW, ch[0], [ch[0]]
     for level, c in enumerate(ch):
         for _ in range(2):
-            fl += res(cin, c, hw)
+            res(cin, c, hw)
             if level < 3:
-                fl += transformer(c, hw)
+                transformer(c, hw)
             cin = c
             skips.append(c)
         if level < 3:
-            fl += conv(c, c, 3, hw // 2) * 1.0
+            conv(c, c, 3, hw // 2)
             hw //= 2
             skips.append(c)
-    fl += res(ch[3], ch[3], hw) * 2 + transformer(ch[3], hw)
+    res(ch[3], ch[3], hw)
+    res(ch[3], ch[3], hw)
+    transformer(ch[3], hw)
     for level, c in enumerate(reversed(ch)):
         for _ in range(3):
-            fl += res(cin + skips.pop(), c, hw)
+            res(cin + skips.pop(), c, hw)
             if level > 0:
-                fl += transformer(c, hw)
+                transformer(c, hw)
             cin = c
         if level < 3:
             hw *= 2
-            fl += conv(c, c, 3, hw)
-    fl += conv(ch[0], 4, 3, HW)
-    return fl
+            conv(c, c, 3, hw)
+    conv(ch[0], 4, 3, HW)
+    if parts is not None:
+        parts.update(acc)
+    return sum(acc.values())
