@@ -357,14 +357,16 @@ namespace {
 // Token tile and K split of the streamed kernel from a makespan model: a persistent workgroup
 // per CU runs ceil(units / CUs) units of `steps` K steps each plus an epilogue, and a split adds
 // the fp32 slices' write and read and the reduction launch.  Per-step and per-unit costs (µs) of
-// 64- and 128-token units come from graph-replayed sweeps; 128-token units lost on every SD
-// shape (8192x960x320: 37.1 against 23.8 us), so they run only when MTHIP_GEMM_STREAM_BT=128
-// forces them.
+// 64- and 128-token units come from graph-replayed sweeps: a 128-token step (eight compute
+// waves, two per SIMD) takes ~0.6 µs against ~0.4 for a 64-token step (four), so 128-token
+// units win where they still give every CU a unit (8192x320x1280 + residual: 18.7 -> 14.9 us,
+// 8192x960x320: 17.8 -> 16.3) and lose where they halve the units of a chip-filling 64-token
+// plan (2048x640x2560: 16.1 against 22.6).  MTHIP_GEMM_STREAM_BT=64 or 128 forces one.
 void stream_plan(int64_t M, int64_t N, int64_t K, int64_t cus, int& best_bt, int64_t& best_ks) {
   const int64_t nk = K / 64, groups = nk / 5;
-  const double step_us[2] = {0.40, 0.55}, epi_us = 0.4;
+  const double step_us[2] = {0.40, 0.60}, epi_us = 0.4;
   const double reduce_us = env_flag("MTHIP_GEMM_REDUCE_US", 3);  // fixed cost of a reduction launch
-  const int force_bt = env_flag("MTHIP_GEMM_STREAM_BT", 64);
+  const int force_bt = env_flag("MTHIP_GEMM_STREAM_BT", 0);
   best_bt = 64;
   best_ks = 1;
   double best = 0.0;
@@ -416,9 +418,9 @@ int launch_stream(int device, StreamArgs sa, GemmArgs r, int64_t K, hipStream_t 
   const bool hr = sa.residual != nullptr && ks == 1;
   if (bt == 128) {
     if (hr)
-      hipLaunchKernelGGL((gemm_stream_kernel<128, true, NCHW>), dim3((unsigned)g), dim3(320), 0, s, sa);
+      hipLaunchKernelGGL((gemm_stream_kernel<128, true, NCHW>), dim3((unsigned)g), dim3(640), 0, s, sa);
     else
-      hipLaunchKernelGGL((gemm_stream_kernel<128, false, NCHW>), dim3((unsigned)g), dim3(320), 0, s, sa);
+      hipLaunchKernelGGL((gemm_stream_kernel<128, false, NCHW>), dim3((unsigned)g), dim3(640), 0, s, sa);
   } else {
     if (hr)
       hipLaunchKernelGGL((gemm_stream_kernel<64, true, NCHW>), dim3((unsigned)g), dim3(320), 0, s, sa);
@@ -518,10 +520,11 @@ int try_stream_linear(int device, const GemmArgs& a, hipStream_t s) {
   const int64_t M = a.M, N = a.N, K = a.K;
   // Where it wins (SD projections, graph-replayed): up to 1280 output channels with K >= 640 --
   // 512x1280x1280 13.5 -> 9.7 us, 2048x640x2560 19.7 -> 15.4, 512x1280x5120 22.3 -> 20.0,
-  // 8192x320x1280 19.1 -> 17.7, 2048x640x640 8.9 -> 8.2; the wide or short-K ones stay on the
-  // DTL GEMM (8192x960x320 21.4 against 23.8, 512x3840x1280 13.3 against 17.1).
-  // MTHIP_GEMM_STREAM=2 takes it wherever it applies.
-  if (mode == 1 && !(N <= 1280 && K >= 640)) return -1;
+  // 8192x320x1280 19.1 -> 17.7, 2048x640x640 8.9 -> 8.2 -- and, with 128-token units, K = 320
+  // over >= 8192 tokens (8192x320x320 8.7 -> 8.2, with the residual 9.7 -> 9.3, 8192x960x320
+  // 17.8 -> 16.3); the wide ones stay on the DTL GEMM (512x3840x1280 12.1 against 12.3,
+  // 2048x1920x640 14.5 against 15.2).  MTHIP_GEMM_STREAM=2 takes it wherever it applies.
+  if (mode == 1 && !(N <= 1280 && (K >= 640 || M >= 8192))) return -1;
   if (K == 0 || K % 320 != 0 || N % 16 != 0 || a.ldc % 4 != 0 || ((uintptr_t)a.c & 7) || ((uintptr_t)a.bias & 7))
     return -1;
   if (a.residual && (a.ld_res % 4 != 0 || ((uintptr_t)a.residual & 7))) return -1;

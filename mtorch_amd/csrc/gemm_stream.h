@@ -4,21 +4,25 @@
 //
 // A unit is 80 output channels x BT tokens over a run of K (one slice of the K split); a
 // persistent workgroup takes a contiguous run of units (XCD-contiguous numbering) and streams
-// their K steps (64 k each) back to back through one LDS ring.  Five wave64s: four compute waves
-// (each owns all 80 channels x BT/4 tokens: FC = 5 channel fragments x FP token fragments of
-// v_mfma_f32_16x16x32_f16) and a producer wave that issues every direct-to-LDS load.  The
+// their K steps (64 k each) back to back through one LDS ring.  BT/16 compute waves (each owns
+// all 80 channels x 16 tokens: FC = 5 channel fragments x one token fragment of
+// v_mfma_f32_16x16x32_f16) and a producer wave that issues every direct-to-LDS load.  A
+// compute wave reads 12 KB of fragments from LDS per step against 10 MFMAs; one wave per SIMD
+// draws LDS at about half the rate two waves per SIMD do (~140 against ~250 bytes per clock per
+// CU in a read-only loop), so 128-token units (eight compute waves) keep the LDS busier than
+// 64-token units (four).  The
 // producer runs SW - 1 steps ahead of the compute waves across unit boundaries, so the next
 // unit's first K steps arrive while the compute waves run the previous unit's epilogue -- the
 // DTL GEMM instead starts every unit's pipeline from its own loads, which at K = 320 (five
 // steps) is most of a unit.
 //
-// Step protocol (as in conv_halo.h): before the barrier that opens step s the producer waits
-// (a fixed vmcnt) until step s's operands have landed and the compute waves until their LDS
-// reads of step s are in registers; after it the producer refills the ring stage of step s - 1
-// with step s + SW - 1, and each compute wave reads step s + 1's fragments into its other
-// register set, interleaved one-to-one with step s's MFMAs.  Units hold a multiple of SW steps
-// (the launcher requires K / 64 to be a multiple of 5), so every unit starts at ring stage 0
-// and a group of SW steps has compile-time stages; the register set of step s is s & 1.
+// Step protocol: before barrier s the producer waits (a fixed vmcnt) until step s's operands
+// have landed and the compute waves until every LDS read of step s - 1 is in registers; after
+// it the producer refills the ring stage of step s - 1 with step s + SW - 1.  A compute wave
+// runs step s as: the first 32-k half's MFMAs interleaved with the second half's LDS reads,
+// barrier s + 1, the second half's MFMAs interleaved with step s + 1's first-half reads.  Units
+// hold a multiple of SW steps (the launcher requires K / 64 to be a multiple of 5), so every unit
+// starts at ring stage 0 and a group of SW steps has compile-time stages.
 //
 // NCHW: the 1x1 conv of a channels-last activation (A = x_nhwc [B*HW][Cp], B = the packed weight
 // [O][Cp]) stored NCHW, y[img][n][p] for token m = img*HW + p: the MFMA operands swap so that a
@@ -58,14 +62,13 @@ struct StreamArgs {
 };
 
 template <int BT, bool HAS_R, bool NCHW = false>
-__global__ __launch_bounds__(320) void gemm_stream_kernel(const StreamArgs args) {
-  constexpr int BC = 80, NW = 4, SW = 5;
+__global__ __launch_bounds__((BT / 16 + BT / 64) * 64) void gemm_stream_kernel(const StreamArgs args) {
+  constexpr int BC = 80, NW = BT / 16, NP = BT / 64, SW = 5;
   constexpr int WT = BT / NW;              // tokens per compute wave
   constexpr int FC = BC / 16, FP = WT / 16;
   constexpr int LW = BC / 8, LA = BT / 8;  // DMA instructions per step
   constexpr int L = LW + LA;
   constexpr uint32_t STAGE = (BC + BT) * 128;
-  constexpr int PEND = (SW - 2) * L > 63 ? 63 : (SW - 2) * L;
   static_assert(BT % 64 == 0 && FP >= 1, "tokens per unit: a multiple of 64");
   static_assert((size_t)SW * STAGE <= 160 * 1024, "LDS");
   __shared__ __align__(16) uint8_t lds[SW * STAGE];
@@ -103,7 +106,13 @@ __global__ __launch_bounds__(320) void gemm_stream_kernel(const StreamArgs args)
   };
 
   // =============================================================================== producer
-  if (wave == NW) {
+  // NP producer waves share a step's L loads: load i (the LW weight rows, then the LA token
+  // rows) goes to producer i % NP, and each waits for its own share.
+  auto producer = [&](auto pw_c) {
+    constexpr int PW = decltype(pw_c)::value;
+    constexpr int MINE = (L - PW + NP - 1) / NP;  // loads of this producer per step
+    constexpr int PEND = (SW - 2) * MINE;
+    static_assert(PEND <= 63, "vmcnt range");
     const __amdgpu_buffer_rsrc_t a_rsrc =
         __builtin_amdgcn_make_buffer_rsrc((void*)args.a, (short)0, args.a_bytes, 0x00020000);
     const __amdgpu_buffer_rsrc_t b_rsrc =
@@ -131,14 +140,17 @@ __global__ __launch_bounds__(320) void gemm_stream_kernel(const StreamArgs args)
         a_off[gi] = (live && m < M) ? ((uint32_t)m * (uint32_t)args.lda + (uint32_t)c * 8u) * 2u : kOOB;
       }
     };
-    // one step's loads into ring stage `stage` (past the last unit: out-of-range, zeros)
+    // this producer's share of one step's loads into ring stage `stage` (past the last unit:
+    // out-of-range, zeros)
     auto issue = [&](uint32_t stage) {
       const uint32_t dst = base + stage * STAGE;
       const uint32_t soff = (uint32_t)(k0 + ij) * 128u;
 #pragma unroll
-      for (int gi = 0; gi < LW; ++gi) dma16(b_rsrc, dst + gi * 1024, w_off[gi], soff);
+      for (int gi = 0; gi < LW; ++gi)
+        if (gi % NP == PW) dma16(b_rsrc, dst + gi * 1024, w_off[gi], soff);
 #pragma unroll
-      for (int gi = 0; gi < LA; ++gi) dma16(a_rsrc, dst + (uint32_t)BC * 128u + gi * 1024, a_off[gi], soff);
+      for (int gi = 0; gi < LA; ++gi)
+        if ((LW + gi) % NP == PW) dma16(a_rsrc, dst + (uint32_t)BC * 128u + gi * 1024, a_off[gi], soff);
       if (++ij == steps) {
         ij = 0;
         ++iu;
@@ -161,6 +173,10 @@ __global__ __launch_bounds__(320) void gemm_stream_kernel(const StreamArgs args)
     // the barrier the compute waves pass at the end of their last step
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_s_waitcnt(0);
+  };
+  if (wave >= NW) {
+    if (NP == 1 || wave == NW) producer(ic<0>{});
+    else producer(ic<1>{});
     return;
   }
 
@@ -189,35 +205,51 @@ __global__ __launch_bounds__(320) void gemm_stream_kernel(const StreamArgs args)
   }
 
   floatx4 acc[FC][FP];
-  halfx8 wf[2][2][FC], pf[2][2][FP];  // [set][kk][fragment]
+  halfx8 wf[2][FC], pf[2][FP];  // [kk][fragment]: the two 32-k halves of a step
   auto zero_acc = [&]() {
 #pragma unroll
     for (int fc = 0; fc < FC; ++fc)
 #pragma unroll
       for (int fp = 0; fp < FP; ++fp) acc[fc][fp] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
   };
-  auto read_frags = [&](auto set_c, auto stage_c) {
-    constexpr int set = decltype(set_c)::value;
-    constexpr uint32_t off = decltype(stage_c)::value * STAGE;
+  // this lane's fragments of 32-k half KK of the step in ring stage STAGE_
+  auto read_half = [&](auto kk_c, auto stage_c) {
+    constexpr int KK = decltype(kk_c)::value;
+    constexpr uint32_t off = decltype(stage_c)::value * STAGE, x = KK ? 64u : 0u;
 #pragma unroll
-    for (int fp = 0; fp < FP; ++fp) {
-      pf[set][0][fp] = *reinterpret_cast<const halfx8*>(lds + pa[fp] + off);
-      pf[set][1][fp] = *reinterpret_cast<const halfx8*>(lds + (pa[fp] ^ 64) + off);
-    }
+    for (int fp = 0; fp < FP; ++fp) pf[KK][fp] = *reinterpret_cast<const halfx8*>(lds + (pa[fp] ^ x) + off);
 #pragma unroll
-    for (int fc = 0; fc < FC; ++fc) {
-      wf[set][0][fc] = *reinterpret_cast<const halfx8*>(lds + wa[fc] + off);
-      wf[set][1][fc] = *reinterpret_cast<const halfx8*>(lds + (wa[fc] ^ 64) + off);
+    for (int fc = 0; fc < FC; ++fc) wf[KK][fc] = *reinterpret_cast<const halfx8*>(lds + (wa[fc] ^ x) + off);
+  };
+  auto mfma_half = [&](auto kk_c) {
+    constexpr int KK = decltype(kk_c)::value;
+#pragma unroll
+    for (int fc = 0; fc < FC; ++fc)
+#pragma unroll
+      for (int fp = 0; fp < FP; ++fp)
+        acc[fc][fp] = NCHW ? __builtin_amdgcn_mfma_f32_16x16x32_f16(pf[KK][fp], wf[KK][fc], acc[fc][fp], 0, 0, 0)
+                           : __builtin_amdgcn_mfma_f32_16x16x32_f16(wf[KK][fc], pf[KK][fp], acc[fc][fp], 0, 0, 0);
+  };
+  // the LDS reads of one half interleaved one-to-one with the MFMAs of the other
+  auto interleave = [&]() {
+    constexpr int NMF = FP * FC, NDS = FP + FC;
+    constexpr int A = NDS < NMF ? NDS : NMF;
+#pragma unroll
+    for (int i = 0; i < A; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
     }
+    if constexpr (NDS > A) __builtin_amdgcn_sched_group_barrier(0x100, NDS - A, 0);
+    if constexpr (NMF > A) __builtin_amdgcn_sched_group_barrier(0x008, NMF - A, 0);
+    __builtin_amdgcn_sched_barrier(0);
   };
 
-  // The current unit's epilogue operands, read when the unit starts (they arrive under its K
-  // steps).  Lane l of fragment (fc, fp) holds channels n0 + fc*16 + 4*(l/16) .. +3 of token
-  // m0 + wave*WT + fp*16 + l%16 (NCHW: tokens m0 + wave*WT + fp*16 + 4*(l/16) .. +3 of channel
-  // n0 + fc*16 + l%16).
-  // (A 128-token unit reads its residual at the epilogue: its registers would not fit beside
-  // the tile under the K steps.)
-  constexpr bool R_EARLY = FC * FP <= 5;
+  // The current unit's epilogue operands, read when a 64-token unit starts (they arrive under
+  // its K steps; a 128-token unit reads them at its epilogue: beside the tile and the fragments
+  // of its eight compute waves they would not fit in registers).  Lane l of fragment (fc, fp)
+  // holds channels n0 + fc*16 + 4*(l/16) .. +3 of token m0 + wave*WT + fp*16 + l%16 (NCHW:
+  // tokens m0 + wave*WT + fp*16 + 4*(l/16) .. +3 of channel n0 + fc*16 + l%16).
+  constexpr bool EPI_EARLY = BT == 64;
   Unit cur{};
   uint2 bz[FC], rz[FC][FP];
   // this lane's channel and first token of fragment (fc, fp)
@@ -239,8 +271,7 @@ __global__ __launch_bounds__(320) void gemm_stream_kernel(const StreamArgs args)
         rz[fc][fp] = make_uint2(v[0], v[1]);
       }
   };
-  auto begin_unit = [&](uint32_t u) {
-    cur = decode(u);
+  auto load_epi = [&]() {
 #pragma unroll
     for (int fc = 0; fc < FC; ++fc) {
       const int n = chan(fc);
@@ -253,7 +284,11 @@ __global__ __launch_bounds__(320) void gemm_stream_kernel(const StreamArgs args)
         bz[fc] = make_uint2(v[0], v[1]);
       }
     }
-    if constexpr (HAS_R && R_EARLY) load_residual();
+    if constexpr (HAS_R) load_residual();
+  };
+  auto begin_unit = [&](uint32_t u) {
+    cur = decode(u);
+    if constexpr (EPI_EARLY) load_epi();
     zero_acc();
   };
   auto end_unit = [&]() {
@@ -271,7 +306,7 @@ __global__ __launch_bounds__(320) void gemm_stream_kernel(const StreamArgs args)
         }
       return;
     }
-    if constexpr (HAS_R && !R_EARLY) load_residual();
+    if constexpr (!EPI_EARLY) load_epi();
     // + bias, (narrowed, + residual), narrowed: every value with f2h_nonnan, again with
     // f2h_generic in a wave that met a NaN
     uint2 out[FC][FP];
@@ -310,48 +345,36 @@ __global__ __launch_bounds__(320) void gemm_stream_kernel(const StreamArgs args)
       }
   };
 
-  // one step: this step's fragments are in registers (set SET), the barrier that opens the next
-  // step, the next step's LDS reads (stage STAGE1, set 1 - SET) interleaved with this step's
-  // MFMAs
-  auto step = [&](auto set_c, auto stage1_c) {
-    constexpr int SET = decltype(set_c)::value;
+  // One step (ring stage ST0; the next step's stage ST1), entered with its first 32-k half's
+  // fragments in registers: the second half's LDS reads interleaved with the first half's
+  // MFMAs, the barrier, then the next step's first-half reads interleaved with the second
+  // half's MFMAs.  The barrier sits where every read of this step has completed and none of the
+  // next step's has started, so the producer may refill this step's ring stage after it (and the
+  // next step's operands are in LDS when it opens).  Half a step of fragments in flight (48
+  // registers) instead of a whole step (96) leaves room for two compute waves per SIMD.
+  auto step = [&](auto st0_c, auto st1_c) {
+    read_half(ic<1>{}, st0_c);
+    mfma_half(ic<0>{});
+    interleave();
     __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
-    read_frags(ic<1 - SET>{}, stage1_c);
-#pragma unroll
-    for (int kk = 0; kk < 2; ++kk)
-#pragma unroll
-      for (int fc = 0; fc < FC; ++fc)
-#pragma unroll
-        for (int fp = 0; fp < FP; ++fp)
-          acc[fc][fp] = NCHW ? __builtin_amdgcn_mfma_f32_16x16x32_f16(pf[SET][kk][fp], wf[SET][kk][fc], acc[fc][fp], 0, 0, 0)
-                             : __builtin_amdgcn_mfma_f32_16x16x32_f16(wf[SET][kk][fc], pf[SET][kk][fp], acc[fc][fp], 0, 0, 0);
-    constexpr int NMF = 2 * FP * FC, NDS = 2 * (FP + FC);
-    constexpr int A = NDS < NMF ? NDS : NMF;
-#pragma unroll
-    for (int i = 0; i < A; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-    }
-    if constexpr (NDS > A) __builtin_amdgcn_sched_group_barrier(0x100, NDS - A, 0);
-    if constexpr (NMF > A) __builtin_amdgcn_sched_group_barrier(0x008, NMF - A, 0);
-    __builtin_amdgcn_sched_barrier(0);
+    read_half(ic<0>{}, st1_c);
+    mfma_half(ic<1>{});
+    interleave();
   };
-  // a group of SW steps starting at ring stage 0, the first with register set G
-  auto group = [&](auto g_c) {
-    constexpr int G0 = decltype(g_c)::value;
-    step(ic<(G0 + 0) & 1>{}, ic<1>{});
-    step(ic<(G0 + 1) & 1>{}, ic<2>{});
-    step(ic<(G0 + 2) & 1>{}, ic<3>{});
-    step(ic<(G0 + 3) & 1>{}, ic<4>{});
-    step(ic<(G0 + 4) & 1>{}, ic<0>{});
+  // a group of SW steps starting at ring stage 0
+  auto group = [&]() {
+    step(ic<0>{}, ic<1>{});
+    step(ic<1>{}, ic<2>{});
+    step(ic<2>{}, ic<3>{});
+    step(ic<3>{}, ic<4>{});
+    step(ic<4>{}, ic<0>{});
   };
 
-  // The steps run in blocks of two groups (ten steps, register sets fixed at compile time);
-  // units end on group boundaries, so the epilogue may follow either group.
+  // Units end on group boundaries.
   __builtin_amdgcn_s_barrier();
-  read_frags(ic<0>{}, ic<0>{});
+  read_half(ic<0>{}, ic<0>{});
   uint32_t u = u_begin;
   int left = (int)(u_end - u_begin) * steps;  // steps still to run
   int in_unit = 0;
@@ -366,10 +389,7 @@ __global__ __launch_bounds__(320) void gemm_stream_kernel(const StreamArgs args)
     }
   };
   while (left > 0) {
-    group(ic<0>{});
-    after_group();
-    if (left == 0) break;
-    group(ic<1>{});
+    group();
     after_group();
   }
 }

@@ -308,8 +308,9 @@ def test_linear(dt, M, N, K):
 @pytest.mark.parametrize("bt", ["64", "128"])
 def test_linear_streamed_kernel(M, N, K, res, bt, monkeypatch):
     """fp16 linears with K a multiple of 320 can take the streamed kernel (persistent workgroups
-    over 80-channel x 64-token units, producer wave, K split and reduction where the model picks
-    it); MTHIP_GEMM_STREAM=2 sends every such shape there.  Checked against the oracle on a
+    over 80-channel x 64- or 128-token units -- four or eight compute waves, one or two producer
+    waves -- K split and reduction where the model picks it); MTHIP_GEMM_STREAM=2 sends every
+    such shape there.  Checked against the oracle on a
     strided subset of rows that includes the last, with bias and with the residual, including
     partial channel and token tiles; 64- and 128-token units (MTHIP_GEMM_STREAM_BT)."""
     monkeypatch.setenv("MTHIP_GEMM_STREAM", "2")
@@ -328,6 +329,24 @@ def test_linear_streamed_kernel(M, N, K, res, bt, monkeypatch):
     if res:
         ref = orc.binary(ref, np.ascontiguousarray(r[rows]), "add")
     assert rel(val(got[rows]), val(ref)) <= TOL["float16"]
+
+
+@pytest.mark.parametrize("M,N,res", [(8192, 320, True), (8192, 960, False), (1000, 240, True), (77, 96, False)])
+def test_linear_streamed_token_tiles_agree_bit_for_bit(M, N, res, monkeypatch):
+    """With one K slice (K = 320) every output's fp32 sum runs over the same k order whether its
+    unit holds 64 tokens (four compute waves, one producer) or 128 (eight compute waves, two
+    producers), so the two give the same bits; a stage refilled while a compute wave still
+    reads it, or a token row read from the wrong wave's fragment, would show here."""
+    monkeypatch.setenv("MTHIP_GEMM_STREAM", "2")
+    g = Gen(M + 3 * N)
+    K = 320
+    x, w, b = dev(g.randn((M, K), "float16")), dev(g.randn((N, K), "float16", 1.0 / np.sqrt(K))), dev(g.randn((N,), "float16"))
+    r = dev(g.randn((M, N), "float16")) if res else None
+    outs = []
+    for bt in ("64", "128"):
+        monkeypatch.setenv("MTHIP_GEMM_STREAM_BT", bt)
+        outs.append(host(F.linear_residual(x, w, b, r) if res else F.linear(x, w, b)))
+    assert np.array_equal(outs[0], outs[1])
 
 
 @pytest.mark.parametrize("dt", ["float32", "float16"])
@@ -970,17 +989,20 @@ def test_conv3x3_halo_whole_image_tiles(C, H):
 
 
 @pytest.mark.parametrize("B,C,H,W,O", [(2, 320, 8, 8, 320), (2, 640, 4, 4, 640), (2, 960, 6, 6, 320),
-                                         (1, 1920, 4, 5, 640), (2, 320, 8, 8, 1280), (1, 640, 2, 6, 48)])
-def test_conv1x1_streamed_nchw(B, C, H, W, O, monkeypatch):
+                                         (1, 1920, 4, 5, 640), (2, 320, 8, 8, 1280), (1, 640, 2, 6, 48),
+                                         (2, 320, 64, 64, 320)])
+@pytest.mark.parametrize("bt", ["64", "128"])
+def test_conv1x1_streamed_nchw(B, C, H, W, O, bt, monkeypatch):
     """fp16 1x1 convs of a channels-last activation with K a multiple of 320 take the streamed
     kernel in its NCHW mode (the SD transformer's proj_out, the ResBlock shortcuts), through
     conv2d_tokens (bias + residual, and no bias) and through conv2d on an NCHW input: checked
     against the oracle on a strided subset of output channels, as is the implicit-GEMM path
     (MTHIP_CONV_STREAM=0; its fp32 sums are grouped differently, so the two agree to rounding,
-    not bit for bit).  Covers partial 80-channel and 64-token tiles, images that split a token
-    tile (6x6), K splits with the conv reduction (K = 1920 over few pixels) and, forced, 1280
-    output channels."""
+    not bit for bit).  Covers partial 80-channel and 64/128-token tiles (MTHIP_GEMM_STREAM_BT),
+    images that split a token tile (6x6, and 8x8 under 128-token units), K splits with the conv
+    reduction (K = 1920 over few pixels), forced, 1280 output channels, and the 64x64 proj_out."""
     from mtorch_amd import _ops
+    monkeypatch.setenv("MTHIP_GEMM_STREAM_BT", bt)
     g = Gen(B + C + H + W + O)
     x = g.randn((B, C, H, W), "float16")
     w = g.randn((O, C, 1, 1), "float16", 1.0 / np.sqrt(C))
