@@ -823,6 +823,8 @@ GN1_CASES = [
     (3, 36, 0, 12, 20, 6, "float16", 1, None),  # channel padding (Cp 40 > C), 6-channel groups
     (1, 18, 22, 8, 8, 4, "float16", 1, None),  # a group straddling the two sources
     (4, 64, 0, 16, 24, 8, "float16", 1, None),  # 16-byte stores (8-channel groups)
+    (2, 160, 160, 64, 64, 32, "float16", 1, None),  # 10-channel groups at 64x64, concatenated input
+    (1, 310, 0, 64, 64, 31, "float16", 1, None),  # ... with channel padding (Cp 312), 31 groups
 ]
 
 
