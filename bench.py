@@ -92,7 +92,8 @@ def _traffic(kernel_key):
 def run_resnet(args):
     """One step = GroupNorm(32)+SiLU written channels-last, then the implicit-GEMM conv with bias
     and residual, through the C ABI exactly as F.group_norm_silu_conv2d issues it.  HIP events
-    on the library's stream time every step and, inside it, the conv launch."""
+    on the library's stream time `steps` steps captured into one HIP graph and replayed (and,
+    for comparison, the same steps launched eagerly), and the conv launches alone the same way."""
     import ctypes
 
     import mtorch_amd as mt
@@ -123,36 +124,53 @@ def run_resnet(args):
         if marks:
             marks[1].record()
 
+    def conv():
+        _lib.check(L.mthip_conv2d_nhwc(0, _lib.F16, xn.ptr, wp, bbd.data_ptr(), y.data_ptr(), B, C, H, W, O, 3, 3,
+                                       1, 1, 1, 1, 1, 1, xd.data_ptr(), None, 0))
+
+    def replayed(fn):
+        """(ms of one replay, wall ms) of a HIP graph of `steps` back-to-back fn() calls, after
+        one untimed replay: the device runs the calls back to back whatever the host's launch
+        rate."""
+        g = mt.cuda.CUDAGraph()
+        with mt.cuda.graph(g):
+            for _ in range(args.steps):
+                fn()
+        g.replay()
+        mt.cuda.synchronize()
+        e0, e1 = mt.cuda.Event(), mt.cuda.Event()
+        t0 = time.perf_counter()
+        e0.record()
+        g.replay()
+        e1.record()
+        mt.cuda.synchronize()
+        return e0.elapsed_time(e1), (time.perf_counter() - t0) * 1e3
+
     for _ in range(args.warmup):
         step()
     mt.cuda.synchronize()
+    # The timed region: `steps` steps captured into one graph and replayed once.
+    ms, wall = replayed(step)
+    ms_step, wall_ms = ms / args.steps, wall / args.steps
+    # The same steps launched eagerly from the host, for comparison.
     start, end = mt.cuda.Event(), mt.cuda.Event()
-    t0 = time.perf_counter()
     start.record()
-    for i in range(args.steps):
+    for _ in range(args.steps):
         step()
     end.record()
     mt.cuda.synchronize()
-    wall_ms = (time.perf_counter() - t0) * 1e3 / args.steps
-    ms_step = start.elapsed_time(end) / args.steps
-    # A second, untimed run of the steps with an event pair around each conv launch: in a step
-    # that pair also spans the conv's dispatch after the GroupNorm (the event between them waits
-    # for the GroupNorm to finish), and the event records themselves separate the launches, so
-    # they stay out of the timed steps above.  The roofline uses the average of `steps`
-    # back-to-back conv launches between two events on the library's stream, which is the
-    # kernel's own duration as rocprofv3's kernel trace reports it.
+    eager_ms_step = start.elapsed_time(end) / args.steps
+    # An untimed eager run with an event pair around each conv launch: in a step that pair also
+    # spans the conv's dispatch after the GroupNorm (the event between them waits for the
+    # GroupNorm to finish), and the event records themselves separate the launches, so they stay
+    # out of the timed steps above.  The roofline uses `steps` back-to-back conv launches
+    # replayed as one graph, which is the kernel's own duration as rocprofv3's kernel trace
+    # reports it.
     for i in range(args.steps):
         step(ev[i])
     mt.cuda.synchronize()
     conv_in_step_ms = sum(a.elapsed_time(b_) for a, b_ in ev) / args.steps
-    burst0, burst1 = mt.cuda.Event(), mt.cuda.Event()
-    burst0.record()
-    for _ in range(args.steps):
-        _lib.check(L.mthip_conv2d_nhwc(0, _lib.F16, xn.ptr, wp, bbd.data_ptr(), y.data_ptr(), B, C, H, W, O, 3, 3,
-                                       1, 1, 1, 1, 1, 1, xd.data_ptr(), None, 0))
-    burst1.record()
-    mt.cuda.synchronize()
-    conv_ms = burst0.elapsed_time(burst1) / args.steps
+    conv_ms = replayed(conv)[0] / args.steps
     flops = 2.0 * B * H * W * O * C * 9  # 15.10 GFLOP per step (the conv; GN/SiLU/add are not counted)
     value = flops / (ms_step * 1e-3) / 1e12
     conv_tflops = flops / (conv_ms * 1e-3) / 1e12
@@ -165,6 +183,7 @@ def run_resnet(args):
         "warmup": args.warmup,
         "ms_per_step": round(ms_step, 4),
         "wall_ms_per_step": round(wall_ms, 4),
+        "eager_ms_per_step": round(eager_ms_step, 4),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,

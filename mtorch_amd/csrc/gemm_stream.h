@@ -244,12 +244,15 @@ __global__ __launch_bounds__((BT / 16 + BT / 64) * 64) void gemm_stream_kernel(c
     __builtin_amdgcn_sched_barrier(0);
   };
 
-  // The current unit's epilogue operands, read when a 64-token unit starts (they arrive under
-  // its K steps; a 128-token unit reads them at its epilogue: beside the tile and the fragments
-  // of its eight compute waves they would not fit in registers).  Lane l of fragment (fc, fp)
-  // holds channels n0 + fc*16 + 4*(l/16) .. +3 of token m0 + wave*WT + fp*16 + l%16 (NCHW:
-  // tokens m0 + wave*WT + fp*16 + 4*(l/16) .. +3 of channel n0 + fc*16 + l%16).
-  constexpr bool EPI_EARLY = BT == 64;
+  // The current unit's epilogue operands.  The row-major bias is read when the unit starts (it
+  // arrives under the K steps; at the epilogue its wait cost a 128-token unit ~2 %), the NCHW
+  // bias (one 2-byte load per channel) at the epilogue (3 % faster for the 1x1 convs at 32x32
+  // and 16x16); the residual when a 64-token unit starts and at a 128-token unit's epilogue
+  // (beside the tile and the fragments of eight compute waves it does not fit in registers).
+  // Lane l of fragment (fc, fp) holds channels n0 + fc*16 + 4*(l/16) .. +3 of token
+  // m0 + wave*WT + fp*16 + l%16 (NCHW: tokens m0 + wave*WT + fp*16 + 4*(l/16) .. +3 of channel
+  // n0 + fc*16 + l%16).
+  constexpr bool R_EARLY = BT == 64;
   Unit cur{};
   uint2 bz[FC], rz[FC][FP];
   // this lane's channel and first token of fragment (fc, fp)
@@ -271,7 +274,7 @@ __global__ __launch_bounds__((BT / 16 + BT / 64) * 64) void gemm_stream_kernel(c
         rz[fc][fp] = make_uint2(v[0], v[1]);
       }
   };
-  auto load_epi = [&]() {
+  auto load_bias = [&]() {
 #pragma unroll
     for (int fc = 0; fc < FC; ++fc) {
       const int n = chan(fc);
@@ -284,11 +287,11 @@ __global__ __launch_bounds__((BT / 16 + BT / 64) * 64) void gemm_stream_kernel(c
         bz[fc] = make_uint2(v[0], v[1]);
       }
     }
-    if constexpr (HAS_R) load_residual();
   };
   auto begin_unit = [&](uint32_t u) {
     cur = decode(u);
-    if constexpr (EPI_EARLY) load_epi();
+    if constexpr (!NCHW) load_bias();
+    if constexpr (HAS_R && R_EARLY) load_residual();
     zero_acc();
   };
   auto end_unit = [&]() {
@@ -306,7 +309,8 @@ __global__ __launch_bounds__((BT / 16 + BT / 64) * 64) void gemm_stream_kernel(c
         }
       return;
     }
-    if constexpr (!EPI_EARLY) load_epi();
+    if constexpr (NCHW) load_bias();
+    if constexpr (HAS_R && !R_EARLY) load_residual();
     // + bias, (narrowed, + residual), narrowed: every value with f2h_nonnan, again with
     // f2h_generic in a wave that met a NaN
     uint2 out[FC][FP];
