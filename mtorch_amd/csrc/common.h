@@ -167,6 +167,56 @@ __device__ __forceinline__ uint32_t f2h_nonnan(float value) {
   return (av < 0x1p-14f ? hs : hn) | ((bits >> 16) & 0x8000u);
 }
 
+// mtorch's fp16 narrowing for finite |value| < 65520 as one float add and the hardware's
+// round-toward-zero conversion (v_cvt_pkrtz_f16_f32, two values per instruction): adding half
+// the fp16 spacing at |value| with value's sign and truncating gives the half-away-from-zero
+// result.  For a float exponent e >= -14 the offset is u/2 = 2^(e-11), a multiple of value's
+// float ulp: the sum is exact unless it carries into the next binade, where its rounding cannot
+// reach the next fp16 value.  Below, the spacing is 2^-24 and the offset 2^-25 - 2^-49: a sum
+// that lands 2^-49 under a multiple of 2^-24 rounds up onto it (its ulp is >= 2^-47 there), so
+// ties still truncate upward while every value under a tie stays under, and |value| < 2^-25
+// stays below 2^-24 (a result of 0).  As bits: 2^(e-11) is the exponent field minus 11 << 23,
+// which for e < -116 wraps negative; a signed integer max against the bits of 2^-25 - 2^-49
+// orders these positive floats as floats (and needs no NaN canonicalisation, unlike a float
+// max of bits).  About 5 VALU operations per value against f2h_nonnan's ~10.  NaN, infinities and |value| >= 65520 (where the
+// conversion saturates at 65504) are not covered: callers keep a running maximum of |value|
+// (maximum propagates NaN) and redo a wave that met one with f2h_nonnan / f2h_generic.
+// tests/f2h_fast_model.c checks every covered pattern, with fp32 denormals kept or flushed.
+__device__ __forceinline__ float f2h_rtz_prep(float value) {
+  const uint32_t bits = __float_as_uint(value);
+  const int off = max((int)(bits & 0x7f800000u) - (11 << 23), 0x32ffffff);  // 0x32ffffff: 2^-25 - 2^-49
+  return value + __uint_as_float((bits & 0x80000000u) | (uint32_t)off);
+}
+
+// Two values narrowed by f2h_rtz_prep + the round-toward-zero conversion, packed low | high << 16.
+__device__ __forceinline__ uint32_t f2h_rtz_pack(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(f2h_rtz_prep(lo), f2h_rtz_prep(hi)));
+}
+
+// The largest |value| seen so far, NaN once any value was NaN: the covering test for the
+// f2h_rtz_* narrowings is !(running < 65520).
+__device__ __forceinline__ float abs_max_nan(float running, float value) {
+  return __builtin_elementwise_maximum(running, __builtin_fabsf(value));
+}
+
+// (float)a.half + (float)b.half for fp16 halves of two packed registers (AHI / BHI: the high
+// half) as one v_fma_mix_f32, a * 1.0 + b with both operands widened exactly: the same single
+// rounding as widening both and adding.  A sum of two halves is 0 or at least 2^-24 in magnitude,
+// never an fp32 denormal, so the denormal mode does not enter.
+template <bool AHI, bool BHI>
+__device__ __forceinline__ float add_halves(uint32_t a, uint32_t b) {
+  float d;
+  if constexpr (AHI && BHI)
+    asm("v_fma_mix_f32 %0, %1, 1.0, %2 op_sel:[1,0,1] op_sel_hi:[1,0,1]" : "=v"(d) : "v"(a), "v"(b));
+  else if constexpr (AHI)
+    asm("v_fma_mix_f32 %0, %1, 1.0, %2 op_sel:[1,0,0] op_sel_hi:[1,0,1]" : "=v"(d) : "v"(a), "v"(b));
+  else if constexpr (BHI)
+    asm("v_fma_mix_f32 %0, %1, 1.0, %2 op_sel:[0,0,1] op_sel_hi:[1,0,1]" : "=v"(d) : "v"(a), "v"(b));
+  else
+    asm("v_fma_mix_f32 %0, %1, 1.0, %2 op_sel_hi:[1,0,1]" : "=v"(d) : "v"(a), "v"(b));
+  return d;
+}
+
 // Exact widening; finite values and infinities match tensor.cpp:317-344 bit for bit.
 __device__ __forceinline__ float h2f_bits(uint16_t h) {
   return (float)__builtin_bit_cast(_Float16, h);

@@ -44,6 +44,7 @@
 namespace mthip {
 
 typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 struct HaloArgs {
   const void* x;  // NHWC [B][H][W][Cp]
@@ -215,27 +216,38 @@ __global__ __launch_bounds__(64 * (4 + NPW)) void conv3x3_halo_kernel(const Halo
     const __amdgpu_buffer_rsrc_t w_rsrc =
         __builtin_amdgcn_make_buffer_rsrc((void*)args.w, (short)0, args.w_bytes, 0x00020000);
     // per-lane offsets, fixed for the unit; the channel block and the tap go in soffset
+    // Per-lane offsets, fixed for the unit; the channel block and the tap go in soffset.  Lane l
+    // covers row 8gi + l/8 of instruction gi and 16-byte chunk (l & 7) ^ ((row >> 1) & 7), which
+    // is (l & 7) ^ (l / 16) ^ 4(gi & 1) since 8 | 8gi.  Everything else that varies with gi is a
+    // compile-time constant or wave-uniform, so the offsets cost one multiply per side and a few
+    // adds, compares and selects per instruction (they stand between the wave's start and its
+    // first load).
+    const int Cp2 = Cp * 2;
+    const int l3 = lane >> 3;
+    const uint32_t chunk0 = (uint32_t)((lane & 7) ^ (lane >> 4)) * 16u;
     uint32_t w_off[LW], p_off[LP];
+    const uint32_t wrow = 9u * (uint32_t)Cp2;  // bytes of one output channel's packed weights
+    const uint32_t wlane = (uint32_t)(o0 + l3) * wrow;
 #pragma unroll
-    for (int gi = 0; gi < LW; ++gi) {
-      const int r = gi * 8 + (lane >> 3);
-      const int c = (lane & 7) ^ ((r >> 1) & 7);
-      const int o = o0 + r;
-      w_off[gi] = o < O ? ((uint32_t)o * 9u * (uint32_t)Cp + (uint32_t)c * 8u) * 2u : kOOB;
-    }
+    for (int gi = 0; gi < LW; ++gi)
+      w_off[gi] = o0 + gi * 8 + l3 < O ? wlane + (uint32_t)(gi * 8) * wrow + (chunk0 ^ (gi & 1 ? 64u : 0u)) : kOOB;
+    // Patch pixel pp = 8gi + l/8 lies in patch row pr = pp / PW, column pc = pp % PW, i.e. at
+    // input pixel (y0 - 1 + pr, pc - 1).  With q = 8gi / PW and r = 8gi % PW fixed at compile
+    // time, pr = q + wrap where wrap = (r + l/8 >= PW), and since the launcher sets TW == W
+    // (PW = W + 2) the input pixel index is plane + pp - 2 pr with plane = (img H + y0 - 1) W - 1.
+    // Offsets are computed modulo 2^32; every in-image pixel's comes out exact (< x_bytes).
+    const uint32_t plane = (uint32_t)((img * H + y0 - 1) * TW - 1 + l3) * (uint32_t)Cp2;
 #pragma unroll
     for (int gi = 0; gi < LP; ++gi) {
-      const int pp = gi * 8 + (lane >> 3);
-      const int c = (lane & 7) ^ ((pp >> 1) & 7);
-      const int pr = pp / PW, pc = pp - (pp / PW) * PW;
-      const int iy = y0 - 1 + pr, ix = pc - 1;
-      const bool ok = pp < NP && iy >= 0 && iy < H && ix >= 0 && ix < W;
-      p_off[gi] = ok ? ((((uint32_t)img * (uint32_t)H + (uint32_t)iy) * (uint32_t)W + (uint32_t)ix) * (uint32_t)Cp +
-                        (uint32_t)c * 8u) * 2u
-                     : kOOB;
+      const int q = gi * 8 / PW, r = gi * 8 % PW;
+      const bool wrap = r + 7 >= PW && r + l3 >= PW;
+      const int pc = r + l3 - (wrap ? PW : 0);
+      const int iy = y0 - 1 + q + (wrap ? 1 : 0);
+      const bool ok = (gi * 8 + 7 < NP || gi * 8 + l3 < NP) && (uint32_t)iy < (uint32_t)H && pc >= 1 && pc <= TW;
+      const uint32_t off = plane + (uint32_t)(gi * 8 - 2 * q) * (uint32_t)Cp2 - (wrap ? 2u * (uint32_t)Cp2 : 0u);
+      p_off[gi] = ok ? off + (chunk0 ^ (gi & 1 ? 64u : 0u)) : kOOB;
     }
     const uint32_t base = lds_addr(lds);
-    const int Cp2 = Cp * 2;
     // weights of step (block j2 of the slice, tap t2) into `stage`; past the slice the last block
     // is loaded again (in range, into a stage no step reads)
     auto issue_w = [&](int j2, int t2, int stage) {
@@ -488,9 +500,39 @@ __global__ __launch_bounds__(64 * (4 + NPW)) void conv3x3_halo_kernel(const Halo
     av[fc] = h2f_bits(ah[fc]);
   }
   // conv + bias, then (+ chan_add), then (+ residual), each add narrowed as the unfused op
-  // sequence narrows it.  Every value is narrowed with f2h_nonnan first; a wave in which some
-  // lane met a NaN redoes all of them with f2h_generic (NaN payloads as mtorch keeps them).
+  // sequence narrows it.  Every value is narrowed with f2h_rtz_* (an add and half a conversion)
+  // while a running maximum of |value| watches for what that covers not (NaN, infinities,
+  // |value| >= 65520); a wave in which some lane met one redoes all values with f2h_nonnan, and
+  // with f2h_generic (NaN payloads as mtorch keeps them) if some lane met a NaN.
   uint2 out[FP][FC];
+  float amax = 0.0f;
+  auto narrow_pair = [&](float a, float b) {  // packed narrow(a) | narrow(b) << 16
+    amax = abs_max_nan(abs_max_nan(amax, a), b);
+    return f2h_rtz_pack(a, b);
+  };
+#pragma unroll
+  for (int fp = 0; fp < FP; ++fp)
+#pragma unroll
+    for (int fc = 0; fc < FC; ++fc) {
+      float x[4];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) x[t] = acc[fp][fc][t] + bv[fc];
+      if constexpr (HAS_A) {  // narrowed pairs + the channel's addend, widened inside the add
+        const uint32_t p01 = narrow_pair(x[0], x[1]), p23 = narrow_pair(x[2], x[3]), a = ah[fc];
+        x[0] = add_halves<false, false>(p01, a);
+        x[1] = add_halves<true, false>(p01, a);
+        x[2] = add_halves<false, false>(p23, a);
+        x[3] = add_halves<true, false>(p23, a);
+      }
+      if constexpr (HAS_R) {  // pixels t, t+1 of the residual sit in one register like the pair
+        const uint32_t p01 = narrow_pair(x[0], x[1]), p23 = narrow_pair(x[2], x[3]);
+        x[0] = add_halves<false, false>(p01, rz[fp][fc].u.x);
+        x[1] = add_halves<true, true>(p01, rz[fp][fc].u.x);
+        x[2] = add_halves<false, false>(p23, rz[fp][fc].u.y);
+        x[3] = add_halves<true, true>(p23, rz[fp][fc].u.y);
+      }
+      out[fp][fc] = make_uint2(narrow_pair(x[0], x[1]), narrow_pair(x[2], x[3]));
+    }
   auto epilogue = [&](auto narrow) {
 #pragma unroll
     for (int fp = 0; fp < FP; ++fp)
@@ -507,15 +549,36 @@ __global__ __launch_bounds__(64 * (4 + NPW)) void conv3x3_halo_kernel(const Halo
         out[fp][fc] = make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
       }
   };
-  bool nan_seen = false;
-  epilogue([&](float x) {
-    nan_seen |= x != x;
-    return f2h_nonnan(x);
-  });
-  if (__builtin_amdgcn_ballot_w64(nan_seen)) epilogue([](float x) { return (uint32_t)f2h_generic(x); });
+  if (__builtin_amdgcn_ballot_w64(!(amax < 65520.0f))) {
+    bool nan_seen = false;
+    epilogue([&](float x) {
+      nan_seen |= x != x;
+      return f2h_nonnan(x);
+    });
+    if (__builtin_amdgcn_ballot_w64(nan_seen)) epilogue([](float x) { return (uint32_t)f2h_generic(x); });
+  }
   // lane l of fragment (fp, fc) holds channel oc[fc] at the four pixels wn*WNP + fp*16 + 4*(l/16)
-  // .. +3 of one output row (TW % 4 == 0): one 8-byte store when Y is 8-byte aligned
-  const bool y_al = ((uintptr_t)Y & 7) == 0;
+  // .. +3 of the unit, one output row (TW % 4 == 0).  TW == W, so unit pixel q is image pixel
+  // y0*W + q.  When Y is 8-byte aligned each is one 8-byte buffer store whose address is one
+  // per-lane offset (+ fp*32 bytes, + fc*16 channels in soffset); rows past H and channels past
+  // O get an out-of-range offset, which the store drops.
+  if (((uintptr_t)Y & 7) == 0) {
+    const __amdgpu_buffer_rsrc_t y_rsrc =
+        __builtin_amdgcn_make_buffer_rsrc((void*)Y, (short)0, args.B * O * HW * 2, 0x00020000);
+    const int q0 = wn * WNP + 4 * (lane >> 4);
+    const uint32_t lane_off = (uint32_t)(((img * O + oc[0]) * HW + y0 * TW + q0) * 2);
+#pragma unroll
+    for (int fp = 0; fp < FP; ++fp) {
+      const bool row_ok = y0 + (q0 + fp * 16) / TW < H;
+#pragma unroll
+      for (int fc = 0; fc < FC; ++fc) {
+        const uint32_t voff = row_ok && oc[fc] < O ? lane_off : kOOB;
+        __builtin_amdgcn_raw_buffer_store_b64(u32x2{out[fp][fc].x, out[fp][fc].y}, y_rsrc, voff + fp * 32,
+                                              fc * 32 * HW, 0);
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int fp = 0; fp < FP; ++fp) {
     const int qq = wn * WNP + fp * 16 + 4 * (lane >> 4);
@@ -524,14 +587,10 @@ __global__ __launch_bounds__(64 * (4 + NPW)) void conv3x3_halo_kernel(const Halo
     for (int fc = 0; fc < FC; ++fc) {
       if (oy < H && oc[fc] < O) {
         T* dst = Y + ((int64_t)img * O + oc[fc]) * HW + oy * W + ox;
-        if (y_al) {
-          *reinterpret_cast<uint2*>(dst) = out[fp][fc];
-        } else {
-          dst[0] = (T)(out[fp][fc].x & 0xffffu);
-          dst[1] = (T)(out[fp][fc].x >> 16);
-          dst[2] = (T)(out[fp][fc].y & 0xffffu);
-          dst[3] = (T)(out[fp][fc].y >> 16);
-        }
+        dst[0] = (T)(out[fp][fc].x & 0xffffu);
+        dst[1] = (T)(out[fp][fc].x >> 16);
+        dst[2] = (T)(out[fp][fc].y & 0xffffu);
+        dst[3] = (T)(out[fp][fc].y >> 16);
       }
     }
   }

@@ -3,7 +3,8 @@
  * and f2h_generic must equal mtorch's rounding (round to nearest, ties away from zero, overflow
  * to inf, NaN keeping the top payload bits; tensor.cpp:276-315, restated in oracle/oracle.c).
  * f2h_nonnan (integer and fma steps, no hardware conversion) must equal f2h_generic on every
- * non-NaN pattern, with fp32 denormal inputs kept or flushed to zero.
+ * non-NaN pattern, with fp32 denormal inputs kept or flushed to zero; f2h_rtz_prep followed by
+ * the round-toward-zero conversion on every finite pattern below 65520 in magnitude.
  * The hardware conversion v_cvt_f16_f32 rounds to nearest-even; F16C's _cvtss_sh with
  * round-to-nearest is the same IEEE operation.  fmaf is the correctly rounded fused multiply-add
  * that v_fma_f32 computes. */
@@ -50,6 +51,26 @@ static uint32_t f2h_nonnan(uint32_t bits, int flush) {
   return (av < 0x1p-14f ? hs : hn) | ((bits >> 16) & 0x8000u);
 }
 
+/* f2h_rtz_prep + v_cvt_pkrtz_f16_f32: value + copysign(offset, value) in fp32 (round to nearest
+ * even), then the conversion rounding toward zero (F16C's _cvtss_sh with _MM_FROUND_TO_ZERO is
+ * the same IEEE operation).  Claimed equal to f2h_generic for every finite |value| < 65520, with
+ * fp32 denormals kept or flushed (inputs and results) to zero. */
+static uint32_t f2h_rtz(uint32_t bits, int flush) {
+  float v;
+  memcpy(&v, &bits, 4);
+  if (flush && (bits & 0x7f800000u) == 0u) v = (bits & 0x80000000u) ? -0.0f : 0.0f;
+  int off = (int)(bits & 0x7f800000u) - (11 << 23);
+  off = off > 0x32ffffff ? off : 0x32ffffff; /* 2^-25 - 2^-49 */
+  const uint32_t ob = (bits & 0x80000000u) | (uint32_t)off;
+  float o;
+  memcpy(&o, &ob, 4);
+  float t = v + o;
+  uint32_t tb;
+  memcpy(&tb, &t, 4);
+  if (flush && (tb & 0x7f800000u) == 0u) t = (tb & 0x80000000u) ? -0.0f : 0.0f;
+  return (uint32_t)_cvtss_sh(t, _MM_FROUND_TO_ZERO) & 0xffffu;
+}
+
 /* mtorch's scalar rule, written independently of the hardware conversion */
 static uint32_t f2h_reference(uint32_t bits) {
   const uint32_t sign = (bits >> 16) & 0x8000u;
@@ -75,7 +96,7 @@ static uint32_t f2h_reference(uint32_t bits) {
 }
 
 int main(void) {
-  uint64_t bad_fast = 0, bad_ref = 0, bad_nonnan = 0;
+  uint64_t bad_fast = 0, bad_ref = 0, bad_nonnan = 0, bad_rtz = 0;
   for (uint64_t i = 0; i <= 0xffffffffull; ++i) {
     const uint32_t b = (uint32_t)i;
     const uint32_t g = f2h_generic(b);
@@ -83,8 +104,11 @@ int main(void) {
     if (f2h_reference(b) != g && bad_ref++ < 5) printf("ref %08x: %04x vs %04x\n", b, f2h_reference(b), g);
     if ((b & 0x7fffffffu) <= 0x7f800000u && (f2h_nonnan(b, 0) != g || f2h_nonnan(b, 1) != g) && bad_nonnan++ < 5)
       printf("nonnan %08x: %04x / %04x vs %04x\n", b, f2h_nonnan(b, 0), f2h_nonnan(b, 1), g);
+    if ((b & 0x7fffffffu) < 0x477ff000u && (f2h_rtz(b, 0) != g || f2h_rtz(b, 1) != g) && bad_rtz++ < 5)
+      printf("rtz %08x: %04x / %04x vs %04x\n", b, f2h_rtz(b, 0), f2h_rtz(b, 1), g);
   }
-  printf("fast!=generic %llu, reference!=generic %llu, nonnan!=generic %llu\n", (unsigned long long)bad_fast,
-         (unsigned long long)bad_ref, (unsigned long long)bad_nonnan);
-  return (bad_fast || bad_ref || bad_nonnan) ? 1 : 0;
+  printf("fast!=generic %llu, reference!=generic %llu, nonnan!=generic %llu, rtz!=generic %llu\n",
+         (unsigned long long)bad_fast, (unsigned long long)bad_ref, (unsigned long long)bad_nonnan,
+         (unsigned long long)bad_rtz);
+  return (bad_fast || bad_ref || bad_nonnan || bad_rtz) ? 1 : 0;
 }

@@ -1,6 +1,7 @@
-"""The device fp16 narrowings (csrc/common.h f2h_fast / f2h_generic / f2h_nonnan) against mtorch's rounding
-rule on all 2^32 float patterns, through a C model of the same integer steps with F16C standing
-in for the hardware's round-to-nearest-even conversion (f2h_fast_model.c).  CPU only (~25 s)."""
+"""The device fp16 narrowings (csrc/common.h f2h_fast / f2h_generic / f2h_nonnan / f2h_rtz_prep)
+against mtorch's rounding rule on all 2^32 float patterns, through a C model of the same integer
+steps with F16C standing in for the hardware's round-to-nearest-even and round-toward-zero
+conversions (f2h_fast_model.c).  CPU only (~60 s)."""
 
 import os
 import shutil

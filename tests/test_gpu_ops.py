@@ -507,6 +507,50 @@ def test_fp16_narrowing_in_gemm_epilogue_is_exact():
     assert got.dtype == np.uint16 and np.array_equal(got, ref)
 
 
+def _same_halves(got, ref):
+    """Bit-equal fp16 arrays, except that +0 and -0 match (the sign of a zero sum depends on
+    the summation order, not on the narrowing) and NaNs match NaNs."""
+    g, r = val(got), val(ref)
+    gn, rn = np.isnan(g), np.isnan(r)
+    zero = (g == 0) & (r == 0)
+    bad = (gn != rn) | (~gn & ~rn & ~zero & (got != ref))
+    assert not bad.any(), (int(bad.sum()), np.argwhere(bad)[:5], got[bad][:5], ref[bad][:5])
+
+
+@pytest.mark.parametrize("B,H,W,O", [(2, 64, 64, 80), (1, 63, 64, 100), (2, 32, 32, 80), (1, 16, 16, 80),
+                                     (2, 8, 8, 80)])
+def test_conv3x3_halo_epilogue_narrowing_is_exact(B, H, W, O):
+    """One-hot centre-tap weights (output channel o reads input channel o % 64 times a factor)
+    make every conv sum a single exact fp32 product, so the epilogue's narrowings are the only
+    rounding: conv + bias, then + residual, each narrowed half-away-from-zero must match the
+    oracle bit for bit over every finite half input, on ties (normal and subnormal results),
+    subnormal and zero results, overflow to inf, and residual infinities and NaNs (waves that
+    meet those redo their values on the general path).  Every latent width's kernel, a partial
+    last row block (H = 63) and a partial channel tile (O = 100)."""
+    C = 64
+    bits = np.arange(65536, dtype=np.uint16)
+    finite = bits[(bits & 0x7C00) != 0x7C00]
+    n = B * C * H * W
+    x = np.resize(finite, n).reshape(B, C, H, W)
+    factors = orc.f2h(np.array([1.0, 1.0 + 2.0**-10, 1.5, 0.75 + 2.0**-11, 3.0, 2.0**-10, 2.0**-13 * 3, 2.0**-20,
+                                1.0 + 2.0**-5, 0.1, 2.0**10 + 1.0, 33.0, -1.0 - 2.0**-10], dtype=np.float32))
+    w = np.zeros((O, C, 3, 3), np.uint16)
+    for o in range(O):
+        w[o, o % C, 1, 1] = factors[o % len(factors)]
+    g = Gen(B * 100 + H + O)
+    b = g.randn((O,), "float16")
+    b[::3] = 0
+    b[1::7] = orc.f2h(np.float32(2.0**-20))
+    r = g.randn((B, O, H, W), "float16")
+    r[0, 5, H // 2, 7], r[0, O - 1, H - 1, 3], r[B - 1, 33, 0, 0] = 0x7C00, 0xFC00, 0x7E00
+    r[0, 7, 2, :8] = 0x7BFF  # 65504: large conv outputs overflow after the add
+    ref_conv = orc.conv2d(x, w, b, padding=1)
+    got = host(F.conv2d(dev(x), dev(w), dev(b), padding=1))
+    _same_halves(got, ref_conv)
+    got = host(F.conv2d_residual(dev(x), dev(w), dev(b), dev(r), padding=1))
+    _same_halves(got, orc.binary(ref_conv, r, "add"))
+
+
 @pytest.mark.parametrize("dt", ["float32", "float16"])
 def test_split_k_paths(dt):
     """Shapes whose output tiles cannot fill the chip while K is long take the split-K path
