@@ -217,6 +217,24 @@ __device__ __forceinline__ float add_halves(uint32_t a, uint32_t b) {
   return d;
 }
 
+// (float)a.half * (float)b.half, exact (a product of two halves fits a float, normal or 0), as
+// one v_fma_mix_f32 with a -0.0 addend, which leaves every product as it is (a +0 addend would
+// turn a -0 product into +0).
+template <bool AHI, bool BHI>
+__device__ __forceinline__ float mul_halves(uint32_t a, uint32_t b) {
+  float d;
+  const float nz = -0.0f;
+  if constexpr (AHI && BHI)
+    asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel:[1,1,0] op_sel_hi:[1,1,0]" : "=v"(d) : "v"(a), "v"(b), "v"(nz));
+  else if constexpr (AHI)
+    asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel:[1,0,0] op_sel_hi:[1,1,0]" : "=v"(d) : "v"(a), "v"(b), "v"(nz));
+  else if constexpr (BHI)
+    asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel:[0,1,0] op_sel_hi:[1,1,0]" : "=v"(d) : "v"(a), "v"(b), "v"(nz));
+  else
+    asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel_hi:[1,1,0]" : "=v"(d) : "v"(a), "v"(b), "v"(nz));
+  return d;
+}
+
 // Exact widening; finite values and infinities match tensor.cpp:317-344 bit for bit.
 __device__ __forceinline__ float h2f_bits(uint16_t h) {
   return (float)__builtin_bit_cast(_Float16, h);

@@ -491,6 +491,34 @@ __device__ __forceinline__ void gemm_finish_unit(const GemmArgs& args, const Gem
       // out = value * gelu(gate): the gate narrowed and looked up, the value narrowed, their
       // product narrowed; every gather of a row before the first use
       uint2 out[FM][4];
+      // Every narrowing with f2h_rtz_* (the gate pairwise before its two table gathers, the
+      // value's narrowed pair multiplied by the gelu halves inside v_fma_mix_f32), under a
+      // running maximum of |value|; a wave that met a NaN, an infinity or |value| >= 65520
+      // redoes its outputs with f2h_nonnan, and with f2h_generic if one was NaN.
+      float amax = 0.0f;
+      auto npair = [&](float a, float b) {
+        amax = abs_max_nan(abs_max_nan(amax, a), b);
+        return f2h_rtz_pack(a, b);
+      };
+#pragma unroll
+      for (int i = 0; i < FM; ++i) {
+        uint32_t gh[4][4];
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+#pragma unroll
+          for (int q = 0; q < 2; ++q) {
+            const uint32_t p = npair(acc[i][1][4 * g + 2 * q] + bgate[g][2 * q], acc[i][1][4 * g + 2 * q + 1] + bgate[g][2 * q + 1]);
+            gh[g][2 * q] = args.gelu_tab[p & 0xffffu];
+            gh[g][2 * q + 1] = args.gelu_tab[p >> 16];
+          }
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const uint32_t v01 = npair(acc[i][0][4 * g] + bval[g][0], acc[i][0][4 * g + 1] + bval[g][1]);
+          const uint32_t v23 = npair(acc[i][0][4 * g + 2] + bval[g][2], acc[i][0][4 * g + 3] + bval[g][3]);
+          out[i][g] = make_uint2(npair(mul_halves<false, false>(v01, gh[g][0]), mul_halves<true, false>(v01, gh[g][1])),
+                                 npair(mul_halves<false, false>(v23, gh[g][2]), mul_halves<true, false>(v23, gh[g][3])));
+        }
+      }
       auto chain = [&](auto& narrow) {
 #pragma unroll
         for (int i = 0; i < FM; ++i) {
@@ -509,11 +537,13 @@ __device__ __forceinline__ void gemm_finish_unit(const GemmArgs& args, const Gem
           }
         }
       };
-      NarrowFast fast;
-      chain(fast);
-      if (__builtin_amdgcn_ballot_w64(fast.nan)) {
-        NarrowExact exact;
-        chain(exact);
+      if (__builtin_amdgcn_ballot_w64(!(amax < 65520.0f))) {
+        NarrowFast fast;
+        chain(fast);
+        if (__builtin_amdgcn_ballot_w64(fast.nan)) {
+          NarrowExact exact;
+          chain(exact);
+        }
       }
 #pragma unroll
       for (int i = 0; i < FM; ++i) {

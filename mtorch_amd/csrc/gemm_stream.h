@@ -311,9 +311,36 @@ __global__ __launch_bounds__((BT / 16 + BT / 64) * 64) void gemm_stream_kernel(c
     }
     if constexpr (NCHW) load_bias();
     if constexpr (HAS_R && !R_EARLY) load_residual();
-    // + bias, (narrowed, + residual), narrowed: every value with f2h_nonnan, again with
-    // f2h_generic in a wave that met a NaN
+    // + bias, (narrowed, + residual), narrowed: every value with f2h_rtz_* (a half-spacing add
+    // and half a round-toward-zero conversion; the residual added to the narrowed pair inside
+    // v_fma_mix_f32), under a running maximum of |value|; a wave that met a NaN, an infinity
+    // or |value| >= 65520 redoes its values with f2h_nonnan, and with f2h_generic if one was NaN.
     uint2 out[FC][FP];
+    auto bias_at = [&](int fc, int t) {
+      const uint32_t bw = t < 2 ? bz[fc].x : bz[fc].y;
+      return bias ? h2f_bits((uint16_t)((t & 1) ? bw >> 16 : bw & 0xffffu)) : -0.0f;
+    };
+    float amax = 0.0f;
+    auto narrow_pair = [&](float a, float b) {
+      amax = abs_max_nan(abs_max_nan(amax, a), b);
+      return f2h_rtz_pack(a, b);
+    };
+#pragma unroll
+    for (int fc = 0; fc < FC; ++fc)
+#pragma unroll
+      for (int fp = 0; fp < FP; ++fp) {
+        float x[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) x[t] = acc[fc][fp][t] + bias_at(fc, t);
+        if constexpr (HAS_R) {
+          const uint32_t p01 = narrow_pair(x[0], x[1]), p23 = narrow_pair(x[2], x[3]);
+          x[0] = add_halves<false, false>(p01, rz[fc][fp].x);
+          x[1] = add_halves<true, true>(p01, rz[fc][fp].x);
+          x[2] = add_halves<false, false>(p23, rz[fc][fp].y);
+          x[3] = add_halves<true, true>(p23, rz[fc][fp].y);
+        }
+        out[fc][fp] = make_uint2(narrow_pair(x[0], x[1]), narrow_pair(x[2], x[3]));
+      }
     auto chain = [&](auto& narrow) {
 #pragma unroll
       for (int fc = 0; fc < FC; ++fc)
@@ -322,8 +349,7 @@ __global__ __launch_bounds__((BT / 16 + BT / 64) * 64) void gemm_stream_kernel(c
           uint32_t h[4];
 #pragma unroll
           for (int t = 0; t < 4; ++t) {
-            const uint32_t bw = t < 2 ? bz[fc].x : bz[fc].y;
-            float x = acc[fc][fp][t] + (bias ? h2f_bits((uint16_t)((t & 1) ? bw >> 16 : bw & 0xffffu)) : -0.0f);
+            float x = acc[fc][fp][t] + bias_at(fc, t);
             if constexpr (HAS_R) {
               const uint32_t rw = t < 2 ? rz[fc][fp].x : rz[fc][fp].y;
               x = h2f_bits((uint16_t)narrow(x)) + h2f_bits((uint16_t)((t & 1) ? rw >> 16 : rw & 0xffffu));
@@ -333,11 +359,13 @@ __global__ __launch_bounds__((BT / 16 + BT / 64) * 64) void gemm_stream_kernel(c
           out[fc][fp] = make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
         }
     };
-    NarrowFast fast;
-    chain(fast);
-    if (__builtin_amdgcn_ballot_w64(fast.nan)) {
-      NarrowExact exact;
-      chain(exact);
+    if (__builtin_amdgcn_ballot_w64(!(amax < 65520.0f))) {
+      NarrowFast fast;
+      chain(fast);
+      if (__builtin_amdgcn_ballot_w64(fast.nan)) {
+        NarrowExact exact;
+        chain(exact);
+      }
     }
 #pragma unroll
     for (int fc = 0; fc < FC; ++fc)

@@ -551,6 +551,45 @@ def test_conv3x3_halo_epilogue_narrowing_is_exact(B, H, W, O):
     _same_halves(got, orc.binary(ref_conv, r, "add"))
 
 
+@pytest.mark.parametrize("bt", ["64", "128"])
+def test_streamed_epilogue_narrowing_is_exact(bt, monkeypatch):
+    """The streamed kernel's epilogue (row-major linear and the NCHW 1x1-conv mode, 64- and
+    128-token units) on one-hot weights: each output is one exact fp32 product, so + bias,
+    narrowed, (+ residual, narrowed) must match the oracle bit for bit over every finite half
+    input -- ties, subnormal and zero results, overflow, residual infinities and NaN."""
+    from mtorch_amd import _ops
+    monkeypatch.setenv("MTHIP_GEMM_STREAM", "2")
+    monkeypatch.setenv("MTHIP_CONV_STREAM", "2")
+    monkeypatch.setenv("MTHIP_GEMM_STREAM_BT", bt)
+    bits = np.arange(65536, dtype=np.uint16)
+    finite = bits[(bits & 0x7C00) != 0x7C00]
+    factors = orc.f2h(np.array([1.0, 1.0 + 2.0**-10, 1.5, 0.75 + 2.0**-11, 3.0, 2.0**-10, 2.0**-13 * 3, 2.0**-20,
+                                1.0 + 2.0**-5, 0.1, 2.0**10 + 1.0, 33.0, -1.0 - 2.0**-10], dtype=np.float32))
+    M, K, N = 1024, 320, 200
+    x = np.resize(finite, M * K).reshape(M, K)
+    w = np.zeros((N, K), np.uint16)
+    w[np.arange(N), np.arange(N) % K] = factors[np.arange(N) % len(factors)]
+    g = Gen(int(bt))
+    b = g.randn((N,), "float16")
+    b[::3] = 0
+    r = g.randn((M, N), "float16")
+    r[5, 7], r[M - 1, N - 1], r[300, 33] = 0x7C00, 0xFC00, 0x7E00
+    ref = orc.linear(x, w, b)
+    _same_halves(host(F.linear(dev(x), dev(w), dev(b))), ref)
+    _same_halves(host(F.linear_residual(dev(x), dev(w), dev(b), dev(r))), orc.binary(ref, r, "add"))
+    B, H, W, O = 2, 16, 16, 160
+    tok = np.resize(finite[::-1], B * H * W * K).reshape(B, H * W, K)
+    xc = np.ascontiguousarray(tok.reshape(B, H, W, K).transpose(0, 3, 1, 2))
+    wc = np.zeros((O, K, 1, 1), np.uint16)
+    wc[np.arange(O), np.arange(O) % K, 0, 0] = factors[np.arange(O) % len(factors)]
+    rc = g.randn((B, O, H, W), "float16")
+    rc[1, 3, 4, 5], rc[0, O - 1, 0, 0] = 0x7E00, 0x7C00
+    refc = orc.conv2d(xc, wc, b[:O])
+    _same_halves(host(_ops.conv2d_tokens(dev(tok), dev(wc), dev(b[:O]), H, W)), refc)
+    _same_halves(host(_ops.conv2d_tokens(dev(tok), dev(wc), dev(b[:O]), H, W, residual=dev(rc))),
+                 orc.binary(refc, rc, "add"))
+
+
 @pytest.mark.parametrize("dt", ["float32", "float16"])
 def test_split_k_paths(dt):
     """Shapes whose output tiles cannot fill the chip while K is long take the split-K path
