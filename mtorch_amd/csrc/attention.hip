@@ -133,12 +133,30 @@ void flash_fwd_f16_kernel(const FlashArgs a) {
   // Q^T fragments (B operand of S^T): query q, dims step*16 + hh*8 + [0, 8).  A negative scale
   // runs as softmax((-q) k^T |scale|): the sign goes into Q (an exact fp16 negation), so the
   // scores stay in the "larger is heavier" order the running max relies on.
+  //
+  // KSHIFT (head dims <= 40 in the 48-dim instance, the launcher's choice): Q is taken
+  // pre-multiplied by scale * log2(e) (rounded to fp16; scales with |scale * log2 e| outside
+  // [2^-10, 1] go to the generic instance, so that product neither overflows nor drops Q's low
+  // bits), and padding dim 40 carries -m, the running max, against a K column of ones: the
+  // score MFMAs then deliver score * scale * log2(e) - m, the exp2 argument as it stands, where
+  // the other instances spend a multiply-add per score (a quarter of the softmax's VALU time
+  // next to the exp2 at its quarter rate).  m is kept representable in fp16 while |m| <= 2^15;
+  // beyond, dim 40 carries 0 and the lane subtracts m itself.
+  constexpr bool KSHIFT = VEC && DK == 48;
+  constexpr int KSD = 40;  // the shift dim: qf[KSD / 16][0] of the lanes with hh == 1
   const uint32_t qneg = a.scale < 0.0f ? 0x80008000u : 0u;
   halfx8 qf[NSTEP];
 #pragma unroll
   for (int st = 0; st < NSTEP; ++st) {
     const int d0 = st * 16 + hh * 8;
-    if constexpr (VEC) {
+    if constexpr (KSHIFT) {
+      uint4 r = make_uint4(0, 0, 0, 0);
+      if (q < a.Lq && d0 < E) r = *reinterpret_cast<const uint4*>(Q + q * a.qs[2] + d0);
+      const halfx8 raw = __builtin_bit_cast(halfx8, r);
+      const float qsc = a.scale * kLog2e;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) qf[st][j] = (_Float16)((float)raw[j] * qsc);
+    } else if constexpr (VEC) {
       uint4 r = make_uint4(0, 0, 0, 0);
       if (q < a.Lq && d0 < E) r = *reinterpret_cast<const uint4*>(Q + q * a.qs[2] + d0);
       r.x ^= qneg;
@@ -197,7 +215,11 @@ void flash_fwd_f16_kernel(const FlashArgs a) {
 #pragma unroll
       for (int i = 0; i < KCH; ++i) {
         const int c = tid + i * NT;
-        if (c < BKV * KCHR) *reinterpret_cast<uint4*>(&Ks[(c / KCHR) * KP + (c % KCHR) * 8]) = kreg[i];
+        uint4 val = kreg[i];
+        // KSHIFT: dim KSD of every key is 1 (E <= KSD, so the chunk was loaded as zeros)
+        if constexpr (KSHIFT)
+          if ((c % KCHR) * 8 == KSD) val = make_uint4(0x3c00u, 0u, 0u, 0u);
+        if (c < BKV * KCHR) *reinterpret_cast<uint4*>(&Ks[(c / KCHR) * KP + (c % KCHR) * 8]) = val;
       }
 #pragma unroll
       for (int i = 0; i < VCH; ++i) {
@@ -232,7 +254,8 @@ void flash_fwd_f16_kernel(const FlashArgs a) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[i][r] = 0.0f;
   float m_run = -INFINITY, l_run = 0.0f;
-  const float sl2 = fabsf(a.scale) * kLog2e;  // >= 0; the sign went into Q
+  const float sl2 = fabsf(a.scale) * kLog2e;  // not KSHIFT: >= 0, the sign went into Q
+  bool m_big = false;  // KSHIFT: |m| > 2^15, subtracted by the lane (dim KSD carries 0)
   const bool qok = q < a.Lq;
   const int mask_kind = MASK >= 0 ? MASK : a.mask_kind;
   // This lane's mask row (query q of head `head`), addressed per key by one 32-bit multiply.
@@ -286,7 +309,7 @@ void flash_fwd_f16_kernel(const FlashArgs a) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int key = kv0 + sb * 32 + 8 * (r >> 2) + 4 * hh + (r & 3);
-          float v = t[r] * sl2;
+          float v = KSHIFT ? t[r] : t[r] * sl2;
           if (key >= Lk) {
             v = -INFINITY;
           } else {
@@ -306,30 +329,62 @@ void flash_fwd_f16_kernel(const FlashArgs a) {
     // Lazy rescaling: the running max (log2 units) moves only when a score exceeds it by more
     // than 8, so P <= 2^8 (exact in fp16 and in the fp32 sums) and most tiles skip the
     // accumulator rescale.  O = acc / l is unchanged by the choice of reference max.
-    const float mult = checked ? 1.0f : sl2;
-    const float m_cand = fmaxf(m_run, mx * mult);
+    const float mult = KSHIFT || checked ? 1.0f : sl2;
+    // KSHIFT: the scores are relative to the m the tile ran with (dim KSD's -m, 0 before any
+    // key or when the lane subtracts m itself)
+    const float m_tile = KSHIFT ? (m_run == -INFINITY || m_big ? 0.0f : m_run) : 0.0f;
+    const float m_cand = KSHIFT ? fmaxf(m_run, m_tile + mx) : fmaxf(m_run, mx * mult);
     if (m_cand > m_run + 8.0f) {
-      const float alpha = __builtin_amdgcn_exp2f(m_run - m_cand);  // 0 when m_run = -inf
+      float m_new = m_cand;
+      if constexpr (KSHIFT) {
+        // kept representable in fp16 (a new max a fraction of an ulp below the tile's max
+        // leaves P <= 2^(8 + ulp/2)); dim KSD carries -m from the next tile on
+        m_big = fabsf(m_cand) > 32768.0f;
+        const _Float16 mh = (_Float16)(m_big ? 0.0f : -m_cand);
+        if (!m_big) m_new = -(float)mh;
+        if (hh == 1) qf[KSD / 16][0] = mh;
+      }
+      const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);  // 0 when m_run = -inf
       l_run *= alpha;
 #pragma unroll
       for (int i = 0; i < DVBP; ++i)
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[i][r] *= alpha;
-      m_run = m_cand;
+      if constexpr (KSHIFT) {  // re-base this tile's scores on the new max
+        const float d = (m_big ? 0.0f : m_new) - m_tile;
+#pragma unroll
+        for (int sb = 0; sb < 2; ++sb)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) s[sb][r] -= d;
+      }
+      m_run = m_new;
     }
     const float m_use = m_run == -INFINITY ? 0.0f : m_run;
+    if constexpr (KSHIFT) {  // lanes whose max dim KSD cannot carry subtract it here
+      if (__builtin_amdgcn_ballot_w64(m_big)) {
+        const float d = m_big ? m_use : 0.0f;
+#pragma unroll
+        for (int sb = 0; sb < 2; ++sb)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) s[sb][r] -= d;
+      }
+    }
+    // exp2 argument: KSHIFT the score as it stands, else score * mult - m_use
+    auto p_of = [&](float x) {
+      return KSHIFT ? __builtin_amdgcn_exp2f(x) : __builtin_amdgcn_exp2f(fmaf(x, mult, -m_use));
+    };
     if (kOnes && ones) {
 #pragma unroll
       for (int sb = 0; sb < 2; ++sb)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) s[sb][r] = __builtin_amdgcn_exp2f(fmaf(s[sb][r], mult, -m_use));
+        for (int r = 0; r < 16; ++r) s[sb][r] = p_of(s[sb][r]);
     } else {
       float psum = 0.0f;
 #pragma unroll
       for (int sb = 0; sb < 2; ++sb)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          s[sb][r] = __builtin_amdgcn_exp2f(fmaf(s[sb][r], mult, -m_use));
+          s[sb][r] = p_of(s[sb][r]);
           psum += s[sb][r];
         }
       psum += __shfl_xor(psum, 32, 64);
@@ -726,10 +781,15 @@ extern "C" int mthip_sdpa(int device, int dtype, const void* q, const int64_t* q
   // The flash kernel needs a finite scale (its running max works in scaled units); an infinite
   // or NaN one takes the row-wise kernel, which multiplies each score by it as the reference does.
   if (dtype == MTHIP_F16 && Lk > 0 && dmax <= 160 && small_heads && std::isfinite(a.scale)) {
+    // The 48-dim VEC instance pre-scales Q by scale * log2(e) in fp16 (KSHIFT): for |scale *
+    // log2 e| outside [2^-10, 1] (but 0) that product could overflow or drop Q's low bits, and
+    // the generic instance, which scales the fp32 scores, runs instead.
+    const double sl2 = std::fabs((double)a.scale) * 1.4426950408889634;
+    const bool prescale_ok = !(dmax <= 48 && E <= 40 && dmax > 32) || a.scale == 0.0f || (sl2 >= 1.0 / 1024.0 && sl2 <= 1.0);
     const bool vec = E % 8 == 0 && Ev % 8 == 0 && qs[2] % 8 == 0 && ks[2] % 8 == 0 && vs[2] % 8 == 0 &&
                      qs[0] % 8 == 0 && qs[1] % 8 == 0 && ks[0] % 8 == 0 && ks[1] % 8 == 0 && vs[0] % 8 == 0 &&
                      vs[1] % 8 == 0 && a.os[0] % 8 == 0 && a.os[1] % 8 == 0 && a.os[2] % 8 == 0 &&
-                     aligned16(q) && aligned16(k) && aligned16(v) && aligned16(o);
+                     aligned16(q) && aligned16(k) && aligned16(v) && aligned16(o) && prescale_ok;
     // the instance's padded value dims (DVB * 32) and key splits
     auto run = [&](auto dk_c) -> int {
       constexpr int DK = decltype(dk_c)::value;
@@ -757,7 +817,8 @@ extern "C" int mthip_sdpa(int device, int dtype, const void* q, const int64_t* q
       return rc;
     };
     if (dmax <= 32) return run(std::integral_constant<int, 32>{});
-    if (dmax <= 48) return run(std::integral_constant<int, 48>{});
+    // the 48-dim instance keeps dim 40 free for its max shift (KSHIFT): E 41..48 take 64
+    if (dmax <= 48 && E <= 40) return run(std::integral_constant<int, 48>{});
     if (dmax <= 64) return run(std::integral_constant<int, 64>{});
     if (dmax <= 80) return run(std::integral_constant<int, 80>{});
     if (dmax <= 128) return run(std::integral_constant<int, 128>{});
