@@ -590,6 +590,41 @@ def test_streamed_epilogue_narrowing_is_exact(bt, monkeypatch):
                  orc.binary(refc, rc, "add"))
 
 
+def test_tile_gemm_epilogue_narrowing_is_exact(monkeypatch):
+    """The tile GEMM's epilogue (fp16 linear with bias and residual, MTHIP_GEMM_STREAM=0 keeping
+    the streamed kernel out, and the implicit-GEMM conv with bias and residual: width 24 is not
+    a halo-kernel width) on one-hot weights, so each output is one exact product: the
+    narrowings must match the oracle bit for bit over every finite half input, ties, subnormal
+    and zero results, overflow and residual infinities and NaN included."""
+    monkeypatch.setenv("MTHIP_GEMM_STREAM", "0")
+    bits = np.arange(65536, dtype=np.uint16)
+    finite = bits[(bits & 0x7C00) != 0x7C00]
+    factors = orc.f2h(np.array([1.0, 1.0 + 2.0**-10, 1.5, 0.75 + 2.0**-11, 3.0, 2.0**-10, 2.0**-13 * 3, 2.0**-20,
+                                1.0 + 2.0**-5, 0.1, 2.0**10 + 1.0, 33.0, -1.0 - 2.0**-10], dtype=np.float32))
+    M, K, N = 1024, 64, 256
+    x = np.resize(finite, M * K).reshape(M, K)
+    w = np.zeros((N, K), np.uint16)
+    w[np.arange(N), np.arange(N) % K] = factors[np.arange(N) % len(factors)]
+    g = Gen(91)
+    b = g.randn((N,), "float16")
+    b[::3] = 0
+    r = g.randn((M, N), "float16")
+    r[5, 7], r[M - 1, N - 1], r[300, 33] = 0x7C00, 0xFC00, 0x7E00
+    ref = orc.linear(x, w, b)
+    _same_halves(host(F.linear(dev(x), dev(w), dev(b))), ref)
+    _same_halves(host(F.linear_residual(dev(x), dev(w), dev(b), dev(r))), orc.binary(ref, r, "add"))
+    B, C, H, W, O = 2, 64, 16, 24, 128
+    xc = np.resize(finite[::-1], B * C * H * W).reshape(B, C, H, W)
+    wc = np.zeros((O, C, 3, 3), np.uint16)
+    wc[np.arange(O), np.arange(O) % C, 1, 1] = factors[np.arange(O) % len(factors)]
+    bc = b[:O]
+    rc = g.randn((B, O, H, W), "float16")
+    rc[1, 3, 4, 5], rc[0, O - 1, 0, 0] = 0x7E00, 0x7C00
+    refc = orc.conv2d(xc, wc, bc, padding=1)
+    _same_halves(host(F.conv2d(dev(xc), dev(wc), dev(bc), padding=1)), refc)
+    _same_halves(host(F.conv2d_residual(dev(xc), dev(wc), dev(bc), dev(rc), padding=1)), orc.binary(refc, rc, "add"))
+
+
 @pytest.mark.parametrize("dt", ["float32", "float16"])
 def test_split_k_paths(dt):
     """Shapes whose output tiles cannot fill the chip while K is long take the split-K path
