@@ -1139,6 +1139,94 @@ __global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(const GemmArgs 
   const int64_t total = args.M * n4;
   const int64_t slice = args.M * args.ld_partial;
   const int ks = (int)args.ksplit;
+  // The linear and conv epilogues over at most 8 slices (every split the planners choose):
+  // 32-bit indices, and each thread issues its epilogue operands (bias, addend, residual)
+  // ahead of its slices in one straight-line block, so it waits for one memory round trip
+  // rather than two (slices past ks re-read the last one, in range, and are not added).
+  constexpr bool kFast = EPI == EPI_LINEAR || EPI == EPI_CONV;
+  const int OHW = (int)(args.OH * args.OW);
+  if (kFast && ks <= 8 && total < (int64_t(1) << 31) && (EPI == EPI_LINEAR || OHW % 4 == 0)) {
+    const uint32_t un4 = (uint32_t)n4, ut = (uint32_t)total;
+    const int N = (int)args.N, M = (int)args.M;
+    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < ut; i += gridDim.x * blockDim.x) {
+      const uint32_t row = i / un4;
+      const int col0 = (int)(i - row * un4) * 4;
+      const int nv = N - col0 < 4 ? N - col0 : 4;
+      // range-checked buffer loads: an absent operand has an empty range and reads zeros, so
+      // the block has no branch and the loads stay ahead of the slices
+      float b[4], r[4], av = 0.0f;
+      T* dst;
+      const bool has_b = args.bias != nullptr, has_r = args.residual != nullptr, has_a = args.chan_add != nullptr;
+      if constexpr (EPI == EPI_LINEAR) {
+        const __amdgpu_buffer_rsrc_t b_rsrc =
+            __builtin_amdgcn_make_buffer_rsrc((void*)args.bias, (short)0, has_b ? N * (int)sizeof(T) : 0, 0x00020000);
+        const __amdgpu_buffer_rsrc_t r_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+            (void*)args.residual, (short)0, has_r ? (int)(((int64_t)(M - 1) * args.ld_res + N) * (int64_t)sizeof(T)) : 0,
+            0x00020000);
+#pragma unroll
+        for (int t4 = 0; t4 < 4; ++t4) {
+          const int c = col0 + t4 < N ? col0 + t4 : N - 1;
+          if constexpr (sizeof(T) == 2) {
+            b[t4] = h2f_bits(__builtin_amdgcn_raw_buffer_load_b16(b_rsrc, c * 2, 0, 0));
+            r[t4] = h2f_bits(__builtin_amdgcn_raw_buffer_load_b16(r_rsrc, (int)(((int64_t)row * args.ld_res + c) * 2), 0, 0));
+          } else {
+            b[t4] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(b_rsrc, c * 4, 0, 0));
+            r[t4] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r_rsrc, (int)(((int64_t)row * args.ld_res + c) * 4), 0, 0));
+          }
+        }
+        dst = reinterpret_cast<T*>(args.c) + (int64_t)row * args.ldc + col0;
+      } else {
+        // row = output channel, col = output pixel (image-major; OHW % 4 == 0, so the 4
+        // pixels lie in one image and are contiguous); NCHW store
+        const int img = (int)args.div_ohw.div((uint32_t)col0);
+        const int64_t addr = ((int64_t)img * M + row) * OHW + (col0 - img * OHW);
+        const int B = (int)(N / OHW);
+        const __amdgpu_buffer_rsrc_t b_rsrc =
+            __builtin_amdgcn_make_buffer_rsrc((void*)args.bias, (short)0, has_b ? M * (int)sizeof(T) : 0, 0x00020000);
+        const __amdgpu_buffer_rsrc_t a_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+            (void*)args.chan_add, (short)0, has_a ? (int)(((int64_t)(B - 1) * args.chan_add_ld + M) * (int64_t)sizeof(T)) : 0,
+            0x00020000);
+        const __amdgpu_buffer_rsrc_t r_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+            (void*)args.residual, (short)0, has_r ? (int)((int64_t)B * M * OHW * (int64_t)sizeof(T)) : 0, 0x00020000);
+        float bv;
+        if constexpr (sizeof(T) == 2) {
+          bv = h2f_bits(__builtin_amdgcn_raw_buffer_load_b16(b_rsrc, (int)row * 2, 0, 0));
+          av = h2f_bits(__builtin_amdgcn_raw_buffer_load_b16(a_rsrc, (img * args.chan_add_ld + (int)row) * 2, 0, 0));
+#pragma unroll
+          for (int t4 = 0; t4 < 4; ++t4)
+            r[t4] = h2f_bits(__builtin_amdgcn_raw_buffer_load_b16(r_rsrc, (int)((addr + (t4 < nv ? t4 : 0)) * 2), 0, 0));
+        } else {
+          bv = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(b_rsrc, (int)row * 4, 0, 0));
+          av = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(a_rsrc, (img * args.chan_add_ld + (int)row) * 4, 0, 0));
+#pragma unroll
+          for (int t4 = 0; t4 < 4; ++t4)
+            r[t4] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r_rsrc, (int)((addr + (t4 < nv ? t4 : 0)) * 4), 0, 0));
+        }
+        b[0] = b[1] = b[2] = b[3] = bv;
+        dst = reinterpret_cast<T*>(args.c) + addr;
+      }
+      const float* p = args.partial + (int64_t)row * args.ld_partial + col0;
+      float4 t[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) t[k] = *reinterpret_cast<const float4*>(p + (int64_t)(k < ks ? k : ks - 1) * slice);
+      float4 s = t[0];
+#pragma unroll
+      for (int k = 1; k < 8; ++k)
+        if (k < ks) {
+          s.x += t[k].x;
+          s.y += t[k].y;
+          s.z += t[k].z;
+          s.w += t[k].w;
+        }
+      float v[4] = {s.x, s.y, s.z, s.w};
+      if constexpr (EPI == EPI_LINEAR)
+        epi_math<T, EPI, ACT>(v, b, has_b, 0.0f, false, r, has_r, args.gelu_tab);
+      else
+        epi_math<T, EPI, ACT>(v, b, true, av, has_a, r, has_r);
+      store_cols<T>(dst, v, nv);
+    }
+    return;
+  }
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
     const int row = (int)(i / n4);
     const int col0 = (int)(i - (int64_t)row * n4) * 4;
