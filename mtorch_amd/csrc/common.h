@@ -217,6 +217,30 @@ __device__ __forceinline__ float add_halves(uint32_t a, uint32_t b) {
   return d;
 }
 
+// acc + (float)a.half and acc + (float)a.half * (float)a.half (HI: the high half), each with one
+// rounding as one v_fma_mix_f32: a half times 1.0 or times itself is exact in fp32, so these
+// equal widening, (squaring,) and adding.  For sums of halves and of squares of halves (every
+// term 0 or at least 2^-48 in magnitude, partial sums multiples of 2^-48) no fp32 denormal
+// arises, so the denormal mode does not enter.
+template <bool HI>
+__device__ __forceinline__ float acc_add_half(float acc, uint32_t a) {
+  float d;
+  if constexpr (HI)
+    asm("v_fma_mix_f32 %0, %1, 1.0, %2 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(d) : "v"(a), "v"(acc));
+  else
+    asm("v_fma_mix_f32 %0, %1, 1.0, %2 op_sel_hi:[1,0,0]" : "=v"(d) : "v"(a), "v"(acc));
+  return d;
+}
+template <bool HI>
+__device__ __forceinline__ float acc_add_sq_half(float acc, uint32_t a) {
+  float d;
+  if constexpr (HI)
+    asm("v_fma_mix_f32 %0, %1, %1, %2 op_sel:[1,1,0] op_sel_hi:[1,1,0]" : "=v"(d) : "v"(a), "v"(acc));
+  else
+    asm("v_fma_mix_f32 %0, %1, %1, %2 op_sel_hi:[1,1,0]" : "=v"(d) : "v"(a), "v"(acc));
+  return d;
+}
+
 // (float)a.half * (float)b.half, exact (a product of two halves fits a float, normal or 0), as
 // one v_fma_mix_f32 with a -0.0 addend, which leaves every product as it is (a +0 addend would
 // turn a -0 product into +0).

@@ -1016,12 +1016,15 @@ __global__ __launch_bounds__(1024) void group_norm_nhwc_onepass_kernel(
     const bool have = k < splits && t * V < chunk && i < group_size;
     float s = 0.0f, ss = 0.0f;
     if (have) {
-      float f[V];
-      Vec16<uint16_t>::unpack(d[kk], f);
+      // s += f, ss += f * f in element order, each add one v_fma_mix_f32 on the raw halves
+      // (the same roundings: a half's square is exact in fp32)
+      const uint32_t w[4] = {d[kk].x, d[kk].y, d[kk].z, d[kk].w};
 #pragma unroll
-      for (int j = 0; j < V; ++j) {
-        s += f[j];
-        ss += f[j] * f[j];
+      for (int j = 0; j < 4; ++j) {
+        s = acc_add_half<false>(s, w[j]);
+        ss = acc_add_sq_half<false>(ss, w[j]);
+        s = acc_add_half<true>(s, w[j]);
+        ss = acc_add_sq_half<true>(ss, w[j]);
       }
       const int c = (int)div_hw.div((uint32_t)i), p = i - c * HW;
       if (p >= p_lo && p < p_lo + px) *reinterpret_cast<uint4*>(&tile[c * pitch + (p - p_lo)]) = d[kk];
