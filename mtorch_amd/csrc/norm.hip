@@ -714,6 +714,97 @@ __global__ __launch_bounds__(256) void layer_norm_vec_kernel(const T* __restrict
   const int64_t row0 = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * RPW;
   if (row0 >= rows) return;
   const int chunks = (int)(N / V);
+  if constexpr (sizeof(T) == 2 && sizeof(P) == 4) {
+    // fp16 rows, fp32 parameters (the SD transformer's LayerNorms): the rows stay as raw
+    // halves, every sum term, square and centring subtraction is one v_fma_mix_f32 on them
+    // (the same roundings as widening first), and the outputs are narrowed pairwise with
+    // f2h_rtz_pack; a row in which some lane met a value that covers not (NaN, infinity,
+    // |value| >= 65520) is narrowed again with f2h_fast.
+    uint4 hr[RPW][CPL];
+#pragma unroll
+    for (int r = 0; r < RPW; ++r)
+#pragma unroll
+      for (int j = 0; j < CPL; ++j) {
+        const int c = lane + 64 * j;
+        hr[r][j] = make_uint4(0u, 0u, 0u, 0u);
+        if (row0 + r < rows && c < chunks) hr[r][j] = *reinterpret_cast<const uint4*>(x + (row0 + r) * N + c * V);
+      }
+    float wv[CPL][V], bv[CPL][V];
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+      const int c = lane + 64 * j;
+#pragma unroll
+      for (int k = 0; k < V; ++k) {
+        wv[j][k] = 1.0f;
+        bv[j][k] = 0.0f;
+      }
+      if (c < chunks) {
+        if (w) load_params<P, V>(w + c * V, wv[j]);
+        if (b) load_params<P, V>(b + c * V, bv[j]);
+      }
+    }
+    const float n = (float)N;
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) {
+      if (row0 + r >= rows) break;
+      // fp32: one-pass sum of squares (tensor.cpp:17577-17587), terms in element order
+      float s = 0.0f, ss = 0.0f;
+#pragma unroll
+      for (int j = 0; j < CPL; ++j) {
+        const uint32_t wd[4] = {hr[r][j].x, hr[r][j].y, hr[r][j].z, hr[r][j].w};
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          s = acc_add_half<false>(s, wd[q]);
+          ss = acc_add_sq_half<false>(ss, wd[q]);
+          s = acc_add_half<true>(s, wd[q]);
+          ss = acc_add_sq_half<true>(ss, wd[q]);
+        }
+      }
+      s = wave_sum(s);
+      ss = wave_sum(ss);
+      const float mean = s / n;
+      const float var = fmaxf(0.0f, ss / n - mean * mean);
+      const float inv = 1.0f / sqrtf(var + eps);
+      T* yr = y + (row0 + r) * N;
+      float o[CPL][V];
+      float amax = 0.0f;
+#pragma unroll
+      for (int j = 0; j < CPL; ++j) {
+        const uint32_t wd[4] = {hr[r][j].x, hr[r][j].y, hr[r][j].z, hr[r][j].w};
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          float t0 = acc_add_half<false>(-mean, wd[q]) * inv, t1 = acc_add_half<true>(-mean, wd[q]) * inv;
+          if (w) {
+            t0 = t0 * wv[j][2 * q];
+            t1 = t1 * wv[j][2 * q + 1];
+          }
+          if (b) {
+            t0 = t0 + bv[j][2 * q];
+            t1 = t1 + bv[j][2 * q + 1];
+          }
+          o[j][2 * q] = t0;
+          o[j][2 * q + 1] = t1;
+          amax = abs_max_nan(abs_max_nan(amax, t0), t1);
+        }
+      }
+      const bool redo = __builtin_amdgcn_ballot_w64(!(amax < 65520.0f)) != 0;
+#pragma unroll
+      for (int j = 0; j < CPL; ++j) {
+        const int c = lane + 64 * j;
+        if (c < chunks) {
+          uint4 st;
+          if (!redo) {
+            st = make_uint4(f2h_rtz_pack(o[j][0], o[j][1]), f2h_rtz_pack(o[j][2], o[j][3]), f2h_rtz_pack(o[j][4], o[j][5]),
+                            f2h_rtz_pack(o[j][6], o[j][7]));
+            *reinterpret_cast<uint4*>(yr + c * V) = st;
+          } else {
+            Vec16<T>::store(yr + c * V, o[j]);
+          }
+        }
+      }
+    }
+    return;
+  }
   float v[RPW][CPL][V];
 #pragma unroll
   for (int r = 0; r < RPW; ++r)
