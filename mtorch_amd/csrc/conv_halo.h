@@ -68,7 +68,7 @@ struct HaloArgs {
 // instructions gi with gi % NPW == P of every slot, and waits only for its own.  TR, PW: output
 // rows and patch row width of the unit (patch instruction gi holds patch pixels 8gi .. 8gi+7,
 // row-major).
-template <int LW, int LP, int SW, int NPW, int P, int TR, int PW>
+template <int LW, int LP, int SW, int NPW, int P, int TR, int PW, int PD>
 struct HaloSchedule {
   static constexpr int PPS = (LP + 6) / 7;
   static constexpr int patch_in(int tap) {
@@ -108,38 +108,54 @@ struct HaloSchedule {
     const int n = ((t / 3 + TR) * PW + 7) / 8;
     return n < LP ? n : LP;
   }
-  // The first channel block has no previous block to stream its patch under, so the prologue
-  // issues it in row order with each tap's rows ahead of that tap's weights (taps 0 .. SW-2),
-  // then the rest of the patch: step 0 waits for the top TR rows and its weights only, not for
-  // the whole patch.  Loads allowed in flight at the wait that precedes step T of that block:
+  // The first channel block has no previous block to stream its patch under.  Its loads go out
+  // in row order with each tap's rows ahead of that tap's weights (pre(k): taps k = 0 .. SW-2),
+  // then the rest of the patch; the prologue issues pre(0 .. PD-1) only, and the slot of step
+  // s issues pre(PD + s) (with the rest of the patch after pre(SW-2)) ahead of its own loads,
+  // so that step 0 waits only for the top TR rows and tap 0's weights and the first block's
+  // ~80 KB spread over its first slots instead of all being requested before step 0 can
+  // start.  Loads allowed in flight at the wait that precedes step T of that block:
   // everything this producer issued after its last load that step T reads.
   static constexpr int first_pending(int T) {
     int pos = 0, req = 0, pi = 0;
     const int nT = need(T);
-    for (int k = 0; k <= SW - 2; ++k) {
-      for (; pi < need(k); ++pi)
-        if (pi % NPW == P) {
-          ++pos;
-          if (pi < nT) req = pos;
-        }
-      for (int g = 0; g < LW; ++g)
-        if (g % NPW == P) {
-          ++pos;
-          if (k == T) req = pos;
-        }
-    }
-    for (; pi < LP; ++pi)
-      if (pi % NPW == P) {
-        ++pos;
-        if (pi < nT) req = pos;
+    for (int s = -1; s < T; ++s) {  // s = -1: the prologue; s >= 0: the slot of step s
+      int k_lo = 0, k_hi = 0;
+      bool rest = false;
+      if (s < 0) {
+        k_hi = PD;
+        rest = PD == SW - 1;
+      } else if (PD + s <= SW - 2) {
+        k_lo = PD + s;
+        k_hi = k_lo + 1;
+        rest = k_lo == SW - 2;
       }
-    for (int t = 0; t < T; ++t) {  // slots 0 .. T-1: block 1's patch part, then weights
-      pos += p_loads(t);
-      for (int g = 0; g < LW; ++g)
-        if (g % NPW == P) {
-          ++pos;
-          if (t + SW - 1 == T) req = pos;
-        }
+      for (int k = k_lo; k < k_hi; ++k) {
+        for (; pi < need(k); ++pi)
+          if (pi % NPW == P) {
+            ++pos;
+            if (pi < nT) req = pos;
+          }
+        for (int g = 0; g < LW; ++g)
+          if (g % NPW == P) {
+            ++pos;
+            if (k == T) req = pos;
+          }
+      }
+      if (rest)
+        for (; pi < LP; ++pi)
+          if (pi % NPW == P) {
+            ++pos;
+            if (pi < nT) req = pos;
+          }
+      if (s >= 0) {  // the slot's own loads: block 1's patch part, then the weights of step s + SW - 1
+        pos += p_loads(s);
+        for (int g = 0; g < LW; ++g)
+          if (g % NPW == P) {
+            ++pos;
+            if (s + SW - 1 == T) req = pos;
+          }
+      }
     }
     return pos - req;
   }
@@ -167,10 +183,12 @@ __global__ __launch_bounds__(64 * (4 + NPW)) void conv3x3_halo_kernel(const Halo
   constexpr int LW = BM / 8;            // weight DMA instructions per step
   constexpr int LP = (NP + 7) / 8;      // patch DMA instructions per channel block
   constexpr uint32_t WSTAGE = BM * 128, PBUF = LP * 8 * 128;
-  using Sched0 = HaloSchedule<LW, LP, SW, NPW, 0, TR, PW>;
+  constexpr int PD = 1;                 // pre(k) of the first block issued in the prologue
+  using Sched0 = HaloSchedule<LW, LP, SW, NPW, 0, TR, PW, PD>;
   static_assert(WGM * WGN == NW && WMO % 16 == 0 && WNP % 16 == 0 && TW % 4 == 0 && BM % 8 == 0, "tile shape");
   static_assert(SW >= 3 && SW <= 9 && 18 % SW == 0, "weight ring depth: 3, 6 or 9");
-  static_assert(Sched0::fits() && HaloSchedule<LW, LP, SW, NPW, NPW - 1, TR, PW>::fits(), "vmcnt range");
+  static_assert(Sched0::fits() && HaloSchedule<LW, LP, SW, NPW, NPW - 1, TR, PW, PD>::fits(), "vmcnt range");
+  static_assert(PD >= 1 && PD <= SW - 1 && SW - 1 - PD <= 5, "first-block loads outside slots 0 .. 4");
   static_assert(NPW >= 1 && NPW <= 2, "one or two producer waves");
   static_assert((size_t)(2 * PBUF + SW * WSTAGE) <= 160 * 1024, "LDS");
   static_assert(PBUF < 65536 && (SW - 1) * WSTAGE < 65536, "LDS read offsets are 16-bit immediates");
@@ -210,7 +228,7 @@ __global__ __launch_bounds__(64 * (4 + NPW)) void conv3x3_halo_kernel(const Halo
   // =============================================================================== producer
   auto producer = [&](auto p_c) {
     constexpr int P = decltype(p_c)::value;
-    using Sched = HaloSchedule<LW, LP, SW, NPW, P, TR, PW>;
+    using Sched = HaloSchedule<LW, LP, SW, NPW, P, TR, PW, PD>;
     const __amdgpu_buffer_rsrc_t x_rsrc =
         __builtin_amdgcn_make_buffer_rsrc((void*)args.x, (short)0, args.x_bytes, 0x00020000);
     const __amdgpu_buffer_rsrc_t w_rsrc =
@@ -266,26 +284,23 @@ __global__ __launch_bounds__(64 * (4 + NPW)) void conv3x3_halo_kernel(const Halo
       for (int gi = G0; gi < G1; ++gi)
         if (gi % NPW == P) dma16(x_rsrc, dst + gi * 1024, p_off[gi], soff);
     };
-    // prologue: block 0's patch in row order, the rows of tap k ahead of the weights of step k
-    // (k = 0 .. SW-2), then the rest of the patch (first_pending counts this order)
+    // block 0's patch in row order, the rows of tap k ahead of the weights of step k (pre(k),
+    // k = 0 .. SW-2), then the rest of the patch: pre(0 .. PD-1) here, the others in the first
+    // block's slots (first_pending counts this order)
     auto pre = [&](auto k_c) {
       constexpr int k = decltype(k_c)::value;
       issue_p(ic<k == 0 ? 0 : Sched::need(k - 1)>{}, ic<Sched::need(k)>{}, 0, 0);
       issue_w(0, k, k);
+      if constexpr (k == SW - 2) issue_p(ic<Sched::need(SW - 2)>{}, ic<LP>{}, 0, 0);
     };
     pre(ic<0>{});
-    pre(ic<1>{});
-    if constexpr (SW > 3) {
-      pre(ic<2>{});
-      pre(ic<3>{});
-      pre(ic<4>{});
-    }
-    if constexpr (SW > 6) {
-      pre(ic<5>{});
-      pre(ic<6>{});
-      pre(ic<7>{});
-    }
-    issue_p(ic<Sched::need(SW - 2)>{}, ic<LP>{}, 0, 0);
+    if constexpr (PD > 1) pre(ic<1>{});
+    if constexpr (PD > 2) pre(ic<2>{});
+    if constexpr (PD > 3) pre(ic<3>{});
+    if constexpr (PD > 4) pre(ic<4>{});
+    if constexpr (PD > 5) pre(ic<5>{});
+    if constexpr (PD > 6) pre(ic<6>{});
+    if constexpr (PD > 7) pre(ic<7>{});
     // step s = 9j + T of a block of parity JP: wait for step s's operands, the barrier that
     // opens step s, then slot s
     auto slot = [&](int j, auto jp_c, auto t_c, auto first_c) {
@@ -296,6 +311,7 @@ __global__ __launch_bounds__(64 * (4 + NPW)) void conv3x3_halo_kernel(const Halo
       constexpr int PEND = decltype(first_c)::value ? Sched::first_pending(T) : Sched::pending(T);
       __builtin_amdgcn_s_waitcnt(vmcnt_only(PEND));
       __builtin_amdgcn_s_barrier();
+      if constexpr (decltype(first_c)::value && PD + T <= SW - 2) pre(ic<PD + T>{});
       if constexpr (Sched::patch_in(T) > 0)
         issue_p(ic<T * PPS>{}, ic<T * PPS + Sched::patch_in(T)>{}, j + 1, 1 - JP);
       issue_w(j + WC, WT, STAGE);
