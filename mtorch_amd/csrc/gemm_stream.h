@@ -121,24 +121,23 @@ __global__ __launch_bounds__((BT / 16 + BT / 64) * 64) void gemm_stream_kernel(c
     uint32_t w_off[LW], a_off[LA];
     uint32_t iu = u_begin;  // unit and step of the next load
     int ij = 0, k0 = 0;
+    // Lane l covers row 8gi + l/8 of load gi and 16-byte chunk (l & 7) ^ ((row >> 1) & 7), which
+    // is (l & 7) ^ (l / 16) ^ 4(gi & 1) (8 | 8gi, and BC = 80 is a multiple of 16): per unit one
+    // multiply per operand, the rest wave-uniform steps.
+    const int l3 = lane >> 3;
+    const uint32_t chunk0 = (uint32_t)((lane & 7) ^ (lane >> 4)) * 16u;
+    const uint32_t ldb2 = (uint32_t)args.ldb * 2u, lda2 = (uint32_t)args.lda * 2u;
     auto set_unit = [&]() {
       const bool live = iu < u_end;
       const Unit un = decode(live ? iu : u_begin);
       k0 = un.split * steps;
+      const uint32_t wl = (uint32_t)(un.n0 + l3) * ldb2, al = (uint32_t)(un.m0 + l3) * lda2;
 #pragma unroll
-      for (int gi = 0; gi < LW; ++gi) {
-        const int r = gi * 8 + (lane >> 3);
-        const int c = (lane & 7) ^ ((r >> 1) & 7);
-        const int n = un.n0 + r;
-        w_off[gi] = (live && n < N) ? ((uint32_t)n * (uint32_t)args.ldb + (uint32_t)c * 8u) * 2u : kOOB;
-      }
+      for (int gi = 0; gi < LW; ++gi)
+        w_off[gi] = (live && un.n0 + gi * 8 + l3 < N) ? wl + (uint32_t)(gi * 8) * ldb2 + (chunk0 ^ (gi & 1 ? 64u : 0u)) : kOOB;
 #pragma unroll
-      for (int gi = 0; gi < LA; ++gi) {
-        const int r = BC + gi * 8 + (lane >> 3);
-        const int c = (lane & 7) ^ ((r >> 1) & 7);
-        const int m = un.m0 + gi * 8 + (lane >> 3);
-        a_off[gi] = (live && m < M) ? ((uint32_t)m * (uint32_t)args.lda + (uint32_t)c * 8u) * 2u : kOOB;
-      }
+      for (int gi = 0; gi < LA; ++gi)
+        a_off[gi] = (live && un.m0 + gi * 8 + l3 < M) ? al + (uint32_t)(gi * 8) * lda2 + (chunk0 ^ (gi & 1 ? 64u : 0u)) : kOOB;
     };
     // this producer's share of one step's loads into ring stage `stage` (past the last unit:
     // out-of-range, zeros)
