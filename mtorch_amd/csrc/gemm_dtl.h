@@ -130,22 +130,25 @@ __global__ __launch_bounds__(256) void gemm_dtl_kernel(const GemmArgs args) {
     b_rsrc = __builtin_amdgcn_make_buffer_rsrc(
         (void*)(reinterpret_cast<const T*>(args.b) + (MODE == MODE_CONV ? 0 : un.bz * args.stride_b)), (short)0,
         (int)args.b_bytes, 0x00020000);
-    const uint32_t lda = (uint32_t)args.lda;
+    // Row r = (wave*I + i)*8 + l/8 of instruction i: its chunk is (l & 7) ^ (l / 16) ^ 4 when
+    // wave*I + i is odd (8 | 8(wave*I + i)), so the byte offset is one per-lane multiply plus
+    // wave-uniform steps.
+    const uint32_t lda2 = (uint32_t)args.lda * 2u;
+    const uint32_t a_lane = (uint32_t)(m0 + dma_row(AI, 0)) * lda2;
 #pragma unroll
     for (int i = 0; i < AI; ++i) {
       const int r = dma_row(AI, i), c = dma_chunk(r);
-      const int row = m0 + r;
       a_kc[i] = c * 8;
-      a_off[i] = row < M && !dead ? ((uint32_t)row * lda + (uint32_t)(c * 8)) * 2u : kOOB;
+      a_off[i] = m0 + r < M && !dead ? a_lane + (uint32_t)(i * 8) * lda2 + (uint32_t)c * 16u : kOOB;
     }
     if constexpr (MODE == MODE_NT) {
-      const uint32_t ldb = (uint32_t)args.ldb;
+      const uint32_t ldb2 = (uint32_t)args.ldb * 2u;
+      const uint32_t b_lane = (uint32_t)(n0 + dma_row(BI, 0)) * ldb2;
 #pragma unroll
       for (int i = 0; i < BI; ++i) {
         const int r = dma_row(BI, i), c = dma_chunk(r);
-        const int row = n0 + r;
         b_kc[i] = c * 8;
-        b_off[i] = row < N && !dead ? ((uint32_t)row * ldb + (uint32_t)(c * 8)) * 2u : kOOB;
+        b_off[i] = n0 + r < N && !dead ? b_lane + (uint32_t)(i * 8) * ldb2 + (uint32_t)c * 16u : kOOB;
       }
     } else {
       const int H = (int)args.H, W = (int)args.W, KW = (int)args.KW, KH = (int)args.KH_, Cp = (int)args.Cp;
