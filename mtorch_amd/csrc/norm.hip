@@ -1044,9 +1044,15 @@ __global__ __launch_bounds__(256) void softmax_long_kernel(const T* __restrict__
   }
 }
 
+// Halves of the one-launch GroupNorm's LDS tile: a whole group of up to 5 chunks per part, else
+// a 64 KB share ([gc][HW / NSPLIT + 8] rows, checked by the launcher), so two workgroups of any
+// instance fit one CU's LDS.
+constexpr int gn1_tile_halves(int cpt) { return (cpt <= 5 ? 4 * cpt * 2048 : 32768) + 4096; }
+
 // Channels-last GroupNorm (+ SiLU) of fp16 NCHW input in ONE launch, for groups of at most
-// 4 * CPT stats chunks of <= 2048 elements (every SD group up to 40960 elements): NSPLIT
-// 1024-thread workgroups per (sample, group), each covering HW / NSPLIT pixels of it.
+// 4 * CPT stats chunks of <= 2048 elements (every SD group, the up-block concatenations up to
+// 122880 elements included): NSPLIT 1024-thread workgroups per (sample, group), each covering
+// HW / NSPLIT pixels of it.
 //  phase 1: every workgroup reads the whole group (its chunks replayed as the stats kernel's
 //           workgroups sum them: thread t of part p takes vector t of chunks p, p + 4, ...;
 //           the same per-thread sums, wave butterflies and four-wave combine), keeping the
@@ -1069,7 +1075,7 @@ __global__ __launch_bounds__(1024) void group_norm_nhwc_onepass_kernel(
     float eps, int fuse_silu, int unit, FastDiv div_hw, FastDiv div_units, int xcd_map) {
   constexpr int V = 8;
   constexpr int NPART = 4;
-  constexpr int TILE = NPART * CPT * 2048 + 4096;  // halves: this workgroup's [gc][px + 8] rows
+  constexpr int TILE = gn1_tile_halves(CPT);  // halves: this workgroup's [gc][px + 8] rows
   __shared__ __align__(16) uint16_t tile[TILE];
   __shared__ float red_s[NPART * CPT][4], red_ss[NPART * CPT][4];
   __shared__ float2 ch_s[256];  // per channel: (scale, shift) for fp16 parameters, (gamma, beta) for fp32
@@ -1273,7 +1279,7 @@ bool gn_single_enabled() {
 }
 
 // The one-launch channels-last GroupNorm (group_norm_nhwc_onepass_kernel) where it applies: fp16
-// data with whole 16-byte vectors, an even channel count per group (<= 256), at most 20 stats
+// data with whole 16-byte vectors, an even channel count per group (<= 256), at most 60 stats
 // chunks per group.  Returns -1 when it does not apply.  Workgroups per group: MTHIP_GN1_SPLIT,
 // else 4, 2 or 1 -- the most that keep the grid within two workgroups per CU.  MTHIP_GN_ONEPASS=0
 // turns it off (the two-kernel path then runs).
@@ -1284,9 +1290,10 @@ int try_gn_onepass(int device, const GnSource<uint16_t>& src, const P* gamma, co
   if (const char* e = std::getenv("MTHIP_GN_ONEPASS"))
     if (e[0] == '0') return -1;
   const int64_t gc = C / groups;
-  if (gc % 2 != 0 || gc > 256 || splits > 20 || chunk > 2048 || Cp % 8 != 0 || HW % 8 != 0) return -1;
+  if (gc % 2 != 0 || gc > 256 || splits > 60 || chunk > 2048 || Cp % 8 != 0 || HW % 8 != 0) return -1;
   const int cpt = (int)ceil_div(splits, 4);
-  const int tile_halves = 4 * (cpt <= 2 ? 2 : cpt <= 4 ? 4 : 5) * 2048 + 4096;
+  const int cpt_inst = cpt <= 2 ? 2 : cpt <= 4 ? 4 : cpt <= 5 ? 5 : cpt <= 8 ? 8 : 15;
+  const int tile_halves = gn1_tile_halves(cpt_inst);
   const int64_t n_groups = B * groups;
   const int cus = gn_cu_count(device);
   int nsplit = 1;
@@ -1310,13 +1317,17 @@ int try_gn_onepass(int device, const GnSource<uint16_t>& src, const P* gamma, co
                      gamma, beta, y, raw, (int)C, (int)Cp, (int)groups, (int)HW, (int)group_size, (int)chunk,   \
                      (int)splits, nsplit, eps, fuse_silu, unit, div_hw, div_units, xcd_map)
   if (cat) {
-    if (cpt <= 2) MTHIP_GN1(2, true);
-    else if (cpt <= 4) MTHIP_GN1(4, true);
-    else MTHIP_GN1(5, true);
+    if (cpt_inst == 2) MTHIP_GN1(2, true);
+    else if (cpt_inst == 4) MTHIP_GN1(4, true);
+    else if (cpt_inst == 5) MTHIP_GN1(5, true);
+    else if (cpt_inst == 8) MTHIP_GN1(8, true);
+    else MTHIP_GN1(15, true);
   } else {
-    if (cpt <= 2) MTHIP_GN1(2, false);
-    else if (cpt <= 4) MTHIP_GN1(4, false);
-    else MTHIP_GN1(5, false);
+    if (cpt_inst == 2) MTHIP_GN1(2, false);
+    else if (cpt_inst == 4) MTHIP_GN1(4, false);
+    else if (cpt_inst == 5) MTHIP_GN1(5, false);
+    else if (cpt_inst == 8) MTHIP_GN1(8, false);
+    else MTHIP_GN1(15, false);
   }
 #undef MTHIP_GN1
   return check_launch("group_norm_nhwc_onepass_kernel");

@@ -938,6 +938,10 @@ GN1_CASES = [
     (2, 1280, 640, 16, 16, 32, "float32", 1, None),
     (2, 1280, 1280, 16, 16, 32, "float32", 1, None),
     (2, 1280, 1280, 8, 8, 32, "float32", 1, "4"),
+    (2, 640, 320, 64, 64, 32, "float32", 1, None),  # 60 stats chunks per group (15 per part)
+    (2, 320, 320, 64, 64, 32, "float32", 1, None),  # 40
+    (2, 1280, 640, 32, 32, 32, "float32", 1, None),  # 30 (8 per part)
+    (1, 640, 0, 64, 64, 32, "float16", 1, None),  # 40, one source, against the oracle too
     (3, 36, 0, 12, 20, 6, "float16", 1, None),  # channel padding (Cp 40 > C), 6-channel groups
     (1, 18, 22, 8, 8, 4, "float16", 1, None),  # a group straddling the two sources
     (4, 64, 0, 16, 24, 8, "float16", 1, None),  # 16-byte stores (8-channel groups)
