@@ -764,14 +764,15 @@ def group_norm_silu_conv2d_cat(x0: Tensor, x1: Tensor, num_groups: int, gn_weigh
     concatenated copy -- mthip_group_norm_nhwc_cat reads x0 and x1 in place and writes both the
     normalised activation and x itself channels-last, and the two convs read those.  Values
     equal the unfused cat -> group_norm -> silu -> conv2d / conv2d sequence's bit for bit.
-    Returns None when the inputs do not fit the channels-last fp16 kernel (the caller then
-    concatenates)."""
-    if x0.dtype is not T.float16 or x1.dtype is not T.float16 or x0.dim() != 4 or x1.dim() != 4:
+    x1 = None: x = x0 (a ResBlock with a shortcut conv and one input; the shortcut then reads
+    the GroupNorm's channels-last copy instead of a separate layout change).  Returns None when
+    the inputs do not fit the channels-last fp16 kernel (the caller then concatenates)."""
+    if x0.dtype is not T.float16 or x0.dim() != 4 or (x1 is not None and (x1.dtype is not T.float16 or x1.dim() != 4)):
         return None
     B, C0, H, W = x0.shape
-    C1 = x1.shape[1]
+    C1 = x1.shape[1] if x1 is not None else 0
     C = C0 + C1
-    if list(x1.shape) != [B, C1, H, W] or C % 8 or C0 % 2 or (H * W) % 8 or C % num_groups:
+    if (x1 is not None and list(x1.shape) != [B, C1, H, W]) or C % 8 or C0 % 2 or (H * W) % 8 or C % num_groups:
         return None
     pdt = _norm_param_dtype("group_norm", x0, gn_weight, gn_bias)
     _same_dtype("conv2d", [x0, x1, w, b, chan_add, shortcut_w, shortcut_b], "tensors")
@@ -798,7 +799,8 @@ def group_norm_silu_conv2d_cat(x0: Tensor, x1: Tensor, num_groups: int, gn_weigh
     xn = T._DeviceBuffer(B * H * W * C * 2, dev)
     raw = T._DeviceBuffer(B * H * W * C * 2, dev)
     _lib.check(L.mthip_group_norm_nhwc_cat(dev, x0.dtype.code, x0.contiguous().data_ptr(), C0,
-                                           x1.contiguous().data_ptr(), C1, _ptr(_contig(gn_weight)),
+                                           x1.contiguous().data_ptr() if x1 is not None else None, C1,
+                                           _ptr(_contig(gn_weight)),
                                            _ptr(_contig(gn_bias)), xn.ptr, raw.ptr, B, H * W, num_groups, float(eps), 1,
                                            pdt))
     wp = _conv_packed_weight(w.contiguous(), dev, O, C, KH, KW)

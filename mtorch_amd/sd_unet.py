@@ -146,10 +146,18 @@ class ResBlock(nn.Module):
         n1, n2 = self.norm1, self.norm2
         if t is None:
             t = F.linear(temb_silu, self.time_emb_proj.weight, self.time_emb_proj.bias)
-        # h = conv1(silu(norm1(x))) + t[:, :, None, None], the add in conv1's epilogue
-        h = F.group_norm_silu_conv2d(x, n1.groups, n1.weight, n1.bias, n1.eps, self.conv1.weight, self.conv1.bias,
-                                     padding=1, chan_add=t)
-        res = F.conv2d(x, self.shortcut.weight, self.shortcut.bias) if self.shortcut is not None else x
+        r = None
+        if self.shortcut is not None:
+            # the GroupNorm also writes x channels-last for the shortcut conv
+            r = _ops.group_norm_silu_conv2d_cat(x, None, n1.groups, n1.weight, n1.bias, n1.eps, self.conv1.weight,
+                                                self.conv1.bias, 1, t, self.shortcut.weight, self.shortcut.bias)
+        if r is not None:
+            h, res = r
+        else:
+            # h = conv1(silu(norm1(x))) + t[:, :, None, None], the add in conv1's epilogue
+            h = F.group_norm_silu_conv2d(x, n1.groups, n1.weight, n1.bias, n1.eps, self.conv1.weight,
+                                         self.conv1.bias, padding=1, chan_add=t)
+            res = F.conv2d(x, self.shortcut.weight, self.shortcut.bias) if self.shortcut is not None else x
         return F.group_norm_silu_conv2d(h, n2.groups, n2.weight, n2.bias, n2.eps, self.conv2.weight, self.conv2.bias,
                                         padding=1, residual=res)
 

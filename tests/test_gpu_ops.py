@@ -1178,30 +1178,35 @@ def test_group_norm_silu_conv2d_channel_add_is_the_separate_add(dt, B, C, H, W, 
 
 @pytest.mark.parametrize("B,C0,C1,H,W,O,G,pdt", [(2, 640, 320, 16, 16, 320, 32, "float16"),
                                                  (2, 64, 64, 8, 8, 48, 32, "float16"),
-                                                 (1, 48, 16, 9, 8, 32, 8, "float32")])
+                                                 (1, 48, 16, 9, 8, 32, 8, "float32"),
+                                                 (1, 320, 0, 32, 32, 640, 32, "float16"),
+                                                 (1, 640, 0, 16, 16, 1280, 32, "float16")])
 def test_group_norm_silu_conv2d_cat_equals_cat_then_ops(B, C0, C1, H, W, O, G, pdt):
     """An up-block ResBlock entry on cat([x0, x1], dim=1) read in place (groups straddling the
     two inputs at C0=640, C1=320: 30-channel groups) gives the explicit cat -> GN -> SiLU -> conv
     (+ time add) and the 1x1 shortcut conv on the concatenation bit for bit, and the oracle's
-    values; fp32 GN parameters are the upcast pattern."""
+    values; fp32 GN parameters are the upcast pattern.  C1 = 0 (x1 None): the down-block
+    ResBlocks whose shortcut reads the GroupNorm's channels-last copy of their one input."""
     from mtorch_amd import _ops
 
     g = Gen(B * 300 + C0 + C1 + O)
-    x0, x1 = g.randn((B, C0, H, W), "float16"), g.randn((B, C1, H, W), "float16")
+    x0 = g.randn((B, C0, H, W), "float16")
+    x1 = g.randn((B, C1, H, W), "float16") if C1 else None
     C = C0 + C1
     gamma, beta = g.randn((C,), pdt), g.randn((C,), pdt)
     w, b = g.randn((O, C, 3, 3), "float16", 1.0 / np.sqrt(9 * C)), g.randn((O,), "float16")
     sw, sb = g.randn((O, C, 1, 1), "float16", 1.0 / np.sqrt(C)), g.randn((O,), "float16")
     t = dev(g.randn((B, O), "float16"))
-    xd = mt.cat([dev(x0), dev(x1)], dim=1)
+    xd = mt.cat([dev(x0), dev(x1)], dim=1) if C1 else dev(x0)
+    x1d = dev(x1) if C1 else None
     args = (G, dev(gamma), dev(beta), 1e-5)
-    r = _ops.group_norm_silu_conv2d_cat(dev(x0), dev(x1), *args, dev(w), dev(b), 1, t, dev(sw), dev(sb))
+    r = _ops.group_norm_silu_conv2d_cat(dev(x0), x1d, *args, dev(w), dev(b), 1, t, dev(sw), dev(sb))
     assert r is not None
     out, sc = r
     ref_out = F.group_norm_silu_conv2d(xd, *args, dev(w), dev(b), padding=1, chan_add=t)
     ref_sc = F.conv2d(xd, dev(sw), dev(sb))
     assert np.array_equal(host(out), host(ref_out)) and np.array_equal(host(sc), host(ref_sc))
-    xc = np.concatenate([x0, x1], axis=1)
+    xc = np.concatenate([x0, x1], axis=1) if C1 else x0
     if pdt == "float16":
         h = orc.silu(orc.group_norm(xc, G, gamma, beta, 1e-5))
     else:
@@ -1210,7 +1215,7 @@ def test_group_norm_silu_conv2d_cat_equals_cat_then_ops(B, C0, C1, H, W, O, G, p
     assert rel(val(host(out)), ref) <= 1e-2
     assert rel(val(host(sc)), val(orc.conv2d(xc, sw, sb))) <= 1e-2
     # shapes the channels-last fp16 kernel cannot take are declined (the caller concatenates)
-    assert _ops.group_norm_silu_conv2d_cat(dev(x0)[:, :C0 - 1], dev(x1), *args, dev(w), dev(b), 1, t, dev(sw),
+    assert _ops.group_norm_silu_conv2d_cat(dev(x0)[:, :C0 - 1], x1d, *args, dev(w), dev(b), 1, t, dev(sw),
                                            dev(sb)) is None
 
 
