@@ -240,6 +240,13 @@ int mthip_conv2d_prepacked(int device, int dtype, const void* x, const void* wp,
                            int64_t B, int64_t C, int64_t H, int64_t W, int64_t O, int64_t KH, int64_t KW,
                            int64_t stride_h, int64_t stride_w, int64_t pad_h, int64_t pad_w,
                            int64_t dil_h, int64_t dil_w, const void* residual);
+/* Nearest 2x upsampling of NCHW x[B][C][H][W] written channels-last with Cp >= C channels
+ * (padding channels zero), xp[B][2H*2W][Cp]: interpolate(scale_factor=2, mode="nearest")
+ * (tensor.cpp:10897) and the layout change ahead of mthip_conv2d_nhwc in one pass -- the SD
+ * decoder's Upsample block (upsample, then conv2d 3x3, tensor.cpp:26490). */
+int mthip_upsample2x_to_nhwc(int device, int dtype, const void* x, void* xp, int64_t B, int64_t C,
+                             int64_t Cp, int64_t H, int64_t W);
+
 /* The same conv with the input already channels-last: x_nhwc[B][H][W][Cp] (Cp as for the
  * packed weight, channels C..Cp-1 zero), e.g. as written by mthip_group_norm_nhwc; the output
  * (and residual) stay NCHW.  This is the GroupNorm -> SiLU -> conv hand-off of every SD ResNet

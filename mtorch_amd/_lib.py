@@ -69,6 +69,7 @@ _SIGNATURES = {
     "mthip_conv2d_pack_weight": (_int, [_int, _int, _c_void_p, _c_void_p, _i64, _i64, _i64, _i64]),
     "mthip_conv2d_prepacked": (_int, [_int, _int, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i64,
                                       _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _c_void_p]),
+    "mthip_upsample2x_to_nhwc": (_int, [_int, _int, _c_void_p, _c_void_p, _i64, _i64, _i64, _i64, _i64]),
     "mthip_conv2d_nhwc": (_int, [_int, _int, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i64,
                                  _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _c_void_p,
                                  _c_void_p, _i64]),

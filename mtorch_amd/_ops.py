@@ -813,6 +813,36 @@ def group_norm_silu_conv2d_cat(x0: Tensor, x1: Tensor, num_groups: int, gn_weigh
     return out, sc
 
 
+def upsample2x_conv2d(x: Tensor, w: Tensor, b: Tensor = None, padding=1) -> Tensor:
+    """conv2d(interpolate(x, scale_factor=2, mode="nearest"), w, b, padding=padding) for fp16 NCHW
+    x whose channel count is a whole number of 16-byte chunks: mthip_upsample2x_to_nhwc writes
+    the upsampled input channels-last in one pass (no NCHW upsampled copy, no separate layout
+    change) and mthip_conv2d_nhwc convolves it -- the SD decoder's Upsample block, bit for bit
+    the two-op sequence.  Returns None where it does not apply (the caller runs the two ops)."""
+    if x.dtype is not T.float16 or x.dim() != 4 or w.dim() != 4 or x.shape[1] % 8:
+        return None
+    _same_dtype("conv2d", [x, w, b], "tensors")
+    dev = _gpu("conv2d", x, w, b)
+    B, C, H, W = x.shape
+    O, KH, KW = w.shape[0], w.shape[2], w.shape[3]
+    if w.shape[1] != C:
+        return None
+    ph, pw = _pair(padding, "padding")
+    H2, W2 = 2 * H, 2 * W
+    OH, OW = H2 + 2 * ph - KH + 1, W2 + 2 * pw - KW + 1
+    if OH <= 0 or OW <= 0:
+        return None
+    out = _empty([B, O, OH, OW], x.dtype, dev)
+    L = _L()
+    xp = T._DeviceBuffer(B * H2 * W2 * C * 2, dev)
+    _lib.check(L.mthip_upsample2x_to_nhwc(dev, x.dtype.code, x.contiguous().data_ptr(), xp.ptr, B, C, C, H, W))
+    wp = _conv_packed_weight(w.contiguous(), dev, O, C, KH, KW)
+    _lib.check(L.mthip_conv2d_nhwc(dev, x.dtype.code, xp.ptr, wp, _ptr(_contig(b)), out.data_ptr(), B, C, H2, W2, O,
+                                   KH, KW, 1, 1, ph, pw, 1, 1, None, None, 0))
+    del xp  # stream-ordered free: reused only by later work
+    return out
+
+
 def conv2d_tokens(tok: Tensor, w: Tensor, b: Tensor, H: int, W: int, residual: Tensor = None) -> Tensor:
     """1x1 conv of a channels-last token tensor tok[B, H*W, C] to NCHW [B, O, H, W] (+ residual):
     conv2d(tok.reshape(B, H, W, C).permute(0, 3, 1, 2), w, b) without the permute -- the proj_out

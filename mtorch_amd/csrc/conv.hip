@@ -44,6 +44,39 @@ __global__ void nchw_to_nhwc_pad_kernel(const T* __restrict__ x, T* __restrict__
   }
 }
 
+// Nearest 2x upsampling of NCHW x[B][C][H][W] written channels-last: xp[b][(2y+dy)*2W + 2x+dx][c]
+// = x[b][c][y][x] (0 for c >= C) -- interpolate(scale_factor=2, mode="nearest") and the conv's
+// layout change in one pass.  A 32-pixel x 32-channel tile of x goes through LDS; each element
+// is stored at its four output pixels.
+template <typename T>
+__global__ void upsample2x_to_nhwc_pad_kernel(const T* __restrict__ x, T* __restrict__ xp, int64_t C, int64_t Cp,
+                                              int64_t H, int64_t W) {
+  __shared__ T tile[32][33];
+  const int64_t b = blockIdx.z, HW = H * W;
+  const int64_t hw0 = (int64_t)blockIdx.x * 32, c0 = (int64_t)blockIdx.y * 32;
+  const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;
+  for (int j = ty; j < 32; j += 8) {
+    const int64_t c = c0 + j, hw = hw0 + tx;
+    T v = T(0);
+    if (c < C && hw < HW) v = x[(b * C + c) * HW + hw];
+    tile[j][tx] = v;
+  }
+  __syncthreads();
+  const int64_t W2 = 2 * W;
+  for (int j = ty; j < 32; j += 8) {
+    const int64_t hw = hw0 + j, c = c0 + tx;
+    if (hw < HW && c < Cp) {
+      const int64_t yy = hw / W, xx = hw - yy * W;
+      T* dst = xp + ((b * 4 * HW) + 2 * yy * W2 + 2 * xx) * Cp + c;
+      const T v = tile[tx][j];
+      dst[0] = v;
+      dst[Cp] = v;
+      dst[W2 * Cp] = v;
+      dst[W2 * Cp + Cp] = v;
+    }
+  }
+}
+
 // wp[o][ky][kx][cp] = w[o][c][ky][kx] (0 for c >= C).
 template <typename T>
 __global__ void pack_weight_kernel(const T* __restrict__ w, T* __restrict__ wp, int64_t O, int64_t C, int64_t Cp,
@@ -389,6 +422,25 @@ extern "C" int mthip_conv2d_prepacked(int device, int dtype, const void* x, cons
                                    pad_w, dil_h, dil_w, residual, s);
   return run_conv_gemm<float>(device, dtype, x, wp, b, y, B, C, H, W, O, KH, KW, stride_h, stride_w, pad_h, pad_w,
                               dil_h, dil_w, residual, s);
+}
+
+extern "C" int mthip_upsample2x_to_nhwc(int device, int dtype, const void* x, void* xp, int64_t B, int64_t C,
+                                        int64_t Cp, int64_t H, int64_t W) {
+  MTHIP_REQUIRE(dtype == MTHIP_F16 || dtype == MTHIP_F32, "mthip_upsample2x_to_nhwc: dtype must be F16 or F32");
+  MTHIP_REQUIRE(B >= 0 && C > 0 && Cp >= C && H > 0 && W > 0 && B <= 65535, "mthip_upsample2x_to_nhwc: bad extents");
+  MTHIP_REQUIRE(B * 4 * H * W * Cp < (int64_t(1) << 40), "mthip_upsample2x_to_nhwc: output too large");
+  if (B == 0) return MTHIP_OK;
+  hipStream_t s = stream_for(device);
+  if (!s) return MTHIP_ERR_HIP;
+  if (int rc = use_device(device)) return rc;
+  dim3 grid((unsigned)ceil_div(H * W, 32), (unsigned)ceil_div(Cp, 32), (unsigned)B);
+  if (dtype == MTHIP_F16)
+    hipLaunchKernelGGL(upsample2x_to_nhwc_pad_kernel<uint16_t>, grid, dim3(256), 0, s, (const uint16_t*)x,
+                       (uint16_t*)xp, C, Cp, H, W);
+  else
+    hipLaunchKernelGGL(upsample2x_to_nhwc_pad_kernel<float>, grid, dim3(256), 0, s, (const float*)x, (float*)xp, C,
+                       Cp, H, W);
+  return check_launch("upsample2x_to_nhwc_pad_kernel");
 }
 
 extern "C" int mthip_conv2d_nhwc(int device, int dtype, const void* x_nhwc, const void* wp, const void* b, void* y,

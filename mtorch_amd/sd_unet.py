@@ -250,6 +250,9 @@ class Upsample(nn.Module):
         self.conv = _Conv(init, C, C, 3)
 
     def forward(self, x):
+        y = _ops.upsample2x_conv2d(x, self.conv.weight, self.conv.bias, padding=1)
+        if y is not None:
+            return y
         return F.conv2d(F.interpolate(x, scale_factor=2, mode="nearest"), self.conv.weight, self.conv.bias, padding=1)
 
 

@@ -1219,6 +1219,33 @@ def test_group_norm_silu_conv2d_cat_equals_cat_then_ops(B, C0, C1, H, W, O, G, p
                                            dev(sb)) is None
 
 
+@pytest.mark.parametrize("B,C,H,W,O", [(2, 1280, 8, 8, 1280), (2, 1280, 16, 16, 1280), (1, 640, 32, 32, 640),
+                                         (1, 24, 5, 7, 16)])
+def test_upsample2x_conv2d_equals_interpolate_then_conv(B, C, H, W, O):
+    """The SD decoder's Upsample block through mthip_upsample2x_to_nhwc + the channels-last conv
+    gives interpolate(nearest, x2) -> conv2d 3x3 bit for bit (the halo kernel at 16x16, 32x32
+    and 64x64 outputs, the implicit GEMM for a ragged small one); the staging entry itself
+    against numpy's repeat + transpose, with zero padding channels (Cp > C), for fp16 and fp32."""
+    from mtorch_amd import _lib, _ops
+
+    g = Gen(B * 17 + C + H * 5 + W + O)
+    x = g.randn((B, C, H, W), "float16")
+    w, b = g.randn((O, C, 3, 3), "float16", 1.0 / np.sqrt(9 * C)), g.randn((O,), "float16")
+    got = _ops.upsample2x_conv2d(dev(x), dev(w), dev(b), padding=1)
+    assert got is not None
+    ref = F.conv2d(F.interpolate(dev(x), scale_factor=2, mode="nearest"), dev(w), dev(b), padding=1)
+    assert np.array_equal(host(got).view(np.uint16), host(ref).view(np.uint16))
+    L = _lib.lib()
+    for dt, code in (("float16", _lib.F16), ("float32", _lib.F32)):
+        xs = g.randn((B, C, H, W), dt)
+        Cp = C + 8
+        xp = mt.full((B, 4 * H * W, Cp), 7.0, dtype=getattr(mt, dt), device="cuda")
+        _lib.check(L.mthip_upsample2x_to_nhwc(0, code, dev(xs).data_ptr(), xp.data_ptr(), B, C, Cp, H, W))
+        up = xs.repeat(2, axis=2).repeat(2, axis=3).reshape(B, C, 4 * H * W).transpose(0, 2, 1)
+        want = np.concatenate([up, np.zeros((B, 4 * H * W, 8), up.dtype)], axis=2)
+        assert np.array_equal(host(xp), want)
+
+
 @pytest.mark.parametrize("shape,groups", [((2, 320, 64, 64), 32), ((1, 640, 16, 16), 32), ((2, 64, 7, 9), 8)])
 def test_group_norm_silu_fp16_equals_group_norm_then_silu(shape, groups):
     """The fused fp16 GroupNorm+SiLU (SiLU applied to the narrowed halves) writes exactly the
