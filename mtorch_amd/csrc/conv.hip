@@ -77,6 +77,41 @@ __global__ void upsample2x_to_nhwc_pad_kernel(const T* __restrict__ x, T* __rest
   }
 }
 
+// The same layout change for 16-bit data with HW and Cp multiples of 8, in 16-byte pieces: a
+// 64-pixel x 64-channel tile read as 8-pixel runs of one channel, written as 8-channel runs of
+// one pixel (the scalar kernel above moves 2 bytes per lane each way).
+__global__ __launch_bounds__(256) void nchw_to_nhwc_pad_vec_kernel(const uint16_t* __restrict__ x,
+                                                                   uint16_t* __restrict__ xp, int64_t C, int64_t Cp,
+                                                                   int64_t HW) {
+  constexpr int PITCH = 72;  // halves per LDS channel row (16-byte multiple)
+  __shared__ __align__(16) uint16_t tile[64 * PITCH];
+  const int64_t b = blockIdx.z;
+  const int64_t hw0 = (int64_t)blockIdx.x * 64, c0 = (int64_t)blockIdx.y * 64;
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    const int v = (int)threadIdx.x + 256 * r;
+    const int cl = v >> 3, pv = v & 7;
+    const int64_t c = c0 + cl, p = hw0 + pv * 8;
+    uint4 d = make_uint4(0u, 0u, 0u, 0u);
+    if (c < C && p < HW) d = *reinterpret_cast<const uint4*>(x + (b * C + c) * HW + p);
+    *reinterpret_cast<uint4*>(&tile[cl * PITCH + pv * 8]) = d;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    const int v = (int)threadIdx.x + 256 * r;
+    const int pl = v >> 3, cv = v & 7;
+    const int64_t p = hw0 + pl, c = c0 + cv * 8;
+    if (p < HW && c < Cp) {
+      uint32_t w[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        w[i] = (uint32_t)tile[(cv * 8 + 2 * i) * PITCH + pl] | ((uint32_t)tile[(cv * 8 + 2 * i + 1) * PITCH + pl] << 16);
+      *reinterpret_cast<uint4*>(xp + (b * HW + p) * Cp + c) = make_uint4(w[0], w[1], w[2], w[3]);
+    }
+  }
+}
+
 // wp[o][ky][kx][cp] = w[o][c][ky][kx] (0 for c >= C).
 template <typename T>
 __global__ void pack_weight_kernel(const T* __restrict__ w, T* __restrict__ wp, int64_t O, int64_t C, int64_t Cp,
@@ -331,9 +366,17 @@ int run_conv_gemm(int device, int dtype, const void* x, const void* wp, const vo
     return fail(MTHIP_ERR_UNSUPPORTED, "mthip_conv2d: operands above 2 GiB are not supported");
   void* xp = nullptr;
   if (int rc = mthip_malloc(device, (size_t)(B * HW * Cp) * sizeof(T), &xp)) return rc;
-  dim3 grid((unsigned)ceil_div(HW, 32), (unsigned)ceil_div(Cp, 32), (unsigned)B);
-  hipLaunchKernelGGL(nchw_to_nhwc_pad_kernel<T>, grid, dim3(256), 0, s, (const T*)x, (T*)xp, C, Cp, HW);
-  int rc = check_launch("nchw_to_nhwc_pad_kernel");
+  int rc;
+  if (sizeof(T) == 2 && HW % 8 == 0 && Cp % 8 == 0 && ((uintptr_t)x & 15) == 0 && B <= 65535) {
+    dim3 grid((unsigned)ceil_div(HW, 64), (unsigned)ceil_div(Cp, 64), (unsigned)B);
+    hipLaunchKernelGGL(nchw_to_nhwc_pad_vec_kernel, grid, dim3(256), 0, s, (const uint16_t*)x, (uint16_t*)xp, C, Cp,
+                       HW);
+    rc = check_launch("nchw_to_nhwc_pad_vec_kernel");
+  } else {
+    dim3 grid((unsigned)ceil_div(HW, 32), (unsigned)ceil_div(Cp, 32), (unsigned)B);
+    hipLaunchKernelGGL(nchw_to_nhwc_pad_kernel<T>, grid, dim3(256), 0, s, (const T*)x, (T*)xp, C, Cp, HW);
+    rc = check_launch("nchw_to_nhwc_pad_kernel");
+  }
   if (rc == MTHIP_OK)
     rc = run_conv_gemm_nhwc<T>(device, dtype, xp, wp, b, y, B, C, H, W, O, KH, KW, sh, sw, ph, pw, dh, dw, residual,
                                s);
