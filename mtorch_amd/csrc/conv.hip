@@ -367,7 +367,8 @@ int run_conv_gemm(int device, int dtype, const void* x, const void* wp, const vo
   void* xp = nullptr;
   if (int rc = mthip_malloc(device, (size_t)(B * HW * Cp) * sizeof(T), &xp)) return rc;
   int rc;
-  if (sizeof(T) == 2 && HW % 8 == 0 && Cp % 8 == 0 && ((uintptr_t)x & 15) == 0 && B <= 65535) {
+  if (sizeof(T) == 2 && HW % 8 == 0 && Cp % 8 == 0 && ((uintptr_t)x & 15) == 0 && B <= 65535 &&
+      ceil_div(HW, 64) < (int64_t(1) << 31) && ceil_div(Cp, 64) <= 65535) {
     dim3 grid((unsigned)ceil_div(HW, 64), (unsigned)ceil_div(Cp, 64), (unsigned)B);
     hipLaunchKernelGGL(nchw_to_nhwc_pad_vec_kernel, grid, dim3(256), 0, s, (const uint16_t*)x, (uint16_t*)xp, C, Cp,
                        HW);
@@ -471,7 +472,9 @@ extern "C" int mthip_upsample2x_to_nhwc(int device, int dtype, const void* x, vo
                                         int64_t Cp, int64_t H, int64_t W) {
   MTHIP_REQUIRE(dtype == MTHIP_F16 || dtype == MTHIP_F32, "mthip_upsample2x_to_nhwc: dtype must be F16 or F32");
   MTHIP_REQUIRE(B >= 0 && C > 0 && Cp >= C && H > 0 && W > 0 && B <= 65535, "mthip_upsample2x_to_nhwc: bad extents");
-  MTHIP_REQUIRE(B * 4 * H * W * Cp < (int64_t(1) << 40), "mthip_upsample2x_to_nhwc: output too large");
+  MTHIP_REQUIRE(B * 4 * H * W * Cp < (int64_t(1) << 40) && ceil_div(H * W, 32) < (int64_t(1) << 31) &&
+                    ceil_div(Cp, 32) <= 65535,
+                "mthip_upsample2x_to_nhwc: output too large");
   if (B == 0) return MTHIP_OK;
   hipStream_t s = stream_for(device);
   if (!s) return MTHIP_ERR_HIP;
