@@ -173,13 +173,16 @@ bool dtl_enabled() { return env_flag("MTHIP_GEMM_DTL", 1) != 0; }
 // Default shape per problem, from sweeps of the SD-1.5 GEMMs and convs (fp16, batch 2):
 // convs over more than 128 output pixels with a multiple of 128 output channels take 128x64
 // (5-18% over 64x64 at 640 and 1280 channels; at 320 channels the third 128-row tile is half
-// empty and 64x64 is 9% faster), the 8x8 convs (long K, split) 64x64 with 4 stages; linears take
+// empty and 64x64 is 9% faster), the 8x8 convs (long K, split) and every conv with K >= 2048
+// 64x64 with 4 stages (the SD stride-2 downsampling convs, graph-replayed with the layout pass:
+// 320 @64x64 27.4 -> 26.3 us, 640 @32x32 27.4 -> 24.6 us against 64x64 / 128x64 with 3 stages,
+// which date from before the 3x3 stride-1 convs moved to the halo kernel); linears take
 // 64x64 (3 stages) up to K = 1280, 4 stages beyond, 64x128 when M*N is large, 128x128 with 2
 // stages for the big square problems.
 int dtl_tile_for(int MODE, int64_t M, int64_t N, int64_t K) {
   const int forced = env_flag("MTHIP_GEMM_DTL_TILE", -1);
   if (forced >= 0) return forced;
-  if (MODE == MODE_CONV) return N <= 128 ? 1 : M % 128 == 0 ? 2 : 0;
+  if (MODE == MODE_CONV) return (N <= 128 || K >= 2048) ? 1 : M % 128 == 0 ? 2 : 0;
   if (M >= 4096 && N >= 4096 && K >= 2048) return 5;
   if (K >= 2048) return 1;
   if (M * N >= (int64_t)2048 * 1920 && K >= 640) return 3;
