@@ -131,6 +131,14 @@ int mthip_logical_not(int device, const void* x, void* y, int64_t n);
 int mthip_cat(int device, int dtype, int count, const void* const* inputs, const int64_t* dim_sizes,
               int rank, const int64_t* out_sizes, int dim, void* out);
 
+/* The SD timestep embedding [cos(t f), sin(t f)] of fp32 timesteps t[B] and frequencies
+ * f[half], narrowed to fp16 out[B][2*half]: the reference benchmark's embedding
+ * (tests/compat/benchmarking.py:6031-6032: a broadcast multiply, cos, sin and cat, tensor.cpp:32141)
+ * followed by .half() (tensor.cpp:8479-8508) in one launch, each value computed as those ops
+ * compute it on the device (fp32 product, sin/cos evaluated in double, the mtorch narrowing). */
+int mthip_timestep_embedding_f16(int device, const void* t, const void* freqs, void* out, int64_t B,
+                                 int64_t half);
+
 /* Nearest-neighbour 2-D upsampling of x[B*C, H, W] by integer factors.  Serves
  * interpolate(mode="nearest") (tensor.cpp:10897) on the UNet decoder path. */
 int mthip_upsample_nearest2d(int device, int dtype, const void* x, void* y, int64_t planes,

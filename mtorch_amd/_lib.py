@@ -53,6 +53,7 @@ _SIGNATURES = {
     "mthip_logical_not": (_int, [_int, _c_void_p, _c_void_p, _i64]),
     "mthip_cat": (_int, [_int, _int, _int, ctypes.POINTER(_c_void_p), _i64p, _int, _i64p, _int, _c_void_p]),
     "mthip_upsample_nearest2d": (_int, [_int, _int, _c_void_p, _c_void_p, _i64, _i64, _i64, _i64, _i64]),
+    "mthip_timestep_embedding_f16": (_int, [_int, _c_void_p, _c_void_p, _c_void_p, _i64, _i64]),
     "mthip_binary": (_int, [_int, _int, _int, _c_void_p, _i64p, _c_void_p, _i64p, _c_void_p, _int, _i64p]),
     "mthip_binary_scalar": (_int, [_int, _int, _int, _c_void_p, _dbl, _int, _c_void_p, _i64]),
     "mthip_unary": (_int, [_int, _int, _int, _c_void_p, _c_void_p, _i64]),

@@ -571,12 +571,39 @@ int elem_size(int dtype) {
   }
 }
 
+// The SD timestep embedding narrowed to fp16: out[b][j] = half(cos(t[b] f[j])) for j < half and
+// half(sin(t[b] f[j - half])) after it -- the broadcast product, cos, sin, cat and cast each
+// computed as their own kernels compute them (fp32 product, the double-precision sin/cos of
+// apply_unary<float>, f2h_fast), in one launch.
+__global__ void timestep_embedding_f16_kernel(const float* __restrict__ t, const float* __restrict__ f,
+                                              uint16_t* __restrict__ out, int64_t B, int64_t half) {
+  const int64_t n = B * 2 * half;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+    const int64_t b = i / (2 * half), j = i - b * 2 * half;
+    const bool second = j >= half;
+    const float x = t[b] * f[second ? j - half : j];
+    out[i] = f2h_fast(apply_unary<float>(second ? MTHIP_UNARY_SIN : MTHIP_UNARY_COS, x));
+  }
+}
+
 }  // namespace
 }  // namespace mthip
 
 using namespace mthip;
 
 extern "C" {
+
+int mthip_timestep_embedding_f16(int device, const void* t, const void* freqs, void* out, int64_t B, int64_t half) {
+  MTHIP_REQUIRE(B >= 0 && half > 0 && B * 2 * half < (int64_t(1) << 40), "mthip_timestep_embedding_f16: bad extents");
+  if (B == 0) return MTHIP_OK;
+  hipStream_t s = stream_for(device);
+  if (!s) return MTHIP_ERR_HIP;
+  if (int rc = use_device(device)) return rc;
+  hipLaunchKernelGGL(timestep_embedding_f16_kernel, dim3(grid_for(B * 2 * half)), dim3(kThreads), 0, s,
+                     (const float*)t, (const float*)freqs, (uint16_t*)out, B, half);
+  return check_launch("timestep_embedding_f16_kernel");
+}
 
 int mthip_cast(int device, int src_dtype, const void* src, int dst_dtype, void* dst, int64_t n) {
   MTHIP_REQUIRE(elem_size(src_dtype) && elem_size(dst_dtype), "mthip_cast: unknown dtype");

@@ -273,6 +273,20 @@ def timestep_embedding(t: Tensor, freqs: Tensor) -> Tensor:
     return mt.cat([args.cos(), args.sin()], dim=-1)
 
 
+def timestep_embedding_f16(t: Tensor, freqs: Tensor) -> Tensor:
+    """timestep_embedding(t, freqs).half() in one launch (mthip_timestep_embedding_f16, the same
+    values bit for bit) for fp32 timesteps and frequencies on the device; otherwise the op
+    sequence."""
+    if t.dtype is T.float32 and freqs.dtype is T.float32 and t.dim() == 1 and freqs.dim() == 1 and t.is_cuda:
+        dev = _ops._gpu("timestep_embedding", t, freqs)
+        B, half = t.shape[0], freqs.shape[0]
+        out = _ops._empty([B, 2 * half], T.float16, dev)
+        _lib.check(_lib.lib().mthip_timestep_embedding_f16(dev, t.contiguous().data_ptr(), freqs.contiguous().data_ptr(),
+                                                           out.data_ptr(), B, half))
+        return out
+    return timestep_embedding(t, freqs).half()
+
+
 class UNet(nn.Module):
     """Stable-Diffusion-1.5-shaped conditional UNet, fp16, random N(0, 0.02) weights."""
 
@@ -344,7 +358,7 @@ class UNet(nn.Module):
     def forward(self, latent: Tensor, timesteps: Tensor, context: Tensor) -> Tensor:
         import mtorch_amd as mt
 
-        emb = timestep_embedding(timesteps, self.freqs).half()
+        emb = timestep_embedding_f16(timesteps, self.freqs)
         emb = F.linear_silu(emb, self.time1.weight, self.time1.bias)
         emb = F.linear(emb, self.time2.weight, self.time2.bias)
         temb_silu = F.silu(emb)  # every ResBlock's time projection reads silu(emb)

@@ -61,6 +61,22 @@ def test_resblock_with_channel_change():
     assert rel(got, want) <= 1e-2
 
 
+@pytest.mark.parametrize("ts", [[500.0, 500.0], [0.0, 1.0, 999.0], [981.5, 3.25, 0.5, 640.0]])
+def test_timestep_embedding_one_launch_equals_op_sequence(ts):
+    """The fused fp16 timestep embedding (one launch) gives cat([cos(t f), sin(t f)]).half() of the
+    broadcast-multiply / cos / sin / cat / cast kernels bit for bit, and the float64 values to
+    fp16 rounding."""
+    freqs = sd_unet.timestep_frequencies(320)
+    t = mt.tensor(ts).to("cuda")
+    got = sd_unet.timestep_embedding_f16(t, freqs).cpu().half_bits()
+    want = sd_unet.timestep_embedding(t, freqs).half().cpu().half_bits()
+    assert got.shape == (len(ts), 320)
+    assert np.array_equal(got, want)
+    args = np.asarray(ts, np.float32)[:, None] * freqs.cpu().numpy()[None, :]
+    exact = np.concatenate([np.cos(args.astype(np.float64)), np.sin(args.astype(np.float64))], axis=1)
+    assert np.max(np.abs(got.view(np.float16).astype(np.float64) - exact)) <= 2.0 ** -11
+
+
 @pytest.fixture(scope="module")
 def unet_case():
     model = sd_unet.UNet(seed=0, device="cuda")
