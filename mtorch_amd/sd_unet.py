@@ -360,8 +360,9 @@ class UNet(nn.Module):
 
         emb = timestep_embedding_f16(timesteps, self.freqs)
         emb = F.linear_silu(emb, self.time1.weight, self.time1.bias)
-        emb = F.linear(emb, self.time2.weight, self.time2.bias)
-        temb_silu = F.silu(emb)  # every ResBlock's time projection reads silu(emb)
+        # every ResBlock's time projection reads silu(emb), and nothing reads emb itself: the
+        # SiLU rides in the second linear's epilogue
+        temb_silu = F.linear_silu(emb, self.time2.weight, self.time2.bias)
         # all ResBlock time projections as one GEMM, all cross-attention K/V projections as another
         res_blocks = [b for b in self._blocks() if isinstance(b, ResBlock)]
         tw, tb, toff = self._stacked("time", [b.time_emb_proj for b in res_blocks])
