@@ -439,7 +439,7 @@ int mthip_linear(int device, int dtype, const void* x, int64_t lda, const void* 
   if (a.a_bytes > kMaxBufferBytes || a.b_bytes > kMaxBufferBytes)
     rc = fail(MTHIP_ERR_UNSUPPORTED, "mthip_linear: operands above 2 GiB are not supported");
   else if (dtype == MTHIP_F16) {
-    rc = act == MTHIP_ACT_NONE ? try_stream_linear(device, a, s) : -1;
+    rc = (act == MTHIP_ACT_NONE || act == MTHIP_ACT_GELU) ? try_stream_linear(device, a, s) : -1;
     if (rc < 0) rc = launch_gemm<uint16_t, MODE_NT, EPI_LINEAR>(device, a, 1, s);
   } else {
     rc = launch_gemm<float, MODE_NT, EPI_LINEAR>(device, a, 1, s);

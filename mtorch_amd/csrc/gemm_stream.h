@@ -59,10 +59,14 @@ struct StreamArgs {
   int m_fast;  // 1: consecutive units walk the token tiles of one channel tile
   int hw;          // NCHW: pixels per image
   FastDiv div_hw;  // NCHW: division by hw
+  const uint16_t* gelu_tab;  // GELU: the fp16 gelu of every half value
 };
 
-template <int BT, bool HAS_R, bool NCHW = false>
+// GELU (row-major, no residual): the output is the fp16 gelu of each narrowed value, looked up
+// in gelu_tab as the fp16 gelu op (and the tile GEMM's fused epilogue) computes it.
+template <int BT, bool HAS_R, bool NCHW = false, bool GELU = false>
 __global__ __launch_bounds__((BT / 16 + BT / 64) * 64) void gemm_stream_kernel(const StreamArgs args) {
+  static_assert(!(GELU && (HAS_R || NCHW)), "the GELU epilogue is row-major without a residual");
   constexpr int BC = 80, NW = BT / 16, NP = BT / 64, SW = 5;
   constexpr int WT = BT / NW;              // tokens per compute wave
   constexpr int FC = BC / 16, FP = WT / 16;
@@ -339,6 +343,12 @@ __global__ __launch_bounds__((BT / 16 + BT / 64) * 64) void gemm_stream_kernel(c
           x[3] = add_halves<true, true>(p23, rz[fc][fp].y);
         }
         out[fc][fp] = make_uint2(narrow_pair(x[0], x[1]), narrow_pair(x[2], x[3]));
+        if constexpr (GELU) {
+          auto g = [&](uint32_t p) {
+            return (uint32_t)args.gelu_tab[p & 0xffffu] | ((uint32_t)args.gelu_tab[p >> 16] << 16);
+          };
+          out[fc][fp] = make_uint2(g(out[fc][fp].x), g(out[fc][fp].y));
+        }
       }
     auto chain = [&](auto& narrow) {
 #pragma unroll
@@ -354,6 +364,7 @@ __global__ __launch_bounds__((BT / 16 + BT / 64) * 64) void gemm_stream_kernel(c
               x = h2f_bits((uint16_t)narrow(x)) + h2f_bits((uint16_t)((t & 1) ? rw >> 16 : rw & 0xffffu));
             }
             h[t] = narrow(x);
+            if constexpr (GELU) h[t] = args.gelu_tab[h[t]];
           }
           out[fc][fp] = make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
         }

@@ -67,7 +67,7 @@ void stream_plan(int64_t M, int64_t N, int64_t K, int64_t cus, int& best_bt, int
 // Launches the streamed kernel over sa (operands, bias, residual, layout already set) with the
 // planned tile and split, then the slice reduction (r: the reduction's GemmArgs, EPI_LINEAR
 // row-major or EPI_CONV NCHW).
-template <bool NCHW>
+template <bool NCHW, bool GELU = false>
 int launch_stream(int device, StreamArgs sa, GemmArgs r, int64_t K, hipStream_t s) {
   const int64_t M = sa.M, N = sa.N, cus = cu_count(device);
   int bt;
@@ -93,7 +93,12 @@ int launch_stream(int device, StreamArgs sa, GemmArgs r, int64_t K, hipStream_t 
   int64_t g = std::min<int64_t>(sa.units, cus);
   if (g > 8) g = g / 8 * 8;
   const bool hr = sa.residual != nullptr && ks == 1;
-  if (bt == 128) {
+  if constexpr (GELU) {
+    if (bt == 128)
+      hipLaunchKernelGGL((gemm_stream_kernel<128, false, false, true>), dim3((unsigned)g), dim3(640), 0, s, sa);
+    else
+      hipLaunchKernelGGL((gemm_stream_kernel<64, false, false, true>), dim3((unsigned)g), dim3(320), 0, s, sa);
+  } else if (bt == 128) {
     if (hr)
       hipLaunchKernelGGL((gemm_stream_kernel<128, true, NCHW>), dim3((unsigned)g), dim3(640), 0, s, sa);
     else
@@ -110,6 +115,8 @@ int launch_stream(int device, StreamArgs sa, GemmArgs r, int64_t K, hipStream_t 
     const unsigned rg = (unsigned)std::min<int64_t>(ceil_div(work, 256), 8192);
     if constexpr (NCHW)
       hipLaunchKernelGGL((gemm_splitk_reduce_kernel<uint16_t, EPI_CONV, MTHIP_ACT_NONE>), dim3(rg), dim3(256), 0, s, r);
+    else if constexpr (GELU)
+      hipLaunchKernelGGL((gemm_splitk_reduce_kernel<uint16_t, EPI_LINEAR, MTHIP_ACT_GELU>), dim3(rg), dim3(256), 0, s, r);
     else
       hipLaunchKernelGGL((gemm_splitk_reduce_kernel<uint16_t, EPI_LINEAR, MTHIP_ACT_NONE>), dim3(rg), dim3(256), 0, s, r);
     rc = check_launch("gemm_splitk_reduce_kernel(stream)");
@@ -161,12 +168,15 @@ int try_stream_conv1x1(int device, const void* x_nhwc, const void* wp, const voi
   return launch_stream<true>(device, sa, r, Cp, s);
 }
 
-// fp16 linears without an activation whose K is a multiple of 320 (units of whole 5-step ring
+// fp16 linears without an activation, or with GELU and no residual (the gelu of each narrowed
+// value looked up in a.gelu_tab), whose K is a multiple of 320 (units of whole 5-step ring
 // cycles) can take the streamed kernel (gemm_stream.h); MTHIP_GEMM_STREAM=0 turns it off.
 // Returns -1 when it does not apply.
 int try_stream_linear(int device, const GemmArgs& a, hipStream_t s) {
   const int mode = env_flag("MTHIP_GEMM_STREAM", 1);
   if (!mode) return -1;
+  const bool gelu = a.act == MTHIP_ACT_GELU;
+  if (a.act != MTHIP_ACT_NONE && !(gelu && a.residual == nullptr && a.gelu_tab != nullptr)) return -1;
   const int64_t M = a.M, N = a.N, K = a.K;
   // Where it wins (SD projections, graph-replayed): up to 1280 output channels with K >= 640 --
   // 512x1280x1280 13.5 -> 9.7 us, 2048x640x2560 19.7 -> 15.4, 512x1280x5120 22.3 -> 20.0,
@@ -196,6 +206,10 @@ int try_stream_linear(int device, const GemmArgs& a, hipStream_t s) {
   sa.ld_res = (int)a.ld_res;
   sa.a_bytes = (int)a.a_bytes;
   sa.b_bytes = (int)a.b_bytes;
+  if (gelu) {
+    sa.gelu_tab = a.gelu_tab;
+    return launch_stream<false, true>(device, sa, a, K, s);
+  }
   return launch_stream<false>(device, sa, a, K, s);
 }
 

@@ -331,6 +331,28 @@ def test_linear_streamed_kernel(M, N, K, res, bt, monkeypatch):
     assert rel(val(got[rows]), val(ref)) <= TOL["float16"]
 
 
+@pytest.mark.parametrize("M,N,K", [(8192, 1280, 320), (512, 1280, 1280), (2048, 640, 2560), (77, 96, 640)])
+@pytest.mark.parametrize("bt", ["64", "128"])
+def test_linear_gelu_streamed_kernel(M, N, K, bt, monkeypatch):
+    """fp16 linear+GELU on the streamed kernel (the gelu of each narrowed value looked up in the
+    fp16 table in its epilogue, or in the K-split reduction's): bit for bit gelu(linear(...)) of
+    the same kernel -- every value through the table, so every gate input is covered where the
+    outputs span them -- and the oracle's values on a strided subset of rows; 64- and 128-token
+    units, the planner's K splits, partial channel and token tiles."""
+    monkeypatch.setenv("MTHIP_GEMM_STREAM", "2")
+    monkeypatch.setenv("MTHIP_GEMM_STREAM_BT", bt)
+    g = Gen(M * 3 + N + K)
+    x = g.randn((M, K), "float16")
+    w = g.randn((N, K), "float16", 2.0 / np.sqrt(K))
+    b = g.randn((N,), "float16")
+    fused = host(F.linear_gelu(dev(x), dev(w), dev(b)))
+    unfused = host(F.gelu(F.linear(dev(x), dev(w), dev(b))))
+    assert np.array_equal(fused, unfused)
+    rows = np.unique(np.r_[np.arange(0, M, max(1, M // 40)), M - 1])
+    ref = orc.gelu(orc.linear(np.ascontiguousarray(x[rows]), w, b))
+    assert rel(val(fused[rows]), val(ref)) <= TOL["float16"]
+
+
 @pytest.mark.parametrize("M,N,res", [(8192, 320, True), (8192, 960, False), (1000, 240, True), (77, 96, False)])
 def test_linear_streamed_token_tiles_agree_bit_for_bit(M, N, res, monkeypatch):
     """With one K slice (K = 320) every output's fp32 sum runs over the same k order whether its
